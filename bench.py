@@ -1,0 +1,234 @@
+"""Benchmark of the rl_triton return-estimation path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Workload (BASELINE.json configs[1] and configs[2], the configuration the metric is
+quoted on): one STEP is one compute_gae call on a GAE [4096, 128] batch (terminations
+Bernoulli(0.01), truncations Bernoulli(0.005), bootstrap values at truncations and at
+t = T-1) plus one compute_vtrace call on a V-trace [4096, 128] batch (log-ratios
+N(0, 0.5^2), last_value, terminations Bernoulli(0.01)), both fp32, through the public
+Python API.  Steps rotate over enough input sets (> 3 x 256 MB) that the Infinity Cache
+cannot hold them, so every call streams its inputs from HBM.
+
+Printed JSON (one line, stdout):
+  value          whole-job Gelem/s = 2 * 4096 * 128 elements / ms_per_step
+  roofline       the dominant kernel (V-trace): algorithmic bytes per launch
+                 (28 B/elem: 5 reads + 2 writes) / its average launch duration, timed with
+                 HIP events recorded on the launch stream around each launch, vs 8 TB/s
+  ops            per-op device time, Gelem/s, GB/s and %-of-peak for both kernels
+  cpu_baseline   the reference's sequential torch loops (restated in
+                 oracle/torch_loops.py) on the host CPU, 1 thread, bounded sample
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "rl-triton_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "GAE & V-trace Gelem/s + achieved HBM GB/s (% of peak) at 4096×128 fp32"
+PEAK_GBS = 8000.0
+E, T = 4096, 128
+GAE_BYTES_PER_ELEM = 24     # rewards, values, terminateds, truncateds, bootstrap_values in; advantages out
+VTRACE_BYTES_PER_ELEM = 28  # log_pi_target, log_pi_behavior, values, rewards, terminateds in; 2 out
+MALL_BYTES = 256 * 2 ** 20
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_sets(torch, dev, n_sets):
+    """Input sets: set 0 from a seeded CPU generator (checked against the oracle),
+    the rest drawn with the same distributions by a seeded device generator."""
+    sets = []
+    for i in range(n_sets):
+        if i == 0:
+            g, kw = torch.Generator().manual_seed(0), {}
+        else:
+            g, kw = torch.Generator(device=dev).manual_seed(1000 + i), {"device": dev}
+        rn = lambda *s: torch.randn(*s, generator=g, **kw)  # noqa: E731
+        ru = lambda *s: torch.rand(*s, generator=g, **kw)   # noqa: E731
+        term = (ru(E, T) < 0.01).float()
+        trunc = (ru(E, T) < 0.005).float() * (1.0 - term)
+        boot = torch.where(trunc.bool(), rn(E, T), torch.zeros_like(term))
+        boot[:, -1] = rn(E)
+        gae = dict(rewards=rn(E, T), values=rn(E, T), terminateds=term, truncateds=trunc,
+                   bootstrap_values=boot)
+        vt = dict(log_pi_target=0.5 * rn(E, T), log_pi_behavior=torch.zeros_like(term),
+                  values=rn(E, T), rewards=rn(E, T), terminateds=(ru(E, T) < 0.01).float(),
+                  last_value=rn(E))
+        to = lambda d: {k: v.to(dev).contiguous() for k, v in d.items()}  # noqa: E731
+        sets.append((to(gae), to(vt), (gae, vt) if i == 0 else None))
+    return sets
+
+
+def run_gae(rl, s):
+    return rl.compute_gae(s["rewards"], s["values"], s["terminateds"], s["truncateds"],
+                          gamma=0.99, lambda_=0.95, bootstrap_values=s["bootstrap_values"])
+
+
+def run_vtrace(rl, s):
+    return rl.compute_vtrace(s["log_pi_target"], s["log_pi_behavior"], s["values"], s["rewards"],
+                             s["terminateds"], gamma=0.99, rho_bar=1.0, c_bar=1.0,
+                             last_value=s["last_value"])
+
+
+def parity(np, cpu_sets, outs):
+    from oracle import oracle as orc
+    gae, vt = cpu_sets
+    n = lambda t: t.numpy()  # noqa: E731
+    e_adv = orc.gae(n(gae["rewards"]), n(gae["values"]), n(gae["terminateds"]), n(gae["truncateds"]),
+                    0.99, 0.95, bootstrap=n(gae["bootstrap_values"]))
+    e_tg, e_ad = orc.vtrace(n(vt["log_pi_target"]), n(vt["log_pi_behavior"]), n(vt["values"]),
+                            n(vt["rewards"]), n(vt["terminateds"]), None, 0.99, 1.0, 1.0,
+                            bootstrap=n(vt["last_value"]))
+    errs = {"gae_advantages": float(np.max(np.abs(outs[0].cpu().numpy() - e_adv))),
+            "vtrace_targets": float(np.max(np.abs(outs[1][0].cpu().numpy() - e_tg))),
+            "vtrace_advantages": float(np.max(np.abs(outs[1][1].cpu().numpy() - e_ad)))}
+    return errs
+
+
+def time_ops(torch, rl, sets, iters):
+    """Average device duration of each op: HIP events recorded on the launch stream
+    immediately before and after each call."""
+    stream = torch.cuda.current_stream()
+    res = {}
+    for name, fn, idx in (("gae", run_gae, 0), ("vtrace", run_vtrace, 1)):
+        pairs = []
+        for i in range(iters):
+            s = sets[i % len(sets)][idx]
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fn(rl, s)
+            b.record(stream)
+            pairs.append((a, b))
+        torch.cuda.synchronize()
+        ms = [a.elapsed_time(b) for a, b in pairs]
+        res[name] = sum(ms) / len(ms)
+    return res
+
+
+def cpu_baseline(torch, cpu_sets, budget_s):
+    from oracle import torch_loops
+    gae, vt = cpu_sets
+    prev = torch.get_num_threads()
+    torch.set_num_threads(1)
+    try:
+        n, t0 = 0, time.perf_counter()
+        while True:
+            torch_loops.gae_loop(gae["rewards"], gae["values"], gae["terminateds"], gae["truncateds"],
+                                 0.99, 0.95, bootstrap_values=gae["bootstrap_values"])
+            torch_loops.vtrace_loop(vt["log_pi_target"], vt["log_pi_behavior"], vt["values"],
+                                    vt["rewards"], vt["terminateds"], 0.99, 1.0, 1.0,
+                                    last_value=vt["last_value"])
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+    finally:
+        torch.set_num_threads(prev)
+    return {"value": 2 * E * T * n / el / 1e9, "unit": "Gelem/s", "cores": 1, "kind": "port",
+            "sample": f"{n} full steps (GAE C2 + V-trace C3 at [{E},{T}]) in {el:.1f} s, "
+                      f"torch CPU loops of oracle/torch_loops.py, 1 thread, "
+                      f"host {platform.processor() or platform.machine()} ({os.cpu_count()} cpus)",
+            "ms_per_step": 1e3 * el / n}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    a = ap.parse_args(argv)
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(rows are independent; sharding is described in DESIGN.md). Run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    import rl_triton
+
+    dev = torch.device("cuda:0")
+    set_bytes = E * T * 4 * 10
+    n_sets = max(8, int(3 * MALL_BYTES / set_bytes) + 1)
+    log(f"[bench] {n_sets} input sets ({n_sets * set_bytes / 2**20:.0f} MiB) on {torch.cuda.get_device_name(0)}")
+    sets = make_sets(torch, dev, n_sets)
+    torch.cuda.synchronize()
+
+    outs = (run_gae(rl_triton, sets[0][0]), run_vtrace(rl_triton, sets[0][1]))
+    torch.cuda.synchronize()
+    errs = parity(np, sets[0][2], outs)
+    log(f"[bench] parity vs float64 oracle (max abs err): {errs}")
+    if max(errs.values()) > 1e-4:
+        raise SystemExit(f"parity check failed: {errs}")
+
+    for i in range(a.warmup):
+        s = sets[i % n_sets]
+        run_gae(rl_triton, s[0])
+        run_vtrace(rl_triton, s[1])
+    torch.cuda.synchronize()
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    t0 = time.perf_counter()
+    for i in range(a.steps):
+        s = sets[i % n_sets]
+        run_gae(rl_triton, s[0])
+        run_vtrace(rl_triton, s[1])
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = start.elapsed_time(end) / a.steps
+    value = 2 * E * T / (ms_step * 1e-3) / 1e9
+    log(f"[bench] timed {a.steps} steps: {ms_step * 1e3:.2f} us/step (wall {wall:.3f} s)")
+
+    op_ms = time_ops(torch, rl_triton, sets, max(200, min(a.steps, 2000)))
+    ops = {}
+    for name, bpe in (("gae", GAE_BYTES_PER_ELEM), ("vtrace", VTRACE_BYTES_PER_ELEM)):
+        ms = op_ms[name]
+        gbs = E * T * bpe / (ms * 1e-3) / 1e9
+        ops[name] = {"device_us": round(ms * 1e3, 3), "gelem_s": round(E * T / (ms * 1e-3) / 1e9, 2),
+                     "gb_s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 2),
+                     "bytes_per_elem": bpe, "bytes_per_launch": E * T * bpe}
+        log(f"[bench] {name}: {ms * 1e3:.2f} us/launch, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of 8 TB/s)")
+    dom = max(ops, key=lambda k: ops[k]["device_us"])
+    roofline = {"bound": "hbm", "kernel": dom, "achieved": ops[dom]["gb_s"], "peak": PEAK_GBS,
+                "unit": "GB/s", "frac": round(ops[dom]["gb_s"] / PEAK_GBS, 4), "traffic": None}
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        log(f"[bench] CPU baseline ({a.cpu_seconds:.0f} s sample) ...")
+        cpu = cpu_baseline(torch, sets[0][2], a.cpu_seconds)
+        log(f"[bench] CPU baseline: {cpu['value']:.4f} Gelem/s ({cpu['ms_per_step']:.1f} ms/step)")
+
+    line = {
+        "metric": METRIC, "value": round(value, 3), "unit": "Gelem/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded; BASELINE.json configs[1] GAE and configs[2] V-trace distributions)",
+        "config": {"workload": "GAE [4096,128] term+trunc+bootstrap_values + V-trace [4096,128] "
+                               "last_value, one public-API call each per step, inputs rotated over "
+                               f"{n_sets} HBM-resident sets",
+                   "num_envs": E, "seq_len": T, "gamma": 0.99, "lambda": 0.95,
+                   "rho_bar": 1.0, "c_bar": 1.0, "timing": "eager API calls, HIP events"},
+        "roofline": roofline, "ops": ops, "parity_max_abs_err": errs, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,142 @@
+/*
+ * rl_triton_amd.h -- C ABI of the MI355X (gfx950) return-estimation kernels.
+ *
+ * The reference (simonsays1980/rl-triton v0.1.3) has no C ABI: its boundary is the
+ * Python functions in src/rl_triton/ops/, each of which validates its tensors and
+ * launches one Triton kernel on torch's current stream.  Each entry point below is
+ * the device-side half of one of those functions; the rl_triton Python package in
+ * this repository calls them with tensor data pointers (ctypes), after raising the
+ * reference's AssertionErrors itself.
+ *
+ * Conventions shared by every entry point
+ *   - Tensors are contiguous row-major float32 [num_envs, seq_len] device arrays
+ *     (Retrace: [num_envs, seq_len, num_actions] for the per-action inputs, int64
+ *     actions).  Outputs are written, never read; inputs are never written.
+ *   - All work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the
+ *     default stream).  Nothing allocates and nothing synchronises.
+ *   - Bootstrap mode: RLK_BOOT_NONE (bootstrap == NULL, value 0), RLK_BOOT_ROW
+ *     (bootstrap is [num_envs]: the continuation value after step seq_len-1, the
+ *     reference's `last_value`), RLK_BOOT_FULL (bootstrap is [num_envs, seq_len], the
+ *     reference's `bootstrap_values`).
+ *   - Workspace: rows longer than one workgroup tile are split into tiles chained by a
+ *     decoupled look-back.  Those calls need `workspace` of at least
+ *     rlk_workspace_bytes(num_envs, seq_len) bytes, ZERO-FILLED BEFORE ITS FIRST USE.
+ *     Each call leaves the workspace ready for the next one, so zero it once and reuse
+ *     it; calls that share a workspace must be ordered on one stream (concurrent use
+ *     races).  Calls that need no workspace ignore the argument (NULL is fine).
+ *     Layout (uint64 words): [0] ticket, [1] finished workgroups, [2] call epoch,
+ *     [3] error flag -- nonzero if a look-back wait gave up (results of that call
+ *     are invalid), [4..7] reserved, then two status words per tile.
+ *   - Return value: RLK_OK or a negative RLK_ERR_* code; rlk_status_string() names it.
+ *     Empty inputs (num_envs == 0 or seq_len == 0) return RLK_OK without a launch.
+ */
+#ifndef RL_TRITON_AMD_H
+#define RL_TRITON_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RLK_OK 0
+#define RLK_ERR_INVALID_ARGUMENT (-1)
+#define RLK_ERR_WORKSPACE (-2)
+#define RLK_ERR_LAUNCH (-3)
+
+#define RLK_BOOT_NONE 0
+#define RLK_BOOT_ROW 1
+#define RLK_BOOT_FULL 2
+
+#define RLK_BACKWARD 0
+#define RLK_FORWARD 1
+
+/* Library version, major*10000 + minor*100 + patch. */
+int rlk_version(void);
+
+/* Static text for a status code. */
+const char *rlk_status_string(int status);
+
+/* Workspace bytes a call on [num_envs, seq_len] needs (0 when none is needed). */
+size_t rlk_workspace_bytes(int64_t num_envs, int64_t seq_len);
+
+/* GAE advantages.  Replaces the gae_fused_kernel launch in compute_gae
+ * (src/rl_triton/ops/gae.py:164-190; kernel src/rl_triton/kernels/gae.py:200-318), and
+ * its chunked fallback for seq_len > 131072 (ops/gae.py:192-215).
+ * truncateds may be NULL (done = terminateds). */
+int rlk_gae(const float *rewards, const float *values, const float *terminateds,
+            const float *truncateds, const float *bootstrap, int boot_mode, float *advantages,
+            int64_t num_envs, int64_t seq_len, float gamma, float lambda_, void *workspace,
+            size_t workspace_bytes, void *stream);
+
+/* V-trace targets and advantages.  Replaces vtrace_fused_kernel in compute_vtrace_fused
+ * (src/rl_triton/ops/vtrace_fused.py:161-219; kernel kernels/vtrace_fused.py:7-196) and
+ * the torch + chunked-scan path of compute_vtrace (ops/vtrace.py:161-201).
+ * truncateds may be NULL. */
+int rlk_vtrace(const float *log_pi_target, const float *log_pi_behavior, const float *values,
+               const float *rewards, const float *terminateds, const float *truncateds,
+               const float *bootstrap, int boot_mode, float *targets, float *advantages,
+               int64_t num_envs, int64_t seq_len, float gamma, float rho_bar, float c_bar,
+               void *workspace, size_t workspace_bytes, void *stream);
+
+/* Retrace(lambda) targets and advantages.  Replaces retrace_fused_kernel in
+ * compute_retrace_fused (src/rl_triton/ops/retrace_fused.py:93-118; kernel
+ * kernels/retrace_fused.py:7-201) and the torch + _run_scan path of compute_retrace
+ * (ops/retrace.py:173-196).  action_probs_target / next_q_values_all are
+ * [num_envs, seq_len, num_actions]; actions is int64 [num_envs, seq_len];
+ * truncateds may be NULL. */
+int rlk_retrace(const float *action_probs_target, const float *action_probs_behavior,
+                const float *q_values, const float *next_q_values_all, const int64_t *actions,
+                const float *rewards, const float *terminateds, const float *truncateds,
+                float *targets, float *advantages, int64_t num_envs, int64_t seq_len,
+                int64_t num_actions, float gamma, float lambda_, float c_bar, float rho_bar,
+                void *workspace, size_t workspace_bytes, void *stream);
+
+/* TD(lambda) returns.  Replaces lambda_returns_fused_kernel in compute_lambda_returns
+ * (src/rl_triton/ops/returns.py:113-140; kernel kernels/lambda_returns_fused.py:7-89) and
+ * its chunked fallback (ops/returns.py:142-152).  truncateds may be NULL. */
+int rlk_lambda_returns(const float *rewards, const float *next_values, const float *terminateds,
+                       const float *truncateds, const float *bootstrap, int boot_mode,
+                       float *returns, int64_t num_envs, int64_t seq_len, float gamma,
+                       float lambda_, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Discounted returns.  Replaces discounted_returns_fused_kernel in
+ * compute_discounted_returns (src/rl_triton/ops/returns.py:225-252; kernel
+ * kernels/discounted_returns_fused.py:7-82) and its chunked fallback
+ * (ops/returns.py:254-263).  truncateds may be NULL. */
+int rlk_discounted_returns(const float *rewards, const float *terminateds,
+                           const float *truncateds, const float *bootstrap, int boot_mode,
+                           float *returns, int64_t num_envs, int64_t seq_len, float gamma,
+                           void *workspace, size_t workspace_bytes, void *stream);
+
+/* Eligibility traces (forward).  Replaces eligibility_traces_fused_kernel in
+ * compute_eligibility_traces (src/rl_triton/ops/returns.py:337-346; kernel
+ * kernels/eligibility_traces_fused.py:7-84).  Unlike the reference, seq_len is not
+ * limited to 131072 (ops/returns.py:319-322).  seed_values may be NULL. */
+int rlk_eligibility_traces(const float *gradients, const float *dones, const float *seed_values,
+                           float *traces, int64_t num_envs, int64_t seq_len, float gamma,
+                           float lambda_, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Episodic prefix sum (forward).  Replaces prefix_sum_fused_kernel in
+ * compute_episodic_prefix_sum (src/rl_triton/ops/prefix_sum.py:101-110; kernel
+ * kernels/prefix_sum_fused.py:7-84).  ends_at = 1: boundary="ends_at", 0: "starts_at".
+ * Not limited to seq_len <= 131072 (ops/prefix_sum.py:83-86).  seed_values may be NULL. */
+int rlk_prefix_sum(const float *inputs, const float *dones, const float *seed_values,
+                   float *prefix_sums, int64_t num_envs, int64_t seq_len, int ends_at,
+                   void *workspace, size_t workspace_bytes, void *stream);
+
+/* Generic affine scan.  direction RLK_BACKWARD: out[t] = u[t] + v[t]*out[t+1],
+ * out[T] = carry; RLK_FORWARD: out[t] = u[t] + v[t]*out[t-1], out[-1] = carry.
+ * carry ([num_envs]) may be NULL (0).  Replaces _run_scan / _run_scan_forward
+ * (src/rl_triton/ops/_scan.py:69-213; kernels kernels/scan.py:39-138,
+ * kernels/scan_chunked.py:7-85). */
+int rlk_affine_scan(const float *u, const float *v, const float *carry, float *out,
+                    int64_t num_envs, int64_t seq_len, int direction, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RL_TRITON_AMD_H */

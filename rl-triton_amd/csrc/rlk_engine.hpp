@@ -1,0 +1,419 @@
+// rlk_engine.hpp -- the scan engine shared by every rl_triton estimator on gfx950.
+//
+// Every estimator is one done-masked linear recurrence over a row of T steps,
+//     backward:  x[t] = add[t] + mul[t] * x[t+1],   x[T]  = carry   (GAE, V-trace, ...)
+//     forward:   x[t] = add[t] + mul[t] * x[t-1],   x[-1] = carry   (traces, prefix sum)
+// evaluated as a scan over affine maps m(x) = add + mul * x.  Composition:
+//     (m1 o m2)(x) = m1.add + m1.mul * m2.add  +  (m1.mul * m2.mul) * x.
+//
+// Work decomposition (rows are contiguous, row-major [E, T] fp32):
+//   * a thread owns S consecutive steps of one row ("segment") and keeps its
+//     inputs in registers; it folds them into one affine map serially;
+//   * L threads (L = 2^k) form a row tile of L*S steps; their maps are combined by a
+//     wavefront shuffle scan (width min(L, 64)) and, when L > 64, through LDS;
+//   * short rows: a workgroup of NT threads holds NT/L whole rows, no inter-workgroup
+//     traffic;
+//   * long rows: a row is split into tiles of NT*S steps, one per workgroup, chained by
+//     a decoupled look-back over per-tile status words in a caller-provided workspace.
+//     Tiles are handed out by an atomic ticket in scan order, so a workgroup only waits
+//     on tiles that an already-running workgroup owns.
+//
+// An estimator ("Op") supplies:
+//   Regs                      per-thread registers for S steps
+//   load(row, t0, T, R)       read the segment (padding steps beyond T are identity)
+//   Halo / export / halo_load the one-step neighbour data the producer needs (values[t+1]
+//                             for GAE, done[t-1] for forward traces), passed lane to lane
+//                             and read from global memory at wave/tile edges
+//   coef(...)                 per-step (add, mul) with truncation/bootstrap folded in
+//   row_carry(row)            x[T] (backward) or x[-1] (forward)
+//   emit(...)                 outputs from the scanned x (and x one step further)
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+namespace rlk {
+
+constexpr int kWave = 64;
+
+struct Affine {
+  float mul;
+  float add;
+};
+
+__device__ __forceinline__ Affine compose(Affine outer, Affine inner) {
+  // outer(inner(x))
+  return Affine{outer.mul * inner.mul, fmaf(outer.mul, inner.add, outer.add)};
+}
+
+struct NoHalo {};
+
+// ---------------------------------------------------------------------------------------
+// Segment loads / stores.  VEC: T % 4 == 0 and every base pointer 16-byte aligned, so a
+// segment start t0 (a multiple of 4) is 16-byte aligned and each quad is all-in or all-out.
+// ---------------------------------------------------------------------------------------
+template <int S, bool VEC>
+__device__ __forceinline__ void load_seg(const float* __restrict__ p, int t0, int T, float (&v)[S],
+                                         float fill) {
+  if constexpr (VEC) {
+    static_assert(S % 4 == 0, "vector segments hold whole quads");
+#pragma unroll
+    for (int q = 0; q < S / 4; ++q) {
+      const int t = t0 + 4 * q;
+      if (t < T) {
+        const float4 f = *reinterpret_cast<const float4*>(p + t);
+        v[4 * q + 0] = f.x;
+        v[4 * q + 1] = f.y;
+        v[4 * q + 2] = f.z;
+        v[4 * q + 3] = f.w;
+      } else {
+        v[4 * q + 0] = v[4 * q + 1] = v[4 * q + 2] = v[4 * q + 3] = fill;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < S; ++i) v[i] = (t0 + i < T) ? p[t0 + i] : fill;
+  }
+}
+
+template <int S, bool VEC>
+__device__ __forceinline__ void store_seg(float* __restrict__ p, int t0, int T, const float (&v)[S]) {
+  if constexpr (VEC) {
+#pragma unroll
+    for (int q = 0; q < S / 4; ++q) {
+      const int t = t0 + 4 * q;
+      if (t < T) {
+        *reinterpret_cast<float4*>(p + t) =
+            make_float4(v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+      if (t0 + i < T) p[t0 + i] = v[i];
+  }
+}
+
+// Bootstrap argument shared by the backward estimators: none, one value per row, or
+// one value per step (the reference's last_value / bootstrap_values pair).
+enum BootMode : int { kBootNone = 0, kBootRow = 1, kBootFull = 2 };
+
+__device__ __forceinline__ float boot_at(const float* __restrict__ boot, int mode, int64_t row, int t,
+                                         int T) {
+  if (mode == kBootFull) return boot[row * (int64_t)T + t];
+  if (mode == kBootRow) return (t == T - 1) ? boot[row] : 0.f;
+  return 0.f;
+}
+
+// bt[i] = boot(t0 + i).  per_step = false: the caller only uses boot(T-1) (no truncations),
+// so a per-step bootstrap array is read at its last column only.
+template <int S, bool VEC>
+__device__ __forceinline__ void load_boot(const float* __restrict__ boot, int mode, int64_t row,
+                                          int t0, int T, float (&bt)[S], bool per_step) {
+  if (mode == kBootFull && per_step) {
+    load_seg<S, VEC>(boot + row * (int64_t)T, t0, T, bt, 0.f);
+  } else {
+    const bool has_last = t0 <= T - 1 && T - 1 < t0 + S;
+    const float last = has_last ? boot_at(boot, mode, row, T - 1, T) : 0.f;
+#pragma unroll
+    for (int i = 0; i < S; ++i) bt[i] = (t0 + i == T - 1) ? last : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Lane shuffles of a halo value (float or a small struct of floats).
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ float shfl_next(float v) { return __shfl_down(v, 1, kWave); }
+__device__ __forceinline__ float shfl_prev(float v) { return __shfl_up(v, 1, kWave); }
+
+struct Halo2 {
+  float a, b;
+};
+__device__ __forceinline__ Halo2 shfl_next(Halo2 h) { return Halo2{shfl_next(h.a), shfl_next(h.b)}; }
+__device__ __forceinline__ Halo2 shfl_prev(Halo2 h) { return Halo2{shfl_prev(h.a), shfl_prev(h.b)}; }
+
+// Inclusive scan of affine maps across groups of W lanes (W a power of two <= 64).
+// Backward (FWD=false): lane i ends up with m_i o m_{i+1} o ... o m_{W-1} of its group.
+// Forward  (FWD=true):  lane i ends up with m_i o m_{i-1} o ... o m_0.
+template <bool FWD>
+__device__ __forceinline__ Affine group_scan(Affine m, int W) {
+  const int li = __lane_id() & (W - 1);
+  for (int d = 1; d < W; d <<= 1) {
+    float omul, oadd;
+    bool ok;
+    if constexpr (FWD) {
+      omul = __shfl_up(m.mul, d, W);
+      oadd = __shfl_up(m.add, d, W);
+      ok = li >= d;
+    } else {
+      omul = __shfl_down(m.mul, d, W);
+      oadd = __shfl_down(m.add, d, W);
+      ok = li + d < W;
+    }
+    if (ok) m = compose(m, Affine{omul, oadd});
+  }
+  return m;
+}
+
+// ---------------------------------------------------------------------------------------
+// Decoupled look-back status words.  Per tile two 64-bit words {tag:32 | value:32}:
+//   word0 = AGG: mul   or INC: x at the tile's outgoing edge
+//   word1 = AGG: add
+// tag = (epoch << 2) | kind, kind 1 = AGG, 2 = INC.  A word whose epoch differs from the
+// current call's is "not yet published", so the workspace needs clearing only once.
+// Header (uint64): [0] ticket counter, [1] finished-workgroup counter, [2] epoch,
+//                  [3] error flag (set when a bounded wait gives up), [4..7] reserved.
+// ---------------------------------------------------------------------------------------
+constexpr int kHeaderWords = 8;
+constexpr uint32_t kAgg = 1, kInc = 2;
+constexpr uint32_t kEpochMask = 0x3fffffffu;
+constexpr int kSpinLimit = 1 << 20;  // polls before a wait gives up (~1 s), never reached when correct
+
+__device__ __forceinline__ uint64_t atomic_ld(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void atomic_st(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t pack(uint32_t tag, float v) {
+  return ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v);
+}
+
+// ---------------------------------------------------------------------------------------
+// The kernel.
+//   NT        threads per workgroup (multiple of 64)
+//   S         steps per thread
+//   VEC       16-byte vector loads/stores (see load_seg)
+//   LOOKBACK  rows split into NT*S-step tiles chained by look-back (then L == NT)
+// Launch: !LOOKBACK: grid = ceil(E / (NT/L)); LOOKBACK: grid = E * tiles_per_row.
+// ---------------------------------------------------------------------------------------
+template <class Op, int NT, int S, bool VEC, bool LOOKBACK>
+__global__ __launch_bounds__(NT) void scan_kernel(const Op op, int64_t E, int T, int log2L,
+                                                  int tiles_per_row, uint64_t* __restrict__ ws) {
+  constexpr bool FWD = Op::kForward;
+  constexpr int NW = NT / kWave;
+  using Regs = typename Op::template Regs<S>;
+  using Halo = typename Op::Halo;
+
+  __shared__ float s_mul[NW], s_add[NW];
+  __shared__ float s_carry;
+  __shared__ uint64_t s_ticket;
+  __shared__ uint32_t s_epoch;
+
+  const int tid = threadIdx.x;
+  const int lane = __lane_id();
+  const int wave = tid / kWave;
+  const int L = 1 << log2L;
+  const int W = L < kWave ? L : kWave;  // width of the intra-wave scan
+  const int li = tid & (L - 1);         // lane within the row tile
+
+  int64_t row;
+  int k = 0;  // tile index within the row (LOOKBACK)
+  uint32_t epoch = 0;
+  if constexpr (LOOKBACK) {
+    if (tid == 0) {
+      s_ticket = __hip_atomic_fetch_add(ws + 0, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_epoch = (uint32_t)atomic_ld(ws + 2) & kEpochMask;
+    }
+    __syncthreads();
+    const int64_t ticket = (int64_t)s_ticket;
+    epoch = s_epoch;
+    if (ticket >= (int64_t)gridDim.x) {
+      // A workspace whose counters were not left at rest (e.g. not zero-filled before its
+      // first use): flag the call as failed and touch nothing else.  Uniform per workgroup.
+      if (tid == 0) {
+        atomic_st(ws + 3, (uint64_t)1);
+        const uint64_t fin =
+            __hip_atomic_fetch_add(ws + 1, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (fin == (uint64_t)gridDim.x - 1) {
+          atomic_st(ws + 0, 0);
+          atomic_st(ws + 1, 0);
+          atomic_st(ws + 2, (uint64_t)((epoch + 1) & kEpochMask));
+        }
+      }
+      return;
+    }
+    row = ticket / tiles_per_row;
+    const int j = (int)(ticket - row * tiles_per_row);
+    k = FWD ? j : tiles_per_row - 1 - j;
+  } else {
+    row = (int64_t)blockIdx.x * (NT >> log2L) + (tid >> log2L);
+  }
+  const bool active = row < E;
+  const int t0 = (k * L + li) * S;
+
+  // 1. load the segment
+  Regs R;
+  if (active) op.template load<S, VEC>(row, t0, T, R);
+  else op.template clear<S>(R);
+
+  // 2. neighbour step data
+  Halo h{};
+  if constexpr (!std::is_same<Halo, NoHalo>::value) {
+    if constexpr (FWD) {
+      h = shfl_prev(op.template export_last<S>(R));
+      if (lane == 0 && t0 > 0 && active) h = op.halo_load(row, t0 - 1, T);
+    } else {
+      h = shfl_next(op.template export_first<S>(R));
+      if (lane == kWave - 1 && t0 + S < T && active) h = op.halo_load(row, t0 + S, T);
+    }
+  }
+
+  // 3. per-step coefficients and the segment's map
+  float mul[S], add[S];
+  op.template coef<S>(R, h, row, t0, T, mul, add);
+  Affine m{1.f, 0.f};
+  if constexpr (FWD) {
+#pragma unroll
+    for (int i = 0; i < S; ++i) m = compose(Affine{mul[i], add[i]}, m);
+  } else {
+#pragma unroll
+    for (int i = S - 1; i >= 0; --i) m = compose(Affine{mul[i], add[i]}, m);
+  }
+
+  // 4. combine lanes of the wave
+  m = group_scan<FWD>(m, W);
+
+  // 5. carry into this wave's part of the row tile
+  float carry;
+  if (L > kWave || LOOKBACK) {
+    // wave aggregate: backward lane 0, forward lane 63
+    if (lane == (FWD ? kWave - 1 : 0)) {
+      s_mul[wave] = m.mul;
+      s_add[wave] = m.add;
+    }
+    __syncthreads();
+    float tile_carry;
+    if constexpr (LOOKBACK) {
+      if (wave == 0) {
+        // the whole tile's map
+        Affine tm{1.f, 0.f};
+        if constexpr (FWD) {
+          for (int v = 0; v < NW; ++v) tm = compose(Affine{s_mul[v], s_add[v]}, tm);
+        } else {
+          for (int v = NW - 1; v >= 0; --v) tm = compose(Affine{s_mul[v], s_add[v]}, tm);
+        }
+        const int64_t tile_base = row * tiles_per_row;
+        uint64_t* st = ws + kHeaderWords;
+        const bool first_in_scan = FWD ? (k == 0) : (k == tiles_per_row - 1);
+        const uint32_t tag_agg = (epoch << 2) | kAgg, tag_inc = (epoch << 2) | kInc;
+        float c;
+        if (first_in_scan) {
+          c = op.row_carry(row, T);
+          if (lane == 0) atomic_st(st + 2 * (tile_base + k), pack(tag_inc, fmaf(tm.mul, c, tm.add)));
+        } else {
+          if (lane == 0) {
+            if (tm.mul == 0.f) {
+              // the tile's outgoing value does not depend on its carry
+              atomic_st(st + 2 * (tile_base + k), pack(tag_inc, tm.add));
+            } else {
+              atomic_st(st + 2 * (tile_base + k) + 1, pack(tag_agg, tm.add));
+              atomic_st(st + 2 * (tile_base + k), pack(tag_agg, tm.mul));
+            }
+          }
+          // Look back over the 64 nearest predecessors (lane i <-> i+1 tiles away) until the
+          // nearest published inclusive value X has only aggregates between it and this
+          // tile, then apply those aggregates to X one at a time, nearest last.  Every
+          // published X therefore equals the sequential chain X_k = fma(A_k, X_{k+1}, B_k)
+          // however far the look-back reached, which keeps results bit-reproducible.
+          int spins = 0;
+          while (true) {
+            const int jj = FWD ? k - 1 - lane : k + 1 + lane;
+            const bool inr = FWD ? (jj >= 0) : (jj < tiles_per_row);
+            uint32_t kind = 0;
+            float v0 = 1.f, v1 = 0.f;
+            if (inr) {
+              const uint64_t w0 = atomic_ld(st + 2 * (tile_base + jj));
+              const uint32_t tag0 = (uint32_t)(w0 >> 32);
+              v0 = __uint_as_float((uint32_t)w0);
+              if ((tag0 >> 2) == epoch) kind = tag0 & 3u;
+              if (kind == kAgg) {
+                const uint64_t w1 = atomic_ld(st + 2 * (tile_base + jj) + 1);
+                if ((uint32_t)(w1 >> 32) == tag_agg) v1 = __uint_as_float((uint32_t)w1);
+                else kind = 0;
+              }
+            }
+            const uint64_t inc_mask = __ballot(kind == kInc);
+            const uint64_t bad_mask = __ballot(kind == 0);
+            const int first_inc = inc_mask ? __ffsll((long long)inc_mask) - 1 : kWave;
+            const int first_bad = bad_mask ? __ffsll((long long)bad_mask) - 1 : kWave;
+            if (first_inc < first_bad) {
+              float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v0), first_inc));
+              for (int l = first_inc - 1; l >= 0; --l) {
+                const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v0), l));
+                const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v1), l));
+                x = fmaf(a, x, b);
+              }
+              c = x;
+              break;
+            }
+            if (++spins > kSpinLimit) {
+              if (lane == 0) atomic_st(ws + 3, (uint64_t)1);
+              c = 0.f;
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+          }
+          if (lane == 0 && tm.mul != 0.f)
+            atomic_st(st + 2 * (tile_base + k), pack(tag_inc, fmaf(tm.mul, c, tm.add)));
+        }
+        if (lane == 0) s_carry = c;
+      }
+      __syncthreads();
+      tile_carry = s_carry;
+    } else {
+      tile_carry = active ? op.row_carry(row, T) : 0.f;
+    }
+    // compose the waves between the row tile's carry source and this wave
+    const int wpr = L / kWave;                 // waves per row tile (L >= 64 here)
+    const int first = (wave / wpr) * wpr, last = first + wpr - 1;
+    carry = tile_carry;
+    if constexpr (FWD) {
+      for (int v = first; v < wave; ++v) carry = fmaf(s_mul[v], carry, s_add[v]);
+    } else {
+      for (int v = last; v > wave; --v) carry = fmaf(s_mul[v], carry, s_add[v]);
+    }
+  } else {
+    carry = active ? op.row_carry(row, T) : 0.f;
+  }
+
+  // 6. this segment's incoming value: the neighbour lane's outgoing value
+  const float y = fmaf(m.mul, carry, m.add);
+  float x_in;
+  const int gl = lane & (W - 1);
+  if constexpr (FWD) {
+    x_in = __shfl_up(y, 1, kWave);
+    if (gl == 0) x_in = carry;
+  } else {
+    x_in = __shfl_down(y, 1, kWave);
+    if (gl == W - 1) x_in = carry;
+  }
+
+  // 7. replay the segment and write outputs
+  float xs[S];
+  float x = x_in;
+  if constexpr (FWD) {
+#pragma unroll
+    for (int i = 0; i < S; ++i) xs[i] = x = fmaf(mul[i], x, add[i]);
+  } else {
+#pragma unroll
+    for (int i = S - 1; i >= 0; --i) xs[i] = x = fmaf(mul[i], x, add[i]);
+  }
+  if (active) op.template emit<S, VEC>(R, h, xs, x_in, row, t0, T);
+
+  if constexpr (LOOKBACK) {
+    if (tid == 0) {
+      const uint64_t fin =
+          __hip_atomic_fetch_add(ws + 1, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (fin == (uint64_t)gridDim.x - 1) {
+        // last workgroup of this call: leave the workspace ready for the next call
+        atomic_st(ws + 0, 0);
+        atomic_st(ws + 1, 0);
+        atomic_st(ws + 2, (uint64_t)((epoch + 1) & kEpochMask));
+      }
+    }
+  }
+}
+
+}  // namespace rlk

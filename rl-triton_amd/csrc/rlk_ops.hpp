@@ -1,0 +1,492 @@
+// rlk_ops.hpp -- the rl_triton estimators as producers/epilogues of the scan engine.
+//
+// Each struct turns its inputs into per-step affine coefficients (truncation and
+// bootstrap handling folded in, so there is no extra pass) and turns the scanned
+// values into the estimator's outputs.  Semantics follow the reference's fused Triton
+// kernels (simonsays1980/rl-triton v0.1.3, src/rl_triton/kernels/*.py); each struct
+// cites the lines it reproduces.  Padding steps (t >= T) are the identity map.
+#pragma once
+#include "rlk_engine.hpp"
+
+namespace rlk {
+
+template <int S>
+__device__ __forceinline__ void fill_regs(float (&v)[S], float x) {
+#pragma unroll
+  for (int i = 0; i < S; ++i) v[i] = x;
+}
+
+// ------------------------------------------------------------------------------------------
+// GAE: kernels/gae.py:259-318 (gae_fused_kernel), both HAS_TRUNCATIONS branches.
+//   v_next = boot(t)  if t == T-1 or trunc[t] == 1,  values[t+1] otherwise
+//   add = r + gamma*v_next*(1-term) - v,   mul = gamma*lambda*(1 - done)
+//   done = min(term + trunc, 1) with truncations, term without;   x[T] = 0
+// ------------------------------------------------------------------------------------------
+struct GaeOp {
+  static constexpr bool kForward = false;
+  using Halo = float;  // values[t+1]
+  const float* r;
+  const float* v;
+  const float* term;
+  const float* trunc;  // nullable
+  const float* boot;   // nullable, per boot_mode
+  float* out;
+  int boot_mode;
+  float gamma, gl;  // gl = gamma*lambda
+
+  template <int S>
+  struct Regs {
+    float r[S], v[S], te[S], tr[S], bt[S];
+  };
+
+  template <int S, bool VEC>
+  __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
+    const int64_t o = row * (int64_t)T;
+    load_seg<S, VEC>(r + o, t0, T, R.r, 0.f);
+    load_seg<S, VEC>(v + o, t0, T, R.v, 0.f);
+    load_seg<S, VEC>(term + o, t0, T, R.te, 1.f);
+    if (trunc) load_seg<S, VEC>(trunc + o, t0, T, R.tr, 0.f);
+    else fill_regs(R.tr, 0.f);
+    load_boot<S, VEC>(boot, boot_mode, row, t0, T, R.bt, trunc != nullptr);
+  }
+  template <int S>
+  __device__ void clear(Regs<S>& R) const {
+    fill_regs(R.r, 0.f), fill_regs(R.v, 0.f), fill_regs(R.te, 1.f), fill_regs(R.tr, 0.f),
+        fill_regs(R.bt, 0.f);
+  }
+  template <int S>
+  __device__ float export_first(const Regs<S>& R) const { return R.v[0]; }
+  __device__ float halo_load(int64_t row, int t, int T) const { return v[row * (int64_t)T + t]; }
+
+  template <int S>
+  __device__ void coef(const Regs<S>& R, float vh, int64_t row, int t0, int T, float (&mul)[S],
+                       float (&add)[S]) const {
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const int t = t0 + i;
+      const float raw = (i + 1 < S) ? R.v[i + 1] : vh;
+      const float vn = (t == T - 1 || R.tr[i] == 1.f) ? R.bt[i] : raw;
+      const float done = trunc ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
+      const float a = fmaf(gamma * vn, 1.f - R.te[i], R.r[i]) - R.v[i];
+      const bool in = t < T;  // padding steps are the identity map
+      add[i] = in ? a : 0.f;
+      mul[i] = in ? gl * (1.f - done) : 1.f;
+    }
+  }
+  __device__ float row_carry(int64_t, int) const { return 0.f; }
+
+  template <int S, bool VEC>
+  __device__ void emit(const Regs<S>&, float, const float (&xs)[S], float, int64_t row, int t0,
+                       int T) const {
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
+  }
+};
+
+// ------------------------------------------------------------------------------------------
+// V-trace: kernels/vtrace_fused.py:90-196 (vtrace_fused_kernel).
+//   rho = min(exp(lpt - lpb), rho_bar),  c = min(exp(lpt - lpb), c_bar)
+//   truncations:  v_next = values[t+1]*[t < T-1 and trunc == 0] + boot(t)   (additive)
+//   otherwise:    v_next = boot(T-1) at t = T-1, values[t+1] elsewhere
+//   add = rho*(r + gamma*v_next*(1-term) - v),  mul = gamma*c*(1-done),  x[T] = 0
+//   targets = x + v;  next target by the same rule as v_next with targets for values
+//   advantages = rho*(r + gamma*next_target*(1-term) - v)
+// The reference passes targets[t+1] through global memory (store, barrier, reload,
+// vtrace_fused.py:149-152); here it is the neighbouring register or lane.
+// ------------------------------------------------------------------------------------------
+struct VtraceOp {
+  static constexpr bool kForward = false;
+  using Halo = float;  // values[t+1]
+  const float* lpt;
+  const float* lpb;
+  const float* v;
+  const float* r;
+  const float* term;
+  const float* trunc;  // nullable
+  const float* boot;   // nullable, per boot_mode
+  float* targets;
+  float* adv;
+  int boot_mode;
+  float gamma, rho_bar, c_bar;
+
+  template <int S>
+  struct Regs {
+    float rho[S], c[S], v[S], r[S], te[S], tr[S], bt[S];
+  };
+
+  template <int S, bool VEC>
+  __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
+    const int64_t o = row * (int64_t)T;
+    float a[S], b[S];
+    load_seg<S, VEC>(lpt + o, t0, T, a, 0.f);
+    load_seg<S, VEC>(lpb + o, t0, T, b, 0.f);
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const float ratio = expf(a[i] - b[i]);
+      R.rho[i] = fminf(ratio, rho_bar);
+      R.c[i] = fminf(ratio, c_bar);
+    }
+    load_seg<S, VEC>(v + o, t0, T, R.v, 0.f);
+    load_seg<S, VEC>(r + o, t0, T, R.r, 0.f);
+    load_seg<S, VEC>(term + o, t0, T, R.te, 1.f);
+    if (trunc) load_seg<S, VEC>(trunc + o, t0, T, R.tr, 0.f);
+    else fill_regs(R.tr, 0.f);
+    load_boot<S, VEC>(boot, boot_mode, row, t0, T, R.bt, trunc != nullptr);
+  }
+  template <int S>
+  __device__ void clear(Regs<S>& R) const {
+    fill_regs(R.rho, 0.f), fill_regs(R.c, 0.f), fill_regs(R.v, 0.f), fill_regs(R.r, 0.f),
+        fill_regs(R.te, 1.f), fill_regs(R.tr, 0.f), fill_regs(R.bt, 0.f);
+  }
+  template <int S>
+  __device__ float export_first(const Regs<S>& R) const { return R.v[0]; }
+  __device__ float halo_load(int64_t row, int t, int T) const { return v[row * (int64_t)T + t]; }
+
+  // continuation value at step t from the raw next-step value (values or targets)
+  __device__ __forceinline__ float next_value(float raw, float tr, float bt, int t, int T) const {
+    if (trunc) return ((t < T - 1 && tr == 0.f) ? raw : 0.f) + bt;
+    return (t == T - 1) ? bt : raw;
+  }
+
+  template <int S>
+  __device__ void coef(const Regs<S>& R, float vh, int64_t, int t0, int T, float (&mul)[S],
+                       float (&add)[S]) const {
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const int t = t0 + i;
+      const float vn = next_value((i + 1 < S) ? R.v[i + 1] : vh, R.tr[i], R.bt[i], t, T);
+      const float done = trunc ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
+      const float a = R.rho[i] * (fmaf(gamma * vn, 1.f - R.te[i], R.r[i]) - R.v[i]);
+      const bool in = t < T;
+      add[i] = in ? a : 0.f;
+      mul[i] = in ? gamma * R.c[i] * (1.f - done) : 1.f;
+    }
+  }
+  __device__ float row_carry(int64_t, int) const { return 0.f; }
+
+  template <int S, bool VEC>
+  __device__ void emit(const Regs<S>& R, float vh, const float (&xs)[S], float x_next, int64_t row,
+                       int t0, int T) const {
+    float tg[S], ad[S];
+#pragma unroll
+    for (int i = 0; i < S; ++i) tg[i] = xs[i] + R.v[i];
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const float raw = (i + 1 < S) ? tg[i + 1] : x_next + vh;
+      const float nt = next_value(raw, R.tr[i], R.bt[i], t0 + i, T);
+      ad[i] = R.rho[i] * (fmaf(gamma * nt, 1.f - R.te[i], R.r[i]) - R.v[i]);
+    }
+    const int64_t o = row * (int64_t)T;
+    store_seg<S, VEC>(targets + o, t0, T, tg);
+    store_seg<S, VEC>(adv + o, t0, T, ad);
+  }
+};
+
+// ------------------------------------------------------------------------------------------
+// Retrace(lambda): kernels/retrace_fused.py:430-515 (retrace_fused_kernel).
+//   E_pi[Q'] = sum_a pi[t,a]*nq[t,a];  pi_a = pi[t, a_t] (0 if a_t outside [0, A))
+//   rho = min(pi_a/mu, rho_bar),  c = lambda*min(pi_a/mu, c_bar)
+//   add = r + gamma*E_pi[Q']*(1-term) - q,  mul = gamma*c[t+1]*(1-done),  c[T] = 0
+//   Q_ret = x + q;  advantages = rho*(r + gamma*Q_ret[t+1]*(1-term) - q),  Q_ret[T] = 0
+// NA > 0: compile-time action count (vector loads of the [S, A] block); NA == 0: runtime A.
+// ------------------------------------------------------------------------------------------
+template <int NA>
+struct RetraceOp {
+  static constexpr bool kForward = false;
+  using Halo = Halo2;  // {c[t+1], q[t+1]}
+  const float* pi;     // [E, T, A]
+  const float* mu;     // [E, T]
+  const float* q;
+  const float* nq;     // [E, T, A]
+  const int64_t* act;  // [E, T]
+  const float* r;
+  const float* term;
+  const float* trunc;  // nullable
+  float* targets;
+  float* adv;
+  int A;
+  float gamma, lambda, c_bar, rho_bar;
+
+  template <int S>
+  struct Regs {
+    float q[S], r[S], te[S], tr[S], rho[S], c[S], enq[S];
+  };
+
+  // (rho, c, E_pi[Q']) at one step from its action row
+  __device__ __forceinline__ void step_terms(const float* p, const float* n, int64_t a_t, float m,
+                                             float& rho, float& c, float& enq) const {
+    float e = 0.f, pa = 0.f;
+    const int na = NA > 0 ? NA : A;
+    for (int a = 0; a < na; ++a) {
+      const float pv = p[a];
+      e = fmaf(pv, n[a], e);
+      pa = (a == a_t) ? pv : pa;
+    }
+    const float ratio = pa / m;
+    rho = fminf(ratio, rho_bar);
+    c = lambda * fminf(ratio, c_bar);
+    enq = e;
+  }
+
+  template <int S, bool VEC>
+  __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
+    const int64_t o = row * (int64_t)T;
+    float m[S];
+    load_seg<S, VEC>(q + o, t0, T, R.q, 0.f);
+    load_seg<S, VEC>(r + o, t0, T, R.r, 0.f);
+    load_seg<S, VEC>(term + o, t0, T, R.te, 1.f);
+    if (trunc) load_seg<S, VEC>(trunc + o, t0, T, R.tr, 0.f);
+    else fill_regs(R.tr, 0.f);
+    load_seg<S, VEC>(mu + o, t0, T, m, 1.f);
+    int64_t at[S];
+#pragma unroll
+    for (int i = 0; i < S; ++i) at[i] = (t0 + i < T) ? act[o + t0 + i] : 0;
+    if constexpr (NA > 0 && VEC && (S * NA) % 4 == 0) {
+      // the [S, NA] blocks are contiguous and 16-byte aligned
+      float pb[S * NA], nb[S * NA];
+      const float* pp = pi + (o + t0) * NA;
+      const float* np = nq + (o + t0) * NA;
+#pragma unroll
+      for (int qd = 0; qd < S * NA / 4; ++qd) {
+        if (t0 + (4 * qd) / NA < T) {
+          const float4 a4 = *reinterpret_cast<const float4*>(pp + 4 * qd);
+          const float4 b4 = *reinterpret_cast<const float4*>(np + 4 * qd);
+          pb[4 * qd] = a4.x, pb[4 * qd + 1] = a4.y, pb[4 * qd + 2] = a4.z, pb[4 * qd + 3] = a4.w;
+          nb[4 * qd] = b4.x, nb[4 * qd + 1] = b4.y, nb[4 * qd + 2] = b4.z, nb[4 * qd + 3] = b4.w;
+        } else {
+          pb[4 * qd] = pb[4 * qd + 1] = pb[4 * qd + 2] = pb[4 * qd + 3] = 0.f;
+          nb[4 * qd] = nb[4 * qd + 1] = nb[4 * qd + 2] = nb[4 * qd + 3] = 0.f;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < S; ++i) step_terms(pb + i * NA, nb + i * NA, at[i], m[i], R.rho[i], R.c[i], R.enq[i]);
+    } else {
+      const int na = NA > 0 ? NA : A;
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        if (t0 + i < T) {
+          const int64_t base = (o + t0 + i) * na;
+          step_terms(pi + base, nq + base, at[i], m[i], R.rho[i], R.c[i], R.enq[i]);
+        } else {
+          R.rho[i] = 0.f, R.c[i] = 0.f, R.enq[i] = 0.f;
+        }
+      }
+    }
+  }
+  template <int S>
+  __device__ void clear(Regs<S>& R) const {
+    fill_regs(R.q, 0.f), fill_regs(R.r, 0.f), fill_regs(R.te, 1.f), fill_regs(R.tr, 0.f),
+        fill_regs(R.rho, 0.f), fill_regs(R.c, 0.f), fill_regs(R.enq, 0.f);
+  }
+  template <int S>
+  __device__ Halo2 export_first(const Regs<S>& R) const { return Halo2{R.c[0], R.q[0]}; }
+  __device__ Halo2 halo_load(int64_t row, int t, int T) const {
+    const int64_t i = row * (int64_t)T + t;
+    const int na = NA > 0 ? NA : A;
+    float rho, c, enq;
+    step_terms(pi + i * na, nq + i * na, act[i], mu[i], rho, c, enq);
+    return Halo2{c, q[i]};
+  }
+
+  template <int S>
+  __device__ void coef(const Regs<S>& R, Halo2 h, int64_t, int t0, int T, float (&mul)[S],
+                       float (&add)[S]) const {
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const int t = t0 + i;
+      const float c_next = (t < T - 1) ? ((i + 1 < S) ? R.c[i + 1] : h.a) : 0.f;
+      const float done = fminf(R.te[i] + R.tr[i], 1.f);
+      const float a = fmaf(gamma * R.enq[i], 1.f - R.te[i], R.r[i]) - R.q[i];
+      const bool in = t < T;
+      add[i] = in ? a : 0.f;
+      mul[i] = in ? gamma * c_next * (1.f - done) : 1.f;
+    }
+  }
+  __device__ float row_carry(int64_t, int) const { return 0.f; }
+
+  template <int S, bool VEC>
+  __device__ void emit(const Regs<S>& R, Halo2 h, const float (&xs)[S], float x_next, int64_t row,
+                       int t0, int T) const {
+    float tg[S], ad[S];
+#pragma unroll
+    for (int i = 0; i < S; ++i) tg[i] = xs[i] + R.q[i];
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const int t = t0 + i;
+      const float nxt = (t < T - 1) ? ((i + 1 < S) ? tg[i + 1] : x_next + h.b) : 0.f;
+      ad[i] = R.rho[i] * (fmaf(gamma * nxt, 1.f - R.te[i], R.r[i]) - R.q[i]);
+    }
+    const int64_t o = row * (int64_t)T;
+    store_seg<S, VEC>(targets + o, t0, T, tg);
+    store_seg<S, VEC>(adv + o, t0, T, ad);
+  }
+};
+
+// ------------------------------------------------------------------------------------------
+// TD(lambda) returns: kernels/lambda_returns_fused.py:54-89.
+//   nd = 1 - done;  add = r + gamma*(1-lambda)*nd*nv + gamma*trunc*boot(t);  mul = gamma*lambda*nd
+//   x[T] = boot(T-1)
+// Discounted returns: kernels/discounted_returns_fused.py:139-171 -- the same with
+//   add = r + gamma*trunc*boot(t),  mul = gamma*nd  (nv unused, flagged by nv == nullptr).
+// ------------------------------------------------------------------------------------------
+struct ReturnsOp {
+  static constexpr bool kForward = false;
+  using Halo = NoHalo;
+  const float* r;
+  const float* nv;     // nullptr: discounted returns
+  const float* term;
+  const float* trunc;  // nullable
+  const float* boot;   // nullable, per boot_mode
+  float* out;
+  int boot_mode;
+  float gamma, g1l, gl;  // gamma, gamma*(1-lambda), gamma*lambda (discounted: gl = gamma)
+
+  template <int S>
+  struct Regs {
+    float r[S], nv[S], te[S], tr[S], bt[S];
+  };
+
+  template <int S, bool VEC>
+  __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
+    const int64_t o = row * (int64_t)T;
+    load_seg<S, VEC>(r + o, t0, T, R.r, 0.f);
+    if (nv) load_seg<S, VEC>(nv + o, t0, T, R.nv, 0.f);
+    else fill_regs(R.nv, 0.f);
+    load_seg<S, VEC>(term + o, t0, T, R.te, 1.f);
+    if (trunc) {
+      load_seg<S, VEC>(trunc + o, t0, T, R.tr, 0.f);
+      load_boot<S, VEC>(boot, boot_mode, row, t0, T, R.bt, trunc != nullptr);
+    } else {
+      fill_regs(R.tr, 0.f), fill_regs(R.bt, 0.f);
+    }
+  }
+  template <int S>
+  __device__ void clear(Regs<S>& R) const {
+    fill_regs(R.r, 0.f), fill_regs(R.nv, 0.f), fill_regs(R.te, 1.f), fill_regs(R.tr, 0.f),
+        fill_regs(R.bt, 0.f);
+  }
+
+  template <int S>
+  __device__ void coef(const Regs<S>& R, NoHalo, int64_t, int t0, int T, float (&mul)[S],
+                       float (&add)[S]) const {
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const int t = t0 + i;
+      const float nd = 1.f - (trunc ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i]);
+      float a = nv ? fmaf(g1l * nd, R.nv[i], R.r[i]) : R.r[i];
+      if (trunc) a = fmaf(gamma * R.tr[i], R.bt[i], a);
+      const bool in = t < T;
+      add[i] = in ? a : 0.f;
+      mul[i] = in ? gl * nd : 1.f;
+    }
+  }
+  __device__ float row_carry(int64_t row, int T) const { return boot_at(boot, boot_mode, row, T - 1, T); }
+
+  template <int S, bool VEC>
+  __device__ void emit(const Regs<S>&, NoHalo, const float (&xs)[S], float, int64_t row, int t0,
+                       int T) const {
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
+  }
+};
+
+// ------------------------------------------------------------------------------------------
+// Forward scans gated on done.
+//   eligibility traces (kernels/eligibility_traces_fused.py:238-255):
+//       mul = gamma*lambda*(1 - done[t-1]), done[-1] = 0, add = g, x[-1] = seed
+//   episodic prefix sum (kernels/prefix_sum_fused.py:174-195):
+//       ends_at:   mul = 1 - done[t-1];  starts_at: mul = 1 - done[t];  add = x, x[-1] = seed
+// (decay = gamma*lambda for traces, 1 for the prefix sum)
+// ------------------------------------------------------------------------------------------
+struct DoneGatedForwardOp {
+  static constexpr bool kForward = true;
+  using Halo = float;  // done[t-1]
+  const float* x;
+  const float* dones;
+  const float* seed;  // nullable
+  float* out;
+  float decay;
+  int ends_at;
+
+  template <int S>
+  struct Regs {
+    float x[S], d[S];
+  };
+
+  template <int S, bool VEC>
+  __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
+    const int64_t o = row * (int64_t)T;
+    load_seg<S, VEC>(x + o, t0, T, R.x, 0.f);
+    load_seg<S, VEC>(dones + o, t0, T, R.d, 0.f);
+  }
+  template <int S>
+  __device__ void clear(Regs<S>& R) const { fill_regs(R.x, 0.f), fill_regs(R.d, 0.f); }
+  template <int S>
+  __device__ float export_last(const Regs<S>& R) const { return R.d[S - 1]; }
+  __device__ float halo_load(int64_t row, int t, int T) const { return dones[row * (int64_t)T + t]; }
+
+  template <int S>
+  __device__ void coef(const Regs<S>& R, float dh, int64_t, int t0, int T, float (&mul)[S],
+                       float (&add)[S]) const {
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const int t = t0 + i;
+      float gate;
+      if (ends_at) gate = (i > 0) ? R.d[i - 1] : (t == 0 ? 0.f : dh);
+      else gate = R.d[i];
+      const bool in = t < T;
+      mul[i] = in ? decay * (1.f - gate) : 1.f;
+      add[i] = in ? R.x[i] : 0.f;
+    }
+  }
+  __device__ float row_carry(int64_t row, int) const { return seed ? seed[row] : 0.f; }
+
+  template <int S, bool VEC>
+  __device__ void emit(const Regs<S>&, float, const float (&xs)[S], float, int64_t row, int t0,
+                       int T) const {
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
+  }
+};
+
+// ------------------------------------------------------------------------------------------
+// Generic affine scans (ops/_scan.py:69-213, kernels/scan.py:39-138):
+//   backward A[t] = u[t] + v[t]*A[t+1], A[T] = carry;  forward e[t] = u[t] + v[t]*e[t-1], e[-1] = carry
+// ------------------------------------------------------------------------------------------
+template <bool FWD>
+struct AffineScanOp {
+  static constexpr bool kForward = FWD;
+  using Halo = NoHalo;
+  const float* u;
+  const float* v;
+  const float* carry;  // nullable, [E]
+  float* out;
+
+  template <int S>
+  struct Regs {
+    float u[S], v[S];
+  };
+  template <int S, bool VEC>
+  __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
+    const int64_t o = row * (int64_t)T;
+    load_seg<S, VEC>(u + o, t0, T, R.u, 0.f);
+    load_seg<S, VEC>(v + o, t0, T, R.v, 1.f);
+  }
+  template <int S>
+  __device__ void clear(Regs<S>& R) const { fill_regs(R.u, 0.f), fill_regs(R.v, 1.f); }
+  template <int S>
+  __device__ void coef(const Regs<S>& R, NoHalo, int64_t, int t0, int T, float (&mul)[S],
+                       float (&add)[S]) const {
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const bool in = t0 + i < T;
+      mul[i] = in ? R.v[i] : 1.f;
+      add[i] = in ? R.u[i] : 0.f;
+    }
+  }
+  __device__ float row_carry(int64_t row, int) const { return carry ? carry[row] : 0.f; }
+  template <int S, bool VEC>
+  __device__ void emit(const Regs<S>&, NoHalo, const float (&xs)[S], float, int64_t row, int t0,
+                       int T) const {
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
+  }
+};
+
+}  // namespace rlk

@@ -1,0 +1,93 @@
+import torch
+
+from rl_triton.ops._scan import _FLAT_MAX_SEQ_LEN, _CORRECTNESS_WARNINGS
+from rl_triton.ops.vtrace_fused import _vtrace_launch, compute_vtrace_fused
+
+
+def compute_vtrace(
+    log_pi_target: torch.Tensor,
+    log_pi_behavior: torch.Tensor,
+    values: torch.Tensor,
+    rewards: torch.Tensor,
+    terminateds: torch.Tensor,
+    truncateds: torch.Tensor | None = None,
+    gamma: float = 0.99,
+    rho_bar: float = 1.0,
+    c_bar: float = 1.0,
+    bootstrap_values: torch.Tensor | None = None,
+    last_value: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """
+    V-trace targets and advantages (IMPALA, Espeholt et al. 2018).
+
+    Drop-in for src/rl_triton/ops/vtrace.py:7-201.  The input checks run only with
+    RL_TRITON_CORRECTNESS_WARNINGS=1, as in the reference; seq_len <= 131072 goes
+    through compute_vtrace_fused (with its always-on checks), longer rows go straight
+    to the same kernel, whose look-back path replaces the reference's torch +
+    chunked-scan fallback.  Recurrence and bootstrap rules: see compute_vtrace_fused.
+
+    Returns:
+        vtrace_targets:    vs[t], [num_envs, seq_len], float32.
+        vtrace_advantages: A[t],  [num_envs, seq_len], float32.
+    """
+    num_envs, seq_len = rewards.shape
+    has_truncations   = truncateds is not None
+
+    if _CORRECTNESS_WARNINGS():
+        for name, t in [
+            ("log_pi_target",   log_pi_target),
+            ("log_pi_behavior", log_pi_behavior),
+            ("values",          values),
+            ("rewards",         rewards),
+            ("terminateds",     terminateds),
+        ]:
+            assert t.is_cuda,                f"{name} must be on CUDA"
+            assert t.dtype == torch.float32, f"{name}: expected float32, got {t.dtype}"
+            assert t.shape == rewards.shape, f"{name} shape {t.shape} != rewards shape {rewards.shape}"
+        if has_truncations:
+            assert truncateds.is_cuda,                "truncateds must be on CUDA"
+            assert truncateds.dtype == torch.float32, "truncateds: expected float32"
+            assert truncateds.shape == rewards.shape, \
+                f"truncateds shape {truncateds.shape} != rewards shape {rewards.shape}"
+            assert not (terminateds.bool() & truncateds.bool()).any(), \
+                "terminated and truncated are mutually exclusive: a step cannot be both"
+        if last_value is not None:
+            assert bootstrap_values is None, \
+                "pass either last_value (shape [num_envs], convenience for the " \
+                "window boundary) or bootstrap_values (shape [num_envs, seq_len], " \
+                "full per-step control), not both."
+            assert last_value.shape == (num_envs,), \
+                f"last_value must have shape [{num_envs}], got {last_value.shape}"
+        if bootstrap_values is not None:
+            assert bootstrap_values.is_cuda,                "bootstrap_values must be on CUDA"
+            assert bootstrap_values.dtype == torch.float32, "bootstrap_values: expected float32"
+            assert bootstrap_values.shape == rewards.shape, \
+                f"bootstrap_values shape {bootstrap_values.shape} != rewards shape {rewards.shape}"
+        if has_truncations and bootstrap_values is not None:
+            interior = torch.ones_like(truncateds, dtype=torch.bool)
+            interior[:, -1] = False
+            stray = (bootstrap_values != 0) & (truncateds == 0) & interior
+            assert not stray.any(), (
+                "bootstrap_values must be zero at non-truncated interior steps. "
+                "Nonzero entries there double-count via the additive v_next trick "
+                "and corrupt delta. Populate bootstrap_values only at truncated "
+                "steps and at the final column (window boundary)."
+            )
+
+    if seq_len <= _FLAT_MAX_SEQ_LEN:
+        return compute_vtrace_fused(
+            log_pi_target, log_pi_behavior,
+            values, rewards, terminateds,
+            truncateds=truncateds if has_truncations else None,
+            gamma=gamma, rho_bar=rho_bar, c_bar=c_bar,
+            bootstrap_values=bootstrap_values,
+            last_value=last_value,
+        )
+
+    if last_value is not None:
+        assert bootstrap_values is None, \
+            "pass either last_value (shape [num_envs], convenience for the " \
+            "window boundary) or bootstrap_values (shape [num_envs, seq_len], " \
+            "full per-step control), not both."
+    return _vtrace_launch(log_pi_target, log_pi_behavior, values, rewards, terminateds,
+                          truncateds, gamma, rho_bar, c_bar, bootstrap_values, last_value)
