@@ -22,11 +22,12 @@
  *     decoupled look-back.  Those calls need `workspace` of at least
  *     rlk_workspace_bytes(num_envs, seq_len) bytes, ZERO-FILLED BEFORE ITS FIRST USE.
  *     Each call leaves the workspace ready for the next one, so zero it once and reuse
- *     it; calls that share a workspace must be ordered on one stream (concurrent use
- *     races).  Calls that need no workspace ignore the argument (NULL is fine).
- *     Layout (uint64 words): [0] ticket, [1] finished workgroups, [2] call epoch,
- *     [3] error flag -- nonzero if a look-back wait gave up (results of that call
- *     are invalid), [4..7] reserved, then two status words per tile.
+ *     it, across calls of any shape; calls that share a workspace must be ordered on one
+ *     stream (concurrent use races).  Calls that need no workspace ignore the argument
+ *     (NULL is fine).  Layout (uint64 words): [0..7] header, word [3] the error flag --
+ *     nonzero if a look-back wait gave up or the counters were not at rest (results of
+ *     that call are invalid); [8..2055] 64 ticket-counter slots; then two status words
+ *     per tile.
  *   - Return value: RLK_OK or a negative RLK_ERR_* code; rlk_status_string() names it.
  *     Empty inputs (num_envs == 0 or seq_len == 0) return RLK_OK without a launch.
  */

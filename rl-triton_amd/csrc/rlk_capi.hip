@@ -8,10 +8,19 @@
 namespace rlk {
 namespace {
 
-constexpr int kNT = 256;         // threads per workgroup (4 wavefronts)
-constexpr int kShortMaxT = 2048; // rows up to this length are kept whole in one workgroup
-constexpr int kTileS = 8;        // steps per thread on the look-back path
-constexpr int kTile = kNT * kTileS;
+// Launch geometry.  The macros only exist so that tuning sweeps can rebuild the library
+// with other values; the defaults are the shipped configuration.
+#ifndef RLK_LB_NT
+#define RLK_LB_NT 512
+#endif
+#ifndef RLK_LB_S
+#define RLK_LB_S 8
+#endif
+constexpr int kNT = 256;          // short rows: threads per workgroup (4 wavefronts)
+constexpr int kShortMaxT = 2048;  // rows up to this length are kept whole in one workgroup
+constexpr int kLbNT = RLK_LB_NT;  // look-back path: threads per workgroup
+constexpr int kTileS = RLK_LB_S;  // look-back path: steps per thread
+constexpr int kTile = kLbNT * kTileS;
 
 struct Plan {
   bool lookback;
@@ -28,7 +37,9 @@ int ceil_log2(int64_t x) {
 }
 
 // Short rows: S steps per thread, L = 2^ceil(log2(ceil(T/S))) threads per row, 256/L
-// rows per workgroup.  Long rows: tiles of kTile steps, one workgroup each.
+// rows per workgroup.  Long rows: tiles of kTile steps, one workgroup each; tickets come
+// from min(E, 64) counters (see rlk_engine.hpp), so the grid is padded to a multiple of
+// the slot count and surplus workgroups exit at once.
 Plan make_plan(int64_t E, int64_t T) {
   Plan p{};
   if (T <= kShortMaxT) {
@@ -41,9 +52,10 @@ Plan make_plan(int64_t E, int64_t T) {
   } else {
     p.lookback = true;
     p.S = kTileS;
-    p.log2L = ceil_log2(kNT);
+    p.log2L = ceil_log2(kLbNT);
     p.tiles_per_row = (int)((T + kTile - 1) / kTile);
-    p.grid = E * p.tiles_per_row;
+    const int64_t nslots = lookback_slots(E);
+    p.grid = nslots * ((E + nslots - 1) / nslots) * p.tiles_per_row;
   }
   return p;
 }
@@ -51,17 +63,17 @@ Plan make_plan(int64_t E, int64_t T) {
 size_t workspace_bytes(int64_t E, int64_t T) {
   if (E <= 0 || T <= kShortMaxT) return 0;
   const int64_t tiles = E * ((T + kTile - 1) / kTile);
-  return (size_t)(kHeaderWords + 2 * tiles) * sizeof(uint64_t);
+  return (size_t)(kStatusOffset + 2 * tiles) * sizeof(uint64_t);
 }
 
 bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <class Op, int S, bool VEC, bool LB>
+template <class Op, int NT, int S, bool VEC, bool LB>
 hipError_t launch_one(const Op& op, int64_t E, int T, int log2L, int tpr, uint64_t* ws, int64_t grid,
                       hipStream_t stream) {
   void* args[] = {const_cast<Op*>(&op), &E, &T, &log2L, &tpr, &ws};
-  return hipLaunchKernel(reinterpret_cast<const void*>(&scan_kernel<Op, kNT, S, VEC, LB>),
-                         dim3((unsigned)grid), dim3(kNT), args, 0, stream);
+  return hipLaunchKernel(reinterpret_cast<const void*>(&scan_kernel<Op, NT, S, VEC, LB>),
+                         dim3((unsigned)grid), dim3(NT), args, 0, stream);
 }
 
 template <class Op>
@@ -78,14 +90,14 @@ int launch(const Op& op, int64_t E, int64_t T, bool vec, void* workspace, size_t
   if (p.lookback) {
     if (ws == nullptr || workspace_bytes_given < workspace_bytes(E, T) || !aligned16(ws))
       return RLK_ERR_WORKSPACE;
-    e = vec ? launch_one<Op, kTileS, true, true>(op, E, Ti, p.log2L, p.tiles_per_row, ws, p.grid, s)
-            : launch_one<Op, kTileS, false, true>(op, E, Ti, p.log2L, p.tiles_per_row, ws, p.grid, s);
+    e = vec ? launch_one<Op, kLbNT, kTileS, true, true>(op, E, Ti, p.log2L, p.tiles_per_row, ws, p.grid, s)
+            : launch_one<Op, kLbNT, kTileS, false, true>(op, E, Ti, p.log2L, p.tiles_per_row, ws, p.grid, s);
   } else if (p.S == 4) {
-    e = vec ? launch_one<Op, 4, true, false>(op, E, Ti, p.log2L, 1, nullptr, p.grid, s)
-            : launch_one<Op, 4, false, false>(op, E, Ti, p.log2L, 1, nullptr, p.grid, s);
+    e = vec ? launch_one<Op, kNT, 4, true, false>(op, E, Ti, p.log2L, 1, nullptr, p.grid, s)
+            : launch_one<Op, kNT, 4, false, false>(op, E, Ti, p.log2L, 1, nullptr, p.grid, s);
   } else {
-    e = vec ? launch_one<Op, 8, true, false>(op, E, Ti, p.log2L, 1, nullptr, p.grid, s)
-            : launch_one<Op, 8, false, false>(op, E, Ti, p.log2L, 1, nullptr, p.grid, s);
+    e = vec ? launch_one<Op, kNT, 8, true, false>(op, E, Ti, p.log2L, 1, nullptr, p.grid, s)
+            : launch_one<Op, kNT, 8, false, false>(op, E, Ti, p.log2L, 1, nullptr, p.grid, s);
   }
   return e == hipSuccess ? RLK_OK : RLK_ERR_LAUNCH;
 }

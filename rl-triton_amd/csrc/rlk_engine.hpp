@@ -162,10 +162,25 @@ __device__ __forceinline__ Affine group_scan(Affine m, int W) {
 //   word1 = AGG: add
 // tag = (epoch << 2) | kind, kind 1 = AGG, 2 = INC.  A word whose epoch differs from the
 // current call's is "not yet published", so the workspace needs clearing only once.
-// Header (uint64): [0] ticket counter, [1] finished-workgroup counter, [2] epoch,
-//                  [3] error flag (set when a bounded wait gives up), [4..7] reserved.
+//
+// Workspace (uint64 words), the same layout for every shape so that one buffer serves
+// calls of any shape in stream order:
+//   header   [0..7]               [1] finished-slot counter, [2] epoch of the call,
+//                                 [3] error flag (a bounded wait gave up, or counters were
+//                                 not at rest); others reserved
+//   slots    [8 + 32*s], s < 64   ticket counter slot s (256 bytes each): +0 ticket,
+//                                 +16 finished-workgroup counter (its own 128-byte line)
+//   status   [8 + 32*64 + ...]    two words per tile, tiles of row r at r*tiles_per_row
+// Device-scope atomics on one address serialise (~12 ns each on MI355X), so tickets come
+// from up to 64 counters: row r draws from slot r % 64, and since a tile only ever waits
+// on tiles of its own row, handing out each slot's tiles in scan order is enough for
+// forward progress.  The epoch is global and advances once per call, after every slot
+// has finished, so a status word left by any earlier call never matches the current one.
 // ---------------------------------------------------------------------------------------
 constexpr int kHeaderWords = 8;
+constexpr int kSlots = 64;
+constexpr int kSlotWords = 32;
+constexpr int kStatusOffset = kHeaderWords + kSlots * kSlotWords;
 constexpr uint32_t kAgg = 1, kInc = 2;
 constexpr uint32_t kEpochMask = 0x3fffffffu;
 constexpr int kSpinLimit = 1 << 20;  // polls before a wait gives up (~1 s), never reached when correct
@@ -186,8 +201,30 @@ __device__ __forceinline__ uint64_t pack(uint32_t tag, float v) {
 //   S         steps per thread
 //   VEC       16-byte vector loads/stores (see load_seg)
 //   LOOKBACK  rows split into NT*S-step tiles chained by look-back (then L == NT)
-// Launch: !LOOKBACK: grid = ceil(E / (NT/L)); LOOKBACK: grid = E * tiles_per_row.
+// Launch: !LOOKBACK: grid = ceil(E / (NT/L));
+//         LOOKBACK: nslots = min(E, 64), grid = nslots * ceil(E / nslots) * tiles_per_row;
+//         workgroup b draws a ticket from slot b % nslots (surplus tickets exit at once).
 // ---------------------------------------------------------------------------------------
+__host__ __device__ inline int lookback_slots(int64_t E) { return E < kSlots ? (int)E : kSlots; }
+
+// Last act of a look-back workgroup: count it finished in its slot; the slot's last one
+// leaves the slot at rest, and the last slot to finish advances the epoch.
+__device__ __forceinline__ void lookback_finish(uint64_t* ws, uint64_t* sc, uint64_t wgs_per_slot,
+                                                int nslots, uint32_t epoch) {
+  const uint64_t fin =
+      __hip_atomic_fetch_add(sc + 16, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (fin == wgs_per_slot - 1) {
+    atomic_st(sc + 0, 0);
+    atomic_st(sc + 16, 0);
+    const uint64_t slots_done =
+        __hip_atomic_fetch_add(ws + 1, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (slots_done == (uint64_t)nslots - 1) {
+      atomic_st(ws + 1, 0);
+      atomic_st(ws + 2, (uint64_t)((epoch + 1) & kEpochMask));
+    }
+  }
+}
+
 template <class Op, int NT, int S, bool VEC, bool LOOKBACK>
 __global__ __launch_bounds__(NT) void scan_kernel(const Op op, int64_t E, int T, int log2L,
                                                   int tiles_per_row, uint64_t* __restrict__ ws) {
@@ -211,31 +248,35 @@ __global__ __launch_bounds__(NT) void scan_kernel(const Op op, int64_t E, int T,
   int64_t row;
   int k = 0;  // tile index within the row (LOOKBACK)
   uint32_t epoch = 0;
+  int nslots = 1;
+  uint64_t wgs_per_slot = 0;
+  uint64_t* sc = nullptr;
   if constexpr (LOOKBACK) {
+    nslots = lookback_slots(E);
+    const int slot = (int)(blockIdx.x % (unsigned)nslots);
+    wgs_per_slot = gridDim.x / (unsigned)nslots;
+    sc = ws + kHeaderWords + kSlotWords * slot;
     if (tid == 0) {
-      s_ticket = __hip_atomic_fetch_add(ws + 0, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_ticket = __hip_atomic_fetch_add(sc + 0, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       s_epoch = (uint32_t)atomic_ld(ws + 2) & kEpochMask;
     }
     __syncthreads();
     const int64_t ticket = (int64_t)s_ticket;
     epoch = s_epoch;
-    if (ticket >= (int64_t)gridDim.x) {
-      // A workspace whose counters were not left at rest (e.g. not zero-filled before its
-      // first use): flag the call as failed and touch nothing else.  Uniform per workgroup.
+    const int64_t rows_in_slot = (E - slot + nslots - 1) / nslots;
+    if (ticket >= rows_in_slot * tiles_per_row) {
+      // Surplus workgroup of this slot; a ticket beyond the slot's workgroup count means the
+      // counters were not at rest (workspace not zero-filled before first use): flag the
+      // call as failed.  Either way touch nothing else.  Uniform per workgroup.
       if (tid == 0) {
-        atomic_st(ws + 3, (uint64_t)1);
-        const uint64_t fin =
-            __hip_atomic_fetch_add(ws + 1, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (fin == (uint64_t)gridDim.x - 1) {
-          atomic_st(ws + 0, 0);
-          atomic_st(ws + 1, 0);
-          atomic_st(ws + 2, (uint64_t)((epoch + 1) & kEpochMask));
-        }
+        if (ticket >= (int64_t)wgs_per_slot) atomic_st(ws + 3, (uint64_t)1);
+        lookback_finish(ws, sc, wgs_per_slot, nslots, epoch);
       }
       return;
     }
-    row = ticket / tiles_per_row;
-    const int j = (int)(ticket - row * tiles_per_row);
+    const int64_t local_row = ticket / tiles_per_row;
+    const int j = (int)(ticket - local_row * tiles_per_row);
+    row = slot + (int64_t)nslots * local_row;
     k = FWD ? j : tiles_per_row - 1 - j;
   } else {
     row = (int64_t)blockIdx.x * (NT >> log2L) + (tid >> log2L);
@@ -295,7 +336,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(const Op op, int64_t E, int T,
           for (int v = NW - 1; v >= 0; --v) tm = compose(Affine{s_mul[v], s_add[v]}, tm);
         }
         const int64_t tile_base = row * tiles_per_row;
-        uint64_t* st = ws + kHeaderWords;
+        uint64_t* st = ws + kStatusOffset;
         const bool first_in_scan = FWD ? (k == 0) : (k == tiles_per_row - 1);
         const uint32_t tag_agg = (epoch << 2) | kAgg, tag_inc = (epoch << 2) | kInc;
         float c;
@@ -324,12 +365,15 @@ __global__ __launch_bounds__(NT) void scan_kernel(const Op op, int64_t E, int T,
             uint32_t kind = 0;
             float v0 = 1.f, v1 = 0.f;
             if (inr) {
+              // Both words in flight at once.  word1 is written once per call, before word0's
+              // AGG, so a current-epoch AGG word0 paired with a current-epoch word1 is a
+              // consistent (mul, add) pair; a stale word1 just means "not yet".
               const uint64_t w0 = atomic_ld(st + 2 * (tile_base + jj));
+              const uint64_t w1 = atomic_ld(st + 2 * (tile_base + jj) + 1);
               const uint32_t tag0 = (uint32_t)(w0 >> 32);
               v0 = __uint_as_float((uint32_t)w0);
               if ((tag0 >> 2) == epoch) kind = tag0 & 3u;
               if (kind == kAgg) {
-                const uint64_t w1 = atomic_ld(st + 2 * (tile_base + jj) + 1);
                 if ((uint32_t)(w1 >> 32) == tag_agg) v1 = __uint_as_float((uint32_t)w1);
                 else kind = 0;
               }
@@ -403,16 +447,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(const Op op, int64_t E, int T,
   if (active) op.template emit<S, VEC>(R, h, xs, x_in, row, t0, T);
 
   if constexpr (LOOKBACK) {
-    if (tid == 0) {
-      const uint64_t fin =
-          __hip_atomic_fetch_add(ws + 1, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (fin == (uint64_t)gridDim.x - 1) {
-        // last workgroup of this call: leave the workspace ready for the next call
-        atomic_st(ws + 0, 0);
-        atomic_st(ws + 1, 0);
-        atomic_st(ws + 2, (uint64_t)((epoch + 1) & kEpochMask));
-      }
-    }
+    if (tid == 0) lookback_finish(ws, sc, wgs_per_slot, nslots, epoch);
   }
 }
 
