@@ -14,7 +14,10 @@ Printed JSON (one line, stdout):
   value          whole-job Gelem/s = 2 * 4096 * 128 elements / ms_per_step
   roofline       the dominant kernel (V-trace): algorithmic bytes per launch
                  (28 B/elem: 5 reads + 2 writes) / its average launch duration, timed with
-                 HIP events recorded on the launch stream around each launch, vs 8 TB/s
+                 HIP events on the launch stream around batches of launches that the GPU
+                 runs back to back (queued behind a GPU spin), vs 8 TB/s; traffic = HBM
+                 bytes per launch measured by rocprofv3 counters (profiles/traffic_4096x128.json)
+  graph_replay   the same steps replayed from a captured HIP graph (no host work per call)
   ops            per-op device time, Gelem/s, GB/s and %-of-peak for both kernels
   cpu_baseline   the reference's sequential torch loops (restated in
                  oracle/torch_loops.py) on the host CPU, 1 thread, bounded sample
@@ -81,6 +84,17 @@ def run_vtrace(rl, s):
                              last_value=s["last_value"])
 
 
+def measured_traffic(op):
+    """HBM bytes per launch of `op`'s kernel from the committed rocprofv3 counter passes
+    (FETCH_SIZE and WRITE_SIZE scaled by a known-size copy), or None if absent."""
+    path = os.path.join(ROOT, "profiles", "traffic_4096x128.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["traffic_bytes_per_launch"][op]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def parity(np, cpu_sets, outs):
     from oracle import oracle as orc
     gae, vt = cpu_sets
@@ -96,24 +110,55 @@ def parity(np, cpu_sets, outs):
     return errs
 
 
-def time_ops(torch, rl, sets, iters):
-    """Average device duration of each op: HIP events recorded on the launch stream
-    immediately before and after each call."""
+def time_ops(torch, rl, sets, iters, batch=100):
+    """Average device duration of each op's kernel, from HIP events on the launch stream.
+    Each batch of `batch` calls is queued behind a GPU spin, so the GPU runs the kernels
+    back to back; an event before the first and after the last call brackets the batch."""
     stream = torch.cuda.current_stream()
     res = {}
     for name, fn, idx in (("gae", run_gae, 0), ("vtrace", run_vtrace, 1)):
-        pairs = []
-        for i in range(iters):
-            s = sets[i % len(sets)][idx]
+        total_ms, n = 0.0, 0
+        while n < iters:
+            torch.cuda._sleep(20_000_000)  # ~10 ms of GPU spin: room to queue the batch
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record(stream)
-            fn(rl, s)
+            for i in range(batch):
+                fn(rl, sets[(n + i) % len(sets)][idx])
             b.record(stream)
-            pairs.append((a, b))
-        torch.cuda.synchronize()
-        ms = [a.elapsed_time(b) for a, b in pairs]
-        res[name] = sum(ms) / len(ms)
+            torch.cuda.synchronize()
+            total_ms += a.elapsed_time(b)
+            n += batch
+        res[name] = total_ms / n
     return res
+
+
+def time_graph_steps(torch, rl, sets, steps):
+    """Steps replayed from a captured HIP graph (the same API calls, captured once per input
+    set): the device-bound throughput without per-call host work."""
+    n = min(len(sets), steps)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for i in range(n):  # warm the allocator on the capture stream
+            run_gae(rl, sets[i][0])
+            run_vtrace(rl, sets[i][1])
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(n):
+            run_gae(rl, sets[i][0])
+            run_vtrace(rl, sets[i][1])
+    graph.replay()
+    torch.cuda.synchronize()
+    reps = max(1, steps // n)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / (reps * n)
 
 
 def cpu_baseline(torch, cpu_sets, budget_s):
@@ -149,7 +194,20 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain elementwise copy (out = in * 1.0) of MIB MiB 20 times: "
+                         "the known-size reference that scales rocprofv3 FETCH_SIZE/WRITE_SIZE")
     a = ap.parse_args(argv)
+    if a.copy_calibration:
+        import torch
+        n = a.copy_calibration * 2 ** 20 // 4
+        src = torch.randn(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: 20 x (read {4 * n} B + write {4 * n} B)")
+        return 0
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(rows are independent; sharding is described in DESIGN.md). Run with --gpus 1.",
@@ -206,7 +264,12 @@ def main(argv=None):
         log(f"[bench] {name}: {ms * 1e3:.2f} us/launch, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of 8 TB/s)")
     dom = max(ops, key=lambda k: ops[k]["device_us"])
     roofline = {"bound": "hbm", "kernel": dom, "achieved": ops[dom]["gb_s"], "peak": PEAK_GBS,
-                "unit": "GB/s", "frac": round(ops[dom]["gb_s"] / PEAK_GBS, 4), "traffic": None}
+                "unit": "GB/s", "frac": round(ops[dom]["gb_s"] / PEAK_GBS, 4),
+                "traffic": measured_traffic(dom)}
+
+    graph_ms = time_graph_steps(torch, rl_triton, sets, a.steps)
+    log(f"[bench] graph-replayed step: {graph_ms * 1e3:.2f} us "
+        f"({2 * E * T / (graph_ms * 1e-3) / 1e9:.1f} Gelem/s)")
 
     cpu = None
     if not a.no_cpu_baseline:
@@ -223,8 +286,11 @@ def main(argv=None):
                                "last_value, one public-API call each per step, inputs rotated over "
                                f"{n_sets} HBM-resident sets",
                    "num_envs": E, "seq_len": T, "gamma": 0.99, "lambda": 0.95,
-                   "rho_bar": 1.0, "c_bar": 1.0, "timing": "eager API calls, HIP events"},
-        "roofline": roofline, "ops": ops, "parity_max_abs_err": errs, "cpu_baseline": cpu,
+                   "rho_bar": 1.0, "c_bar": 1.0, "timing": "value: eager public-API calls, HIP events around the timed region"},
+        "roofline": roofline, "ops": ops,
+        "graph_replay": {"ms_per_step": round(graph_ms, 6),
+                         "gelem_s": round(2 * E * T / (graph_ms * 1e-3) / 1e9, 3)},
+        "parity_max_abs_err": errs, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     return 0

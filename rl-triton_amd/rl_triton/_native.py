@@ -83,30 +83,35 @@ def load():
 
 
 # ---------------------------------------------------------------------------------------
-# argument checks (the last line of defence before pointers reach a kernel)
+# argument checks (the last line of defence before pointers reach a kernel).  Written for
+# a short per-call path: a few C-level tensor queries per argument.
 # ---------------------------------------------------------------------------------------
-def _require(t: torch.Tensor, name: str, shape, device, dtype=torch.float32) -> int:
+_F32 = torch.float32
+_I64 = torch.int64
+_raw_stream = torch._C._cuda_getCurrentRawStream
+_cur_device = torch._C._cuda_getDevice
+
+
+def _ptr(t, name, shape, dev, dtype=_F32) -> int:
+    """Data pointer of `t` after checking device index, dtype, shape and contiguity."""
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name}: expected a tensor, got {type(t).__name__}")
-    if t.device != device:
-        raise ValueError(f"{name} is on {t.device}, expected {device}")
-    if t.dtype != dtype:
-        raise ValueError(f"{name}: expected {dtype}, got {t.dtype}")
-    if tuple(t.shape) != shape:
-        raise ValueError(f"{name}: expected shape {list(shape)}, got {list(t.shape)}")
-    if not t.is_contiguous():
-        raise ValueError(f"{name} must be contiguous")
+    if t.get_device() != dev or t.dtype is not dtype or t.shape != shape or not t.is_contiguous():
+        raise ValueError(f"{name}: expected a contiguous {dtype} tensor of shape {list(shape)} on "
+                         f"cuda:{dev}, got {t.dtype} {list(t.shape)} on {t.device} "
+                         f"(contiguous={t.is_contiguous()})")
     return t.data_ptr()
 
 
-def _opt(t, name, shape, device):
-    return None if t is None else _require(t, name, shape, device)
+def _opt(t, name, shape, dev):
+    return None if t is None else _ptr(t, name, shape, dev)
 
 
-def _device_of(t: torch.Tensor) -> torch.device:
-    if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+def _device_of(t) -> int:
+    dev = t.get_device() if isinstance(t, torch.Tensor) else -1
+    if dev < 0 or t.device.type != "cuda":
         raise ValueError("rl_triton kernels need GPU tensors (device type 'cuda' on ROCm)")
-    return t.device
+    return dev
 
 
 def _check(status: int, what: str) -> None:
@@ -116,68 +121,63 @@ def _check(status: int, what: str) -> None:
 
 
 # ---------------------------------------------------------------------------------------
-# look-back workspace: one zero-initialised buffer per (device, stream), grown on demand.
-# Calls on one stream are ordered, which is what the kernels require of a shared
-# workspace.
+# look-back workspace: one zero-initialised buffer per (device, stream), grown on demand and
+# reused by calls of every shape (the kernels leave it ready for the next call).  Calls on
+# one stream are ordered, which is what sharing a workspace requires.
 # ---------------------------------------------------------------------------------------
 _workspaces: dict = {}
+_ws_need: dict = {}
 
 
-def _workspace(device: torch.device, stream: torch.cuda.Stream, n_env: int, n_t: int):
-    need = load().rlk_workspace_bytes(n_env, n_t)
+def _workspace(dev: int, stream: int, n_env: int, n_t: int):
+    key = (n_env, n_t)
+    need = _ws_need.get(key)
+    if need is None:
+        need = _ws_need[key] = load().rlk_workspace_bytes(n_env, n_t)
     if need == 0:
         return None, 0
-    key = (device.index, stream.cuda_stream)
-    ws = _workspaces.get(key)
+    ws = _workspaces.get((dev, stream))
     if ws is None or ws.numel() < need:
         size = max(need, 2 * ws.numel() if ws is not None else 0)
         size = (size + 255) // 256 * 256
-        with torch.cuda.stream(stream):
-            ws = torch.zeros(size, dtype=torch.uint8, device=device)
-        _workspaces[key] = ws
+        cur = torch.cuda.current_stream(dev)
+        if cur.cuda_stream != stream:
+            raise RuntimeError("workspace stream mismatch")
+        ws = torch.zeros(size, dtype=torch.uint8, device=torch.device("cuda", dev))
+        _workspaces[(dev, stream)] = ws
     return ws.data_ptr(), ws.numel()
 
 
 def workspace_error(device=None) -> bool:
     """True if any cached workspace on `device` recorded a look-back wait that gave up."""
+    want = None if device is None else torch.device(device).index
     for (dev, _), ws in list(_workspaces.items()):
-        if device is not None and dev != torch.device(device).index:
+        if want is not None and dev != want:
             continue
-        flag = ws[24:32].cpu().view(torch.int64).item()
-        if flag != 0:
+        if ws[24:32].cpu().view(torch.int64).item() != 0:
             return True
     return False
 
 
-class _Launch:
-    """Current device / stream context for one call."""
-
-    __slots__ = ("device", "stream", "guard")
-
-    def __init__(self, device: torch.device):
-        self.device = device
-        self.guard = None
-        if device.index is not None and device.index != torch.cuda.current_device():
-            self.guard = torch.cuda.device(device)
-        self.stream = torch.cuda.current_stream(device)
-
-    def __enter__(self):
-        if self.guard is not None:
-            self.guard.__enter__()
-        return self
-
-    def __exit__(self, *exc):
-        if self.guard is not None:
-            self.guard.__exit__(*exc)
-        return False
+def _launch(fn, what, dev, n_env, n_t, *args):
+    """Call C entry `fn` with `args` + (workspace, bytes, stream) on the current stream of
+    device `dev` (made current for the call if it is not)."""
+    if dev != _cur_device():
+        with torch.cuda.device(dev):
+            return _launch(fn, what, dev, n_env, n_t, *args)
+    stream = _raw_stream(dev)
+    ws, wsb = _workspace(dev, stream, n_env, n_t)
+    status = fn(*args, ws, wsb, stream)
+    if status != 0:
+        _check(status, what)
 
 
-def _boot_args(boot, n_env, n_t, device):
+def _boot_args(boot, n_env, n_t, dev):
     if boot is None:
         return None, BOOT_NONE
-    if tuple(boot.shape) == (n_env,):
-        return _require(boot, "bootstrap", (n_env,), device), BOOT_ROW
-    return _require(boot, "bootstrap", (n_env, n_t), device), BOOT_FULL
+    if boot.dim() == 1:
+        return _ptr(boot, "bootstrap", torch.Size((n_env,)), dev), BOOT_ROW
+    return _ptr(boot, "bootstrap", torch.Size((n_env, n_t)), dev), BOOT_FULL
 
 
 # ---------------------------------------------------------------------------------------
@@ -185,143 +185,116 @@ def _boot_args(boot, n_env, n_t, device):
 # ---------------------------------------------------------------------------------------
 def gae(rewards, values, terminateds, truncateds, bootstrap, out, gamma, lambda_):
     dev = _device_of(rewards)
-    shape = tuple(rewards.shape)
+    shape = rewards.shape
     n_env, n_t = shape
-    args = [_require(rewards, "rewards", shape, dev), _require(values, "values", shape, dev),
-            _require(terminateds, "terminateds", shape, dev),
-            _opt(truncateds, "truncateds", shape, dev)]
+    lib = _lib or load()
     bp, mode = _boot_args(bootstrap, n_env, n_t, dev)
-    o = _require(out, "out", shape, dev)
-    with _Launch(dev) as L:
-        ws, wsb = _workspace(dev, L.stream, n_env, n_t)
-        _check(load().rlk_gae(*args, bp, mode, o, n_env, n_t, gamma, lambda_, ws, wsb,
-                              L.stream.cuda_stream), "rlk_gae")
+    _launch(lib.rlk_gae, "rlk_gae", dev, n_env, n_t,
+            _ptr(rewards, "rewards", shape, dev), _ptr(values, "values", shape, dev),
+            _ptr(terminateds, "terminateds", shape, dev), _opt(truncateds, "truncateds", shape, dev),
+            bp, mode, _ptr(out, "out", shape, dev), n_env, n_t, gamma, lambda_)
     return out
 
 
 def vtrace(log_pi_target, log_pi_behavior, values, rewards, terminateds, truncateds, bootstrap,
            targets, advantages, gamma, rho_bar, c_bar):
     dev = _device_of(rewards)
-    shape = tuple(rewards.shape)
+    shape = rewards.shape
     n_env, n_t = shape
-    args = [_require(log_pi_target, "log_pi_target", shape, dev),
-            _require(log_pi_behavior, "log_pi_behavior", shape, dev),
-            _require(values, "values", shape, dev), _require(rewards, "rewards", shape, dev),
-            _require(terminateds, "terminateds", shape, dev),
-            _opt(truncateds, "truncateds", shape, dev)]
+    lib = _lib or load()
     bp, mode = _boot_args(bootstrap, n_env, n_t, dev)
-    tg = _require(targets, "targets", shape, dev)
-    ad = _require(advantages, "advantages", shape, dev)
-    with _Launch(dev) as L:
-        ws, wsb = _workspace(dev, L.stream, n_env, n_t)
-        _check(load().rlk_vtrace(*args, bp, mode, tg, ad, n_env, n_t, gamma, rho_bar, c_bar, ws,
-                                 wsb, L.stream.cuda_stream), "rlk_vtrace")
+    _launch(lib.rlk_vtrace, "rlk_vtrace", dev, n_env, n_t,
+            _ptr(log_pi_target, "log_pi_target", shape, dev),
+            _ptr(log_pi_behavior, "log_pi_behavior", shape, dev),
+            _ptr(values, "values", shape, dev), _ptr(rewards, "rewards", shape, dev),
+            _ptr(terminateds, "terminateds", shape, dev), _opt(truncateds, "truncateds", shape, dev),
+            bp, mode, _ptr(targets, "targets", shape, dev), _ptr(advantages, "advantages", shape, dev),
+            n_env, n_t, gamma, rho_bar, c_bar)
     return targets, advantages
 
 
 def retrace(action_probs_target, action_probs_behavior, q_values, next_q_values_all, actions,
             rewards, terminateds, truncateds, targets, advantages, gamma, lambda_, c_bar, rho_bar):
     dev = _device_of(rewards)
-    shape = tuple(rewards.shape)
+    shape = rewards.shape
     n_env, n_t = shape
     if action_probs_target.dim() != 3:
         raise ValueError("action_probs_target must be [num_envs, seq_len, num_actions]")
     n_act = action_probs_target.shape[2]
-    shape3 = (n_env, n_t, n_act)
-    args = [_require(action_probs_target, "action_probs_target", shape3, dev),
-            _require(action_probs_behavior, "action_probs_behavior", shape, dev),
-            _require(q_values, "q_values", shape, dev),
-            _require(next_q_values_all, "next_q_values_all", shape3, dev),
-            _require(actions, "actions", shape, dev, torch.int64),
-            _require(rewards, "rewards", shape, dev),
-            _require(terminateds, "terminateds", shape, dev),
-            _opt(truncateds, "truncateds", shape, dev)]
-    tg = _require(targets, "targets", shape, dev)
-    ad = _require(advantages, "advantages", shape, dev)
+    shape3 = torch.Size((n_env, n_t, n_act))
     if n_act == 0 and n_env * n_t > 0:
         raise ValueError("num_actions must be positive")
-    with _Launch(dev) as L:
-        ws, wsb = _workspace(dev, L.stream, n_env, n_t)
-        if n_env * n_t == 0:
-            return targets, advantages
-        _check(load().rlk_retrace(*args, tg, ad, n_env, n_t, n_act, gamma, lambda_, c_bar, rho_bar,
-                                  ws, wsb, L.stream.cuda_stream), "rlk_retrace")
+    lib = _lib or load()
+    _launch(lib.rlk_retrace, "rlk_retrace", dev, n_env, n_t,
+            _ptr(action_probs_target, "action_probs_target", shape3, dev),
+            _ptr(action_probs_behavior, "action_probs_behavior", shape, dev),
+            _ptr(q_values, "q_values", shape, dev),
+            _ptr(next_q_values_all, "next_q_values_all", shape3, dev),
+            _ptr(actions, "actions", shape, dev, _I64),
+            _ptr(rewards, "rewards", shape, dev), _ptr(terminateds, "terminateds", shape, dev),
+            _opt(truncateds, "truncateds", shape, dev),
+            _ptr(targets, "targets", shape, dev), _ptr(advantages, "advantages", shape, dev),
+            n_env, n_t, max(n_act, 1), gamma, lambda_, c_bar, rho_bar)
     return targets, advantages
 
 
 def lambda_returns(rewards, next_values, terminateds, truncateds, bootstrap, out, gamma, lambda_):
     dev = _device_of(rewards)
-    shape = tuple(rewards.shape)
+    shape = rewards.shape
     n_env, n_t = shape
-    args = [_require(rewards, "rewards", shape, dev),
-            _require(next_values, "next_values", shape, dev),
-            _require(terminateds, "terminateds", shape, dev),
-            _opt(truncateds, "truncateds", shape, dev)]
+    lib = _lib or load()
     bp, mode = _boot_args(bootstrap, n_env, n_t, dev)
-    o = _require(out, "out", shape, dev)
-    with _Launch(dev) as L:
-        ws, wsb = _workspace(dev, L.stream, n_env, n_t)
-        _check(load().rlk_lambda_returns(*args, bp, mode, o, n_env, n_t, gamma, lambda_, ws, wsb,
-                                         L.stream.cuda_stream), "rlk_lambda_returns")
+    _launch(lib.rlk_lambda_returns, "rlk_lambda_returns", dev, n_env, n_t,
+            _ptr(rewards, "rewards", shape, dev), _ptr(next_values, "next_values", shape, dev),
+            _ptr(terminateds, "terminateds", shape, dev), _opt(truncateds, "truncateds", shape, dev),
+            bp, mode, _ptr(out, "out", shape, dev), n_env, n_t, gamma, lambda_)
     return out
 
 
 def discounted_returns(rewards, terminateds, truncateds, bootstrap, out, gamma):
     dev = _device_of(rewards)
-    shape = tuple(rewards.shape)
+    shape = rewards.shape
     n_env, n_t = shape
-    args = [_require(rewards, "rewards", shape, dev),
-            _require(terminateds, "terminateds", shape, dev),
-            _opt(truncateds, "truncateds", shape, dev)]
+    lib = _lib or load()
     bp, mode = _boot_args(bootstrap, n_env, n_t, dev)
-    o = _require(out, "out", shape, dev)
-    with _Launch(dev) as L:
-        ws, wsb = _workspace(dev, L.stream, n_env, n_t)
-        _check(load().rlk_discounted_returns(*args, bp, mode, o, n_env, n_t, gamma, ws, wsb,
-                                             L.stream.cuda_stream), "rlk_discounted_returns")
+    _launch(lib.rlk_discounted_returns, "rlk_discounted_returns", dev, n_env, n_t,
+            _ptr(rewards, "rewards", shape, dev), _ptr(terminateds, "terminateds", shape, dev),
+            _opt(truncateds, "truncateds", shape, dev), bp, mode,
+            _ptr(out, "out", shape, dev), n_env, n_t, gamma)
     return out
 
 
 def eligibility_traces(gradients, dones, seed, out, gamma, lambda_):
     dev = _device_of(gradients)
-    shape = tuple(gradients.shape)
+    shape = gradients.shape
     n_env, n_t = shape
-    g = _require(gradients, "gradients", shape, dev)
-    d = _require(dones, "dones", shape, dev)
-    s = _opt(seed, "seed_values", (n_env,), dev)
-    o = _require(out, "out", shape, dev)
-    with _Launch(dev) as L:
-        ws, wsb = _workspace(dev, L.stream, n_env, n_t)
-        _check(load().rlk_eligibility_traces(g, d, s, o, n_env, n_t, gamma, lambda_, ws, wsb,
-                                             L.stream.cuda_stream), "rlk_eligibility_traces")
+    lib = _lib or load()
+    _launch(lib.rlk_eligibility_traces, "rlk_eligibility_traces", dev, n_env, n_t,
+            _ptr(gradients, "gradients", shape, dev), _ptr(dones, "dones", shape, dev),
+            _opt(seed, "seed_values", torch.Size((n_env,)), dev), _ptr(out, "out", shape, dev),
+            n_env, n_t, gamma, lambda_)
     return out
 
 
 def prefix_sum(inputs, dones, seed, out, ends_at):
     dev = _device_of(inputs)
-    shape = tuple(inputs.shape)
+    shape = inputs.shape
     n_env, n_t = shape
-    x = _require(inputs, "inputs", shape, dev)
-    d = _require(dones, "dones", shape, dev)
-    s = _opt(seed, "seed_values", (n_env,), dev)
-    o = _require(out, "out", shape, dev)
-    with _Launch(dev) as L:
-        ws, wsb = _workspace(dev, L.stream, n_env, n_t)
-        _check(load().rlk_prefix_sum(x, d, s, o, n_env, n_t, int(bool(ends_at)), ws, wsb,
-                                     L.stream.cuda_stream), "rlk_prefix_sum")
+    lib = _lib or load()
+    _launch(lib.rlk_prefix_sum, "rlk_prefix_sum", dev, n_env, n_t,
+            _ptr(inputs, "inputs", shape, dev), _ptr(dones, "dones", shape, dev),
+            _opt(seed, "seed_values", torch.Size((n_env,)), dev), _ptr(out, "out", shape, dev),
+            n_env, n_t, int(bool(ends_at)))
     return out
 
 
 def affine_scan(u, v, carry, out, direction):
     dev = _device_of(u)
-    shape = tuple(u.shape)
+    shape = u.shape
     n_env, n_t = shape
-    up = _require(u, "u", shape, dev)
-    vp = _require(v, "v", shape, dev)
-    c = _opt(carry, "bootstrap" if direction == BACKWARD else "seed", (n_env,), dev)
-    o = _require(out, "out", shape, dev)
-    with _Launch(dev) as L:
-        ws, wsb = _workspace(dev, L.stream, n_env, n_t)
-        _check(load().rlk_affine_scan(up, vp, c, o, n_env, n_t, direction, ws, wsb,
-                                      L.stream.cuda_stream), "rlk_affine_scan")
+    lib = _lib or load()
+    _launch(lib.rlk_affine_scan, "rlk_affine_scan", dev, n_env, n_t,
+            _ptr(u, "u", shape, dev), _ptr(v, "v", shape, dev),
+            _opt(carry, "bootstrap" if direction == BACKWARD else "seed", torch.Size((n_env,)), dev),
+            _ptr(out, "out", shape, dev), n_env, n_t, direction)
     return out

@@ -1,0 +1,124 @@
+"""CPU-side checks of the boundary: the C-ABI library and the drop-in API contract.
+
+No kernel runs here.  The library is loaded (a HIP fat binary loads without a GPU), its
+exported symbols are compared with include/rl_triton_amd.h, host-only entry points are
+called, and the reference's always-on AssertionErrors are raised on CPU tensors before
+any launch (ops/gae.py:106-129 and the matching blocks of the other ops).
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import rl_triton
+from rl_triton import _native
+from rl_triton.ops._scan import _FLAT_MAX_SEQ_LEN, _run_scan, _run_scan_forward
+from rl_triton.ops.retrace_fused import compute_retrace_fused
+from rl_triton.ops.vtrace_fused import compute_vtrace_fused
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "rl_triton_amd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char \*)\s*(rlk_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_native.library_path())
+    names = _declared()
+    assert len(names) >= 11
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in rl_triton_amd.h but not exported"
+    assert set(names) == set(_native.SIGNATURES), "binding signatures out of sync with the header"
+
+
+def test_host_only_entry_points():
+    lib = _native.load()
+    assert lib.rlk_version() >= 100
+    assert lib.rlk_status_string(0) == b"ok"
+    assert b"workspace" in lib.rlk_status_string(-2)
+    # short rows need no workspace; long rows need one, growing with the tile count
+    assert lib.rlk_workspace_bytes(4096, 128) == 0
+    assert lib.rlk_workspace_bytes(256, 2048) == 0
+    a = lib.rlk_workspace_bytes(8, 1 << 20)
+    b = lib.rlk_workspace_bytes(16, 1 << 20)
+    assert 0 < a < b and a % 8 == 0
+    assert lib.rlk_workspace_bytes(0, 1 << 20) == 0
+
+
+def test_entry_points_reject_bad_arguments_without_launching():
+    lib = _native.load()
+    # empty shapes succeed with null pointers; missing required pointers are refused
+    assert lib.rlk_gae(None, None, None, None, None, 0, None, 0, 128, 0.99, 0.95, None, 0, None) == 0
+    assert lib.rlk_gae(None, None, None, None, None, 0, None, 4, 128, 0.99, 0.95, None, 0, None) == -1
+    assert lib.rlk_prefix_sum(None, None, None, None, 4, 4, 1, None, 0, None) == -1
+    assert lib.rlk_affine_scan(None, None, None, None, 2, 8, 7, None, 0, None) == -1
+    fake = ctypes.c_void_p(16)  # never dereferenced: the call fails before any launch
+    # invalid bootstrap mode / missing bootstrap pointer
+    assert lib.rlk_gae(fake, fake, fake, None, None, 2, fake, 4, 8, 0.99, 0.95, None, 0, None) == -1
+    assert lib.rlk_gae(fake, fake, fake, None, fake, 9, fake, 4, 8, 0.99, 0.95, None, 0, None) == -1
+    # long rows without a workspace
+    assert lib.rlk_prefix_sum(fake, fake, None, fake, 2, 1 << 20, 1, None, 0, None) == -2
+
+
+def _cpu(*shape):
+    return torch.zeros(*shape)
+
+
+def test_gae_reference_assertions():
+    r = _cpu(4, 16)
+    with pytest.raises(AssertionError, match="rewards must be on CUDA"):
+        rl_triton.compute_gae(r, r, r)
+
+
+def test_vtrace_reference_assertions():
+    r = _cpu(4, 16)
+    with pytest.raises(AssertionError, match="log_pi_target must be on CUDA"):
+        rl_triton.compute_vtrace(r, r, r, r, r)
+    with pytest.raises(AssertionError, match="log_pi_target must be on CUDA"):
+        compute_vtrace_fused(r, r, r, r, r)
+
+
+def test_retrace_and_returns_reference_assertions():
+    r = _cpu(4, 16)
+    a3 = _cpu(4, 16, 2)
+    act = torch.zeros(4, 16, dtype=torch.int64)
+    with pytest.raises(AssertionError, match="must be on CUDA"):
+        rl_triton.compute_retrace(a3, r, r, a3, act, r, r, r, gamma=0.99)
+    with pytest.raises(AssertionError, match="rewards must be on CUDA"):
+        rl_triton.compute_lambda_returns(r, r, r)
+    with pytest.raises(AssertionError, match="rewards must be on CUDA"):
+        rl_triton.compute_discounted_returns(r, r)
+    with pytest.raises(AssertionError, match="gradients and dones must be on CUDA"):
+        rl_triton.compute_eligibility_traces(r, r, 0.99, 0.95)
+
+
+def test_flag_gated_paths_still_refuse_cpu_tensors(monkeypatch):
+    """Prefix sum and _run_scan check only under RL_TRITON_CORRECTNESS_WARNINGS (as in the
+    reference); without it the GPU binding itself refuses host tensors."""
+    monkeypatch.setenv("RL_TRITON_CORRECTNESS_WARNINGS", "0")
+    r = _cpu(4, 16)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        rl_triton.compute_episodic_prefix_sum(r, r)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        _run_scan(r, r)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        _run_scan_forward(r, r)
+    with pytest.raises(ValueError, match="boundary"):
+        rl_triton.compute_episodic_prefix_sum(r, r, boundary="middle")
+    monkeypatch.setenv("RL_TRITON_CORRECTNESS_WARNINGS", "1")
+    with pytest.raises(AssertionError, match="must be on CUDA"):
+        rl_triton.compute_episodic_prefix_sum(r, r)
+
+
+def test_public_surface_matches_reference():
+    assert rl_triton.__version__ == "0.1.3"
+    assert sorted(rl_triton.__all__) == sorted([
+        "compute_discounted_returns", "compute_eligibility_traces", "compute_episodic_prefix_sum",
+        "compute_gae", "compute_lambda_returns", "compute_retrace", "compute_vtrace"])
+    assert _FLAT_MAX_SEQ_LEN == 131072
+    assert callable(compute_retrace_fused)

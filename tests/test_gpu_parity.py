@@ -186,6 +186,20 @@ def test_last_value_equals_bootstrap_column(device):
     assert torch.equal(a, b)
 
 
+def test_last_value_and_bootstrap_values_are_exclusive(device):
+    """tests/test_gae.py:526-536, tests/test_vtrace.py:604-616."""
+    import rl_triton
+    r = torch.rand(4, 16, device=device)
+    z = torch.zeros(4, 16, device=device)
+    lv = torch.rand(4, device=device)
+    with pytest.raises(AssertionError, match="not both"):
+        rl_triton.compute_gae(r, r, z, bootstrap_values=z, last_value=lv)
+    with pytest.raises(AssertionError, match="not both"):
+        rl_triton.compute_vtrace(r, r, r, r, z, bootstrap_values=z, last_value=lv)
+    with pytest.raises(AssertionError, match="cannot be combined with truncateds"):
+        rl_triton.compute_gae(r, r, z, z, last_value=lv)
+
+
 def test_vtrace_fused_rejects_long(device):
     from rl_triton.ops.vtrace_fused import compute_vtrace_fused
     z = torch.zeros(1, 131073, device=device)
