@@ -2,6 +2,10 @@
 // include/rl_triton_amd.h): argument checks, launch planning and kernel launches.
 #include <hip/hip_runtime.h>
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "rl_triton_amd.h"
 #include "rlk_ops.hpp"
 
@@ -37,9 +41,8 @@ int ceil_log2(int64_t x) {
 }
 
 // Short rows: S steps per thread, L = 2^ceil(log2(ceil(T/S))) threads per row, 256/L
-// rows per workgroup.  Long rows: tiles of kTile steps, one workgroup each; tickets come
-// from min(E, 64) counters (see rlk_engine.hpp), so the grid is padded to a multiple of
-// the slot count and surplus workgroups exit at once.
+// rows per workgroup.  Long rows: tiles of kTile steps, drawn by a persistent grid of
+// min(E, 64) * k workgroups (see lookback_kernel in rlk_engine.hpp).
 Plan make_plan(int64_t E, int64_t T) {
   Plan p{};
   if (T <= kShortMaxT) {
@@ -54,8 +57,7 @@ Plan make_plan(int64_t E, int64_t T) {
     p.S = kTileS;
     p.log2L = ceil_log2(kLbNT);
     p.tiles_per_row = (int)((T + kTile - 1) / kTile);
-    const int64_t nslots = lookback_slots(E);
-    p.grid = nslots * ((E + nslots - 1) / nslots) * p.tiles_per_row;
+    p.grid = E * p.tiles_per_row;  // upper bound; the persistent grid is smaller
   }
   return p;
 }
@@ -68,12 +70,43 @@ size_t workspace_bytes(int64_t E, int64_t T) {
 
 bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <class Op, int NT, int S, bool VEC, bool LB>
-hipError_t launch_one(const Op& op, int64_t E, int T, int log2L, int tpr, uint64_t* ws, int64_t grid,
-                      hipStream_t stream) {
-  void* args[] = {const_cast<Op*>(&op), &E, &T, &log2L, &tpr, &ws};
-  return hipLaunchKernel(reinterpret_cast<const void*>(&scan_kernel<Op, NT, S, VEC, LB>),
-                         dim3((unsigned)grid), dim3(NT), args, 0, stream);
+// Resident workgroups of `kernel` on the current device (occupancy x compute units),
+// cached per kernel and device: the persistent look-back grid is sized to it.
+int resident_workgroups(const void* kernel, int nt) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find({kernel, dev});
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, nt, 0) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  const int n = per_cu * cus;
+  cache[{kernel, dev}] = n;
+  return n;
+}
+
+template <class Op, int S, bool VEC>
+hipError_t launch_rows(const Op& op, int64_t E, int T, int log2L, int64_t grid, hipStream_t stream) {
+  void* args[] = {const_cast<Op*>(&op), &E, &T, &log2L};
+  return hipLaunchKernel(reinterpret_cast<const void*>(&rows_kernel<Op, kNT, S, VEC>),
+                         dim3((unsigned)grid), dim3(kNT), args, 0, stream);
+}
+
+template <class Op, bool VEC>
+hipError_t launch_lookback(const Op& op, int64_t E, int T, int tpr, uint64_t* ws, hipStream_t stream) {
+  const void* kernel = reinterpret_cast<const void*>(&lookback_kernel<Op, kLbNT, kTileS, VEC>);
+  const int64_t nslots = lookback_slots(E);
+  const int64_t tiles_per_slot = ((E + nslots - 1) / nslots) * (int64_t)tpr;
+  int64_t wgs = resident_workgroups(kernel, kLbNT) / nslots;
+  if (wgs < 1) wgs = 1;
+  if (wgs > tiles_per_slot) wgs = tiles_per_slot;
+  const int64_t grid = nslots * wgs;
+  void* args[] = {const_cast<Op*>(&op), &E, &T, &tpr, &ws};
+  return hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(kLbNT), args, 0, stream);
 }
 
 template <class Op>
@@ -90,14 +123,14 @@ int launch(const Op& op, int64_t E, int64_t T, bool vec, void* workspace, size_t
   if (p.lookback) {
     if (ws == nullptr || workspace_bytes_given < workspace_bytes(E, T) || !aligned16(ws))
       return RLK_ERR_WORKSPACE;
-    e = vec ? launch_one<Op, kLbNT, kTileS, true, true>(op, E, Ti, p.log2L, p.tiles_per_row, ws, p.grid, s)
-            : launch_one<Op, kLbNT, kTileS, false, true>(op, E, Ti, p.log2L, p.tiles_per_row, ws, p.grid, s);
+    e = vec ? launch_lookback<Op, true>(op, E, Ti, p.tiles_per_row, ws, s)
+            : launch_lookback<Op, false>(op, E, Ti, p.tiles_per_row, ws, s);
   } else if (p.S == 4) {
-    e = vec ? launch_one<Op, kNT, 4, true, false>(op, E, Ti, p.log2L, 1, nullptr, p.grid, s)
-            : launch_one<Op, kNT, 4, false, false>(op, E, Ti, p.log2L, 1, nullptr, p.grid, s);
+    e = vec ? launch_rows<Op, 4, true>(op, E, Ti, p.log2L, p.grid, s)
+            : launch_rows<Op, 4, false>(op, E, Ti, p.log2L, p.grid, s);
   } else {
-    e = vec ? launch_one<Op, kNT, 8, true, false>(op, E, Ti, p.log2L, 1, nullptr, p.grid, s)
-            : launch_one<Op, kNT, 8, false, false>(op, E, Ti, p.log2L, 1, nullptr, p.grid, s);
+    e = vec ? launch_rows<Op, 8, true>(op, E, Ti, p.log2L, p.grid, s)
+            : launch_rows<Op, 8, false>(op, E, Ti, p.log2L, p.grid, s);
   }
   return e == hipSuccess ? RLK_OK : RLK_ERR_LAUNCH;
 }

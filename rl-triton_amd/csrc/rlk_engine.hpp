@@ -196,14 +196,154 @@ __device__ __forceinline__ uint64_t pack(uint32_t tag, float v) {
 }
 
 // ---------------------------------------------------------------------------------------
-// The kernel.
-//   NT        threads per workgroup (multiple of 64)
-//   S         steps per thread
-//   VEC       16-byte vector loads/stores (see load_seg)
-//   LOOKBACK  rows split into NT*S-step tiles chained by look-back (then L == NT)
-// Launch: !LOOKBACK: grid = ceil(E / (NT/L));
-//         LOOKBACK: nslots = min(E, 64), grid = nslots * ceil(E / nslots) * tiles_per_row;
-//         workgroup b draws a ticket from slot b % nslots (surplus tickets exit at once).
+// Segment pieces shared by both kernels.
+// ---------------------------------------------------------------------------------------
+
+// Issue the loads of this thread's segment, and of the neighbour step for the edge lane
+// whose neighbour lives outside its wave, together: the edge lane must not pay a second
+// memory round trip after its segment has arrived.
+template <class Op, int S, bool VEC>
+__device__ __forceinline__ void load_segment(const Op& op, bool active, int64_t row, int t0, int T,
+                                             int lane, typename Op::template Regs<S>& R,
+                                             typename Op::Halo& edge) {
+  if constexpr (!std::is_same<typename Op::Halo, NoHalo>::value) {
+    if constexpr (Op::kForward) {
+      if (active && lane == 0 && t0 > 0) edge = op.halo_load(row, t0 - 1, T);
+    } else {
+      if (active && lane == kWave - 1 && t0 + S < T) edge = op.halo_load(row, t0 + S, T);
+    }
+  }
+  if (active) op.template load<S, VEC>(row, t0, T, R);
+  else op.template clear<S>(R);
+}
+
+// The neighbour step's data: from the adjacent lane, or the edge load.
+template <class Op, int S>
+__device__ __forceinline__ typename Op::Halo neighbour(const Op& op,
+                                                       const typename Op::template Regs<S>& R,
+                                                       typename Op::Halo edge, int lane, int t0,
+                                                       int T) {
+  typename Op::Halo h{};
+  if constexpr (!std::is_same<typename Op::Halo, NoHalo>::value) {
+    if constexpr (Op::kForward) {
+      h = shfl_prev(op.template export_last<S>(R));
+      if (lane == 0 && t0 > 0) h = edge;
+    } else {
+      h = shfl_next(op.template export_first<S>(R));
+      if (lane == kWave - 1 && t0 + S < T) h = edge;
+    }
+  }
+  return h;
+}
+
+// The segment's map: steps composed in scan order.
+template <bool FWD, int S>
+__device__ __forceinline__ Affine fold_segment(const float (&mul)[S], const float (&add)[S]) {
+  Affine m{1.f, 0.f};
+  if constexpr (FWD) {
+#pragma unroll
+    for (int i = 0; i < S; ++i) m = compose(Affine{mul[i], add[i]}, m);
+  } else {
+#pragma unroll
+    for (int i = S - 1; i >= 0; --i) m = compose(Affine{mul[i], add[i]}, m);
+  }
+  return m;
+}
+
+// Every step's value from the value entering the segment.
+template <bool FWD, int S>
+__device__ __forceinline__ void replay(const float (&mul)[S], const float (&add)[S], float x_in,
+                                       float (&xs)[S]) {
+  float x = x_in;
+  if constexpr (FWD) {
+#pragma unroll
+    for (int i = 0; i < S; ++i) xs[i] = x = fmaf(mul[i], x, add[i]);
+  } else {
+#pragma unroll
+    for (int i = S - 1; i >= 0; --i) xs[i] = x = fmaf(mul[i], x, add[i]);
+  }
+}
+
+// The value entering each lane's segment, given the value entering its group of W lanes
+// (`carry`) and the lane's inclusive group-scan map `m`: the neighbour lane's outgoing value.
+template <bool FWD>
+__device__ __forceinline__ float lane_input(Affine m, float carry, int lane, int W) {
+  const float y = fmaf(m.mul, carry, m.add);
+  const int gl = lane & (W - 1);
+  float x_in;
+  if constexpr (FWD) {
+    x_in = __shfl_up(y, 1, kWave);
+    if (gl == 0) x_in = carry;
+  } else {
+    x_in = __shfl_down(y, 1, kWave);
+    if (gl == W - 1) x_in = carry;
+  }
+  return x_in;
+}
+
+// ---------------------------------------------------------------------------------------
+// Short rows: a workgroup of NT threads holds NT/L whole rows of L threads each
+// (L = 2^log2L, L*S >= T).  Launch: grid = ceil(E / (NT/L)).
+// ---------------------------------------------------------------------------------------
+template <class Op, int NT, int S, bool VEC>
+__global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T, int log2L) {
+  constexpr bool FWD = Op::kForward;
+  constexpr int NW = NT / kWave;
+  using Regs = typename Op::template Regs<S>;
+  using Halo = typename Op::Halo;
+  __shared__ float s_mul[NW], s_add[NW];
+
+  const int tid = threadIdx.x;
+  const int lane = __lane_id();
+  const int wave = tid / kWave;
+  const int L = 1 << log2L;
+  const int W = L < kWave ? L : kWave;
+  const int li = tid & (L - 1);
+  const int64_t row = (int64_t)blockIdx.x * (NT >> log2L) + (tid >> log2L);
+  const bool active = row < E;
+  const int t0 = li * S;
+
+  Regs R;
+  Halo edge{};
+  load_segment<Op, S, VEC>(op, active, row, t0, T, lane, R, edge);
+  const Halo h = neighbour<Op, S>(op, R, edge, lane, t0, T);
+
+  float mul[S], add[S];
+  op.template coef<S>(R, h, row, t0, T, mul, add);
+  const Affine m = group_scan<FWD>(fold_segment<FWD, S>(mul, add), W);
+
+  float carry = active ? op.row_carry(row, T) : 0.f;
+  if (L > kWave) {
+    // rows spanning several waves: combine the wave aggregates of the row through LDS
+    if (lane == (FWD ? kWave - 1 : 0)) {
+      s_mul[wave] = m.mul;
+      s_add[wave] = m.add;
+    }
+    __syncthreads();
+    const int wpr = L / kWave;
+    const int first = (wave / wpr) * wpr, last = first + wpr - 1;
+    if constexpr (FWD) {
+      for (int v = first; v < wave; ++v) carry = fmaf(s_mul[v], carry, s_add[v]);
+    } else {
+      for (int v = last; v > wave; --v) carry = fmaf(s_mul[v], carry, s_add[v]);
+    }
+  }
+  const float x_in = lane_input<FWD>(m, carry, lane, W);
+  float xs[S];
+  replay<FWD, S>(mul, add, x_in, xs);
+  if (active) op.template emit<S, VEC>(R, h, xs, x_in, row, t0, T);
+}
+
+// ---------------------------------------------------------------------------------------
+// Long rows: rows split into tiles of NT*S steps chained by a decoupled look-back.
+//
+// Persistent and software-pipelined: a workgroup keeps drawing tiles from its slot's
+// ticket counter (slot = blockIdx % nslots, nslots = min(E, 64); each slot hands out the
+// tiles of rows r = slot (mod nslots) in scan order) and works one tile ahead -- the next
+// tile's loads and the ticket after it are in flight while the current tile waits on its
+// predecessors and writes its outputs.  A workgroup only ever waits on tiles with smaller
+// tickets of its own slot, whose holders are running, so any grid size makes progress.
+// Launch: grid = nslots * wgs_per_slot.
 // ---------------------------------------------------------------------------------------
 __host__ __device__ inline int lookback_slots(int64_t E) { return E < kSlots ? (int)E : kSlots; }
 
@@ -225,230 +365,190 @@ __device__ __forceinline__ void lookback_finish(uint64_t* ws, uint64_t* sc, uint
   }
 }
 
-template <class Op, int NT, int S, bool VEC, bool LOOKBACK>
-__global__ __launch_bounds__(NT) void scan_kernel(const Op op, int64_t E, int T, int log2L,
-                                                  int tiles_per_row, uint64_t* __restrict__ ws) {
+__device__ __forceinline__ uint64_t draw_ticket(uint64_t* sc) {
+  return __hip_atomic_fetch_add(sc, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Carry entering tile k of `row` (wave 0 only, all 64 lanes): publish the tile's map and
+// look back.  Predecessors are read 64 at a time (lane i <-> i+1 tiles away).  Once the
+// nearest published inclusive value X has only aggregates between it and this tile, they
+// are applied to X one at a time, nearest last, so every published X equals the sequential
+// chain X_k = fma(A_k, X_{k+1}, B_k) however far the look-back reached: results are
+// bit-reproducible.  A bounded wait gives up (error flag, carry 0) rather than hang.
+template <class Op, bool FWD>
+__device__ __forceinline__ float tile_carry(const Op& op, Affine tm, int64_t row, int k, int T,
+                                            int tiles_per_row, uint32_t epoch, uint64_t* ws,
+                                            int lane) {
+  uint64_t* st = ws + kStatusOffset + 2 * (row * (int64_t)tiles_per_row);
+  const uint32_t tag_agg = (epoch << 2) | kAgg, tag_inc = (epoch << 2) | kInc;
+  if (FWD ? (k == 0) : (k == tiles_per_row - 1)) {
+    const float c = op.row_carry(row, T);
+    if (lane == 0) atomic_st(st + 2 * k, pack(tag_inc, fmaf(tm.mul, c, tm.add)));
+    return c;
+  }
+  if (lane == 0) {
+    if (tm.mul == 0.f) {
+      // the tile's outgoing value does not depend on its carry
+      atomic_st(st + 2 * k, pack(tag_inc, tm.add));
+    } else {
+      atomic_st(st + 2 * k + 1, pack(tag_agg, tm.add));
+      atomic_st(st + 2 * k, pack(tag_agg, tm.mul));
+    }
+  }
+  float c = 0.f;
+  for (int spins = 0;; ++spins) {
+    const int jj = FWD ? k - 1 - lane : k + 1 + lane;
+    const bool inr = FWD ? (jj >= 0) : (jj < tiles_per_row);
+    uint32_t kind = 0;
+    float v0 = 1.f, v1 = 0.f;
+    if (inr) {
+      // Both words in flight at once.  word1 is written once per call, before word0's AGG,
+      // so a current-epoch AGG word0 with a current-epoch word1 is a consistent (mul, add)
+      // pair; a stale word1 just means "not yet".
+      const uint64_t w0 = atomic_ld(st + 2 * jj);
+      const uint64_t w1 = atomic_ld(st + 2 * jj + 1);
+      const uint32_t tag0 = (uint32_t)(w0 >> 32);
+      v0 = __uint_as_float((uint32_t)w0);
+      if ((tag0 >> 2) == epoch) kind = tag0 & 3u;
+      if (kind == kAgg) {
+        if ((uint32_t)(w1 >> 32) == tag_agg) v1 = __uint_as_float((uint32_t)w1);
+        else kind = 0;
+      }
+    }
+    const uint64_t inc_mask = __ballot(kind == kInc);
+    const uint64_t bad_mask = __ballot(kind == 0);
+    const int first_inc = inc_mask ? __ffsll((long long)inc_mask) - 1 : kWave;
+    const int first_bad = bad_mask ? __ffsll((long long)bad_mask) - 1 : kWave;
+    if (first_inc < first_bad) {
+      float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v0), first_inc));
+      for (int l = first_inc - 1; l >= 0; --l) {
+        const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v0), l));
+        const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v1), l));
+        x = fmaf(a, x, b);
+      }
+      c = x;
+      break;
+    }
+    if (spins >= kSpinLimit) {
+      if (lane == 0) atomic_st(ws + 3, (uint64_t)1);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (lane == 0 && tm.mul != 0.f) atomic_st(st + 2 * k, pack(tag_inc, fmaf(tm.mul, c, tm.add)));
+  return c;
+}
+
+template <class Op, int NT, int S, bool VEC>
+__global__ __launch_bounds__(NT) void lookback_kernel(const Op op, int64_t E, int T,
+                                                      int tiles_per_row, uint64_t* __restrict__ ws) {
   constexpr bool FWD = Op::kForward;
   constexpr int NW = NT / kWave;
   using Regs = typename Op::template Regs<S>;
   using Halo = typename Op::Halo;
-
   __shared__ float s_mul[NW], s_add[NW];
   __shared__ float s_carry;
-  __shared__ uint64_t s_ticket;
+  __shared__ uint64_t s_q[2];
   __shared__ uint32_t s_epoch;
 
   const int tid = threadIdx.x;
   const int lane = __lane_id();
   const int wave = tid / kWave;
-  const int L = 1 << log2L;
-  const int W = L < kWave ? L : kWave;  // width of the intra-wave scan
-  const int li = tid & (L - 1);         // lane within the row tile
+  const int nslots = lookback_slots(E);
+  const int slot = (int)(blockIdx.x % (unsigned)nslots);
+  const uint64_t wgs_per_slot = gridDim.x / (unsigned)nslots;
+  uint64_t* sc = ws + kHeaderWords + kSlotWords * slot;
+  const int64_t rows_in_slot = (E - slot + nslots - 1) / nslots;
+  const uint64_t tiles_in_slot = (uint64_t)rows_in_slot * (uint64_t)tiles_per_row;
 
-  int64_t row;
-  int k = 0;  // tile index within the row (LOOKBACK)
-  uint32_t epoch = 0;
-  int nslots = 1;
-  uint64_t wgs_per_slot = 0;
-  uint64_t* sc = nullptr;
-  if constexpr (LOOKBACK) {
-    nslots = lookback_slots(E);
-    const int slot = (int)(blockIdx.x % (unsigned)nslots);
-    wgs_per_slot = gridDim.x / (unsigned)nslots;
-    sc = ws + kHeaderWords + kSlotWords * slot;
-    if (tid == 0) {
-      s_ticket = __hip_atomic_fetch_add(sc + 0, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_epoch = (uint32_t)atomic_ld(ws + 2) & kEpochMask;
-    }
-    __syncthreads();
-    const int64_t ticket = (int64_t)s_ticket;
-    epoch = s_epoch;
-    const int64_t rows_in_slot = (E - slot + nslots - 1) / nslots;
-    if (ticket >= rows_in_slot * tiles_per_row) {
-      // Surplus workgroup of this slot; a ticket beyond the slot's workgroup count means the
-      // counters were not at rest (workspace not zero-filled before first use): flag the
-      // call as failed.  Either way touch nothing else.  Uniform per workgroup.
-      if (tid == 0) {
-        if (ticket >= (int64_t)wgs_per_slot) atomic_st(ws + 3, (uint64_t)1);
-        lookback_finish(ws, sc, wgs_per_slot, nslots, epoch);
-      }
-      return;
-    }
-    const int64_t local_row = ticket / tiles_per_row;
-    const int j = (int)(ticket - local_row * tiles_per_row);
-    row = slot + (int64_t)nslots * local_row;
+  if (tid == 0) {
+    s_q[0] = draw_ticket(sc);
+    s_q[1] = draw_ticket(sc);
+    s_epoch = (uint32_t)atomic_ld(ws + 2) & kEpochMask;
+  }
+  __syncthreads();
+  uint64_t q = s_q[0], qn = s_q[1];
+  const uint32_t epoch = s_epoch;
+  if (tid == 0 && q >= tiles_in_slot + 2 * wgs_per_slot) atomic_st(ws + 3, (uint64_t)1);  // not at rest
+
+  // ticket -> (row, tile index in scan order -> tile position k)
+  auto decode = [&](uint64_t qq, int64_t& row, int& k) {
+    const int64_t lr = (int64_t)(qq / (uint64_t)tiles_per_row);
+    const int j = (int)(qq - (uint64_t)lr * tiles_per_row);
+    row = slot + (int64_t)nslots * lr;
     k = FWD ? j : tiles_per_row - 1 - j;
-  } else {
-    row = (int64_t)blockIdx.x * (NT >> log2L) + (tid >> log2L);
+  };
+
+  Regs cur;
+  Halo ecur{};
+  int64_t row = 0;
+  int k = 0;
+  if (q < tiles_in_slot) {
+    decode(q, row, k);
+    load_segment<Op, S, VEC>(op, true, row, (k * NT + tid) * S, T, lane, cur, ecur);
   }
-  const bool active = row < E;
-  const int t0 = (k * L + li) * S;
-
-  // 1. load the segment
-  Regs R;
-  if (active) op.template load<S, VEC>(row, t0, T, R);
-  else op.template clear<S>(R);
-
-  // 2. neighbour step data
-  Halo h{};
-  if constexpr (!std::is_same<Halo, NoHalo>::value) {
-    if constexpr (FWD) {
-      h = shfl_prev(op.template export_last<S>(R));
-      if (lane == 0 && t0 > 0 && active) h = op.halo_load(row, t0 - 1, T);
+  while (q < tiles_in_slot) {
+    const int t0 = (k * NT + tid) * S;
+    // prefetch: the next tile's loads and the ticket after it
+    const bool has_next = qn < tiles_in_slot;
+    Regs nxt;
+    Halo enxt{};
+    int64_t nrow = 0;
+    int nk = 0;
+    if (has_next) {
+      decode(qn, nrow, nk);
+      load_segment<Op, S, VEC>(op, true, nrow, (nk * NT + tid) * S, T, lane, nxt, enxt);
     } else {
-      h = shfl_next(op.template export_first<S>(R));
-      if (lane == kWave - 1 && t0 + S < T && active) h = op.halo_load(row, t0 + S, T);
+      op.template clear<S>(nxt);
     }
-  }
+    uint64_t qnn = ~(uint64_t)0;
+    if (tid == 0 && has_next) qnn = draw_ticket(sc);
 
-  // 3. per-step coefficients and the segment's map
-  float mul[S], add[S];
-  op.template coef<S>(R, h, row, t0, T, mul, add);
-  Affine m{1.f, 0.f};
-  if constexpr (FWD) {
-#pragma unroll
-    for (int i = 0; i < S; ++i) m = compose(Affine{mul[i], add[i]}, m);
-  } else {
-#pragma unroll
-    for (int i = S - 1; i >= 0; --i) m = compose(Affine{mul[i], add[i]}, m);
-  }
-
-  // 4. combine lanes of the wave
-  m = group_scan<FWD>(m, W);
-
-  // 5. carry into this wave's part of the row tile
-  float carry;
-  if (L > kWave || LOOKBACK) {
-    // wave aggregate: backward lane 0, forward lane 63
+    // the current tile
+    const Halo h = neighbour<Op, S>(op, cur, ecur, lane, t0, T);
+    float mul[S], add[S];
+    op.template coef<S>(cur, h, row, t0, T, mul, add);
+    const Affine m = group_scan<FWD>(fold_segment<FWD, S>(mul, add), kWave);
     if (lane == (FWD ? kWave - 1 : 0)) {
       s_mul[wave] = m.mul;
       s_add[wave] = m.add;
     }
     __syncthreads();
-    float tile_carry;
-    if constexpr (LOOKBACK) {
-      if (wave == 0) {
-        // the whole tile's map
-        Affine tm{1.f, 0.f};
-        if constexpr (FWD) {
-          for (int v = 0; v < NW; ++v) tm = compose(Affine{s_mul[v], s_add[v]}, tm);
-        } else {
-          for (int v = NW - 1; v >= 0; --v) tm = compose(Affine{s_mul[v], s_add[v]}, tm);
-        }
-        const int64_t tile_base = row * tiles_per_row;
-        uint64_t* st = ws + kStatusOffset;
-        const bool first_in_scan = FWD ? (k == 0) : (k == tiles_per_row - 1);
-        const uint32_t tag_agg = (epoch << 2) | kAgg, tag_inc = (epoch << 2) | kInc;
-        float c;
-        if (first_in_scan) {
-          c = op.row_carry(row, T);
-          if (lane == 0) atomic_st(st + 2 * (tile_base + k), pack(tag_inc, fmaf(tm.mul, c, tm.add)));
-        } else {
-          if (lane == 0) {
-            if (tm.mul == 0.f) {
-              // the tile's outgoing value does not depend on its carry
-              atomic_st(st + 2 * (tile_base + k), pack(tag_inc, tm.add));
-            } else {
-              atomic_st(st + 2 * (tile_base + k) + 1, pack(tag_agg, tm.add));
-              atomic_st(st + 2 * (tile_base + k), pack(tag_agg, tm.mul));
-            }
-          }
-          // Look back over the 64 nearest predecessors (lane i <-> i+1 tiles away) until the
-          // nearest published inclusive value X has only aggregates between it and this
-          // tile, then apply those aggregates to X one at a time, nearest last.  Every
-          // published X therefore equals the sequential chain X_k = fma(A_k, X_{k+1}, B_k)
-          // however far the look-back reached, which keeps results bit-reproducible.
-          int spins = 0;
-          while (true) {
-            const int jj = FWD ? k - 1 - lane : k + 1 + lane;
-            const bool inr = FWD ? (jj >= 0) : (jj < tiles_per_row);
-            uint32_t kind = 0;
-            float v0 = 1.f, v1 = 0.f;
-            if (inr) {
-              // Both words in flight at once.  word1 is written once per call, before word0's
-              // AGG, so a current-epoch AGG word0 paired with a current-epoch word1 is a
-              // consistent (mul, add) pair; a stale word1 just means "not yet".
-              const uint64_t w0 = atomic_ld(st + 2 * (tile_base + jj));
-              const uint64_t w1 = atomic_ld(st + 2 * (tile_base + jj) + 1);
-              const uint32_t tag0 = (uint32_t)(w0 >> 32);
-              v0 = __uint_as_float((uint32_t)w0);
-              if ((tag0 >> 2) == epoch) kind = tag0 & 3u;
-              if (kind == kAgg) {
-                if ((uint32_t)(w1 >> 32) == tag_agg) v1 = __uint_as_float((uint32_t)w1);
-                else kind = 0;
-              }
-            }
-            const uint64_t inc_mask = __ballot(kind == kInc);
-            const uint64_t bad_mask = __ballot(kind == 0);
-            const int first_inc = inc_mask ? __ffsll((long long)inc_mask) - 1 : kWave;
-            const int first_bad = bad_mask ? __ffsll((long long)bad_mask) - 1 : kWave;
-            if (first_inc < first_bad) {
-              float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v0), first_inc));
-              for (int l = first_inc - 1; l >= 0; --l) {
-                const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v0), l));
-                const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v1), l));
-                x = fmaf(a, x, b);
-              }
-              c = x;
-              break;
-            }
-            if (++spins > kSpinLimit) {
-              if (lane == 0) atomic_st(ws + 3, (uint64_t)1);
-              c = 0.f;
-              break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-          }
-          if (lane == 0 && tm.mul != 0.f)
-            atomic_st(st + 2 * (tile_base + k), pack(tag_inc, fmaf(tm.mul, c, tm.add)));
-        }
-        if (lane == 0) s_carry = c;
+    if (wave == 0) {
+      Affine tm{1.f, 0.f};
+      if constexpr (FWD) {
+        for (int v = 0; v < NW; ++v) tm = compose(Affine{s_mul[v], s_add[v]}, tm);
+      } else {
+        for (int v = NW - 1; v >= 0; --v) tm = compose(Affine{s_mul[v], s_add[v]}, tm);
       }
-      __syncthreads();
-      tile_carry = s_carry;
-    } else {
-      tile_carry = active ? op.row_carry(row, T) : 0.f;
+      const float c = tile_carry<Op, FWD>(op, tm, row, k, T, tiles_per_row, epoch, ws, lane);
+      if (lane == 0) {
+        s_carry = c;
+        s_q[0] = qnn;
+      }
     }
-    // compose the waves between the row tile's carry source and this wave
-    const int wpr = L / kWave;                 // waves per row tile (L >= 64 here)
-    const int first = (wave / wpr) * wpr, last = first + wpr - 1;
-    carry = tile_carry;
+    __syncthreads();
+    float carry = s_carry;
     if constexpr (FWD) {
-      for (int v = first; v < wave; ++v) carry = fmaf(s_mul[v], carry, s_add[v]);
+      for (int v = 0; v < wave; ++v) carry = fmaf(s_mul[v], carry, s_add[v]);
     } else {
-      for (int v = last; v > wave; --v) carry = fmaf(s_mul[v], carry, s_add[v]);
+      for (int v = NW - 1; v > wave; --v) carry = fmaf(s_mul[v], carry, s_add[v]);
     }
-  } else {
-    carry = active ? op.row_carry(row, T) : 0.f;
-  }
+    const uint64_t q_after = s_q[0];
+    const float x_in = lane_input<FWD>(m, carry, lane, kWave);
+    float xs[S];
+    replay<FWD, S>(mul, add, x_in, xs);
+    op.template emit<S, VEC>(cur, h, xs, x_in, row, t0, T);
+    __syncthreads();  // LDS is rewritten by the next tile
 
-  // 6. this segment's incoming value: the neighbour lane's outgoing value
-  const float y = fmaf(m.mul, carry, m.add);
-  float x_in;
-  const int gl = lane & (W - 1);
-  if constexpr (FWD) {
-    x_in = __shfl_up(y, 1, kWave);
-    if (gl == 0) x_in = carry;
-  } else {
-    x_in = __shfl_down(y, 1, kWave);
-    if (gl == W - 1) x_in = carry;
+    q = qn;
+    qn = has_next ? q_after : ~(uint64_t)0;
+    cur = nxt;
+    ecur = enxt;
+    row = nrow;
+    k = nk;
   }
-
-  // 7. replay the segment and write outputs
-  float xs[S];
-  float x = x_in;
-  if constexpr (FWD) {
-#pragma unroll
-    for (int i = 0; i < S; ++i) xs[i] = x = fmaf(mul[i], x, add[i]);
-  } else {
-#pragma unroll
-    for (int i = S - 1; i >= 0; --i) xs[i] = x = fmaf(mul[i], x, add[i]);
-  }
-  if (active) op.template emit<S, VEC>(R, h, xs, x_in, row, t0, T);
-
-  if constexpr (LOOKBACK) {
-    if (tid == 0) lookback_finish(ws, sc, wgs_per_slot, nslots, epoch);
-  }
+  if (tid == 0) lookback_finish(ws, sc, wgs_per_slot, nslots, epoch);
 }
 
 }  // namespace rlk
