@@ -27,6 +27,9 @@ FLAGS = [
     f"--offload-arch={ARCH}",
     # no packed-FP32 (v_pk_*_f32) code generation
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # every atomic here is issued by one lane; the wave-aggregating rewrite would consume
+    # the ticket right after issuing it and stall the coordinator on it
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wall", "-Wno-unused-result",
 ]
 

@@ -14,17 +14,18 @@ namespace {
 
 // Launch geometry.  The macros only exist so that tuning sweeps can rebuild the library
 // with other values; the defaults are the shipped configuration.
-#ifndef RLK_LB_NT
-#define RLK_LB_NT 512
+#ifndef RLK_LB_NTD
+#define RLK_LB_NTD 512
 #endif
 #ifndef RLK_LB_S
 #define RLK_LB_S 8
 #endif
-constexpr int kNT = 256;          // short rows: threads per workgroup (4 wavefronts)
-constexpr int kShortMaxT = 2048;  // rows up to this length are kept whole in one workgroup
-constexpr int kLbNT = RLK_LB_NT;  // look-back path: threads per workgroup
-constexpr int kTileS = RLK_LB_S;  // look-back path: steps per thread
-constexpr int kTile = kLbNT * kTileS;
+constexpr int kNT = 256;             // short rows: threads per workgroup (4 wavefronts)
+constexpr int kShortMaxT = 2048;     // rows up to this length are kept whole in one workgroup
+constexpr int kLbNTD = RLK_LB_NTD;   // look-back path: data threads per workgroup
+constexpr int kLbBlock = kLbNTD + kWave;  // ... plus the coordinator wave
+constexpr int kTileS = RLK_LB_S;     // look-back path: steps per data thread
+constexpr int kTile = kLbNTD * kTileS;
 
 struct Plan {
   bool lookback;
@@ -55,7 +56,7 @@ Plan make_plan(int64_t E, int64_t T) {
   } else {
     p.lookback = true;
     p.S = kTileS;
-    p.log2L = ceil_log2(kLbNT);
+    p.log2L = 0;
     p.tiles_per_row = (int)((T + kTile - 1) / kTile);
     p.grid = E * p.tiles_per_row;  // upper bound; the persistent grid is smaller
   }
@@ -98,15 +99,15 @@ hipError_t launch_rows(const Op& op, int64_t E, int T, int log2L, int64_t grid, 
 
 template <class Op, bool VEC>
 hipError_t launch_lookback(const Op& op, int64_t E, int T, int tpr, uint64_t* ws, hipStream_t stream) {
-  const void* kernel = reinterpret_cast<const void*>(&lookback_kernel<Op, kLbNT, kTileS, VEC>);
+  const void* kernel = reinterpret_cast<const void*>(&lookback_kernel<Op, kLbNTD, kTileS, VEC>);
   const int64_t nslots = lookback_slots(E);
   const int64_t tiles_per_slot = ((E + nslots - 1) / nslots) * (int64_t)tpr;
-  int64_t wgs = resident_workgroups(kernel, kLbNT) / nslots;
+  int64_t wgs = resident_workgroups(kernel, kLbBlock) / nslots;
   if (wgs < 1) wgs = 1;
   if (wgs > tiles_per_slot) wgs = tiles_per_slot;
   const int64_t grid = nslots * wgs;
   void* args[] = {const_cast<Op*>(&op), &E, &T, &tpr, &ws};
-  return hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(kLbNT), args, 0, stream);
+  return hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(kLbBlock), args, 0, stream);
 }
 
 template <class Op>
@@ -175,11 +176,17 @@ int rlk_gae(const float* rewards, const float* values, const float* terminateds,
   if (is_empty(num_envs, seq_len)) return RLK_OK;
   if (!rewards || !values || !terminateds || !advantages || !valid_boot(bootstrap, boot_mode))
     return RLK_ERR_INVALID_ARGUMENT;
-  GaeOp op{rewards, values, terminateds, truncateds, boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap,
-           advantages, boot_mode, gamma, gamma * lambda_};
+  const float* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
   const bool vec = seq_len % 4 == 0 && aligned16(rewards) && aligned16(values) &&
                    aligned16(terminateds) && aligned16(truncateds) && aligned16(advantages) &&
                    (boot_mode != RLK_BOOT_FULL || aligned16(bootstrap));
+  if (truncateds) {
+    GaeOp<true> op{rewards, values, terminateds, truncateds, boot, advantages, boot_mode, gamma,
+                   gamma * lambda_};
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  }
+  GaeOp<false> op{rewards, values, terminateds, nullptr, boot, advantages, boot_mode, gamma,
+                  gamma * lambda_};
   return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
 }
 
@@ -192,13 +199,18 @@ int rlk_vtrace(const float* log_pi_target, const float* log_pi_behavior, const f
   if (!log_pi_target || !log_pi_behavior || !values || !rewards || !terminateds || !targets ||
       !advantages || !valid_boot(bootstrap, boot_mode))
     return RLK_ERR_INVALID_ARGUMENT;
-  VtraceOp op{log_pi_target, log_pi_behavior, values, rewards, terminateds, truncateds,
-              boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap, targets, advantages, boot_mode,
-              gamma, rho_bar, c_bar};
+  const float* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
   const bool vec = seq_len % 4 == 0 && aligned16(log_pi_target) && aligned16(log_pi_behavior) &&
                    aligned16(values) && aligned16(rewards) && aligned16(terminateds) &&
                    aligned16(truncateds) && aligned16(targets) && aligned16(advantages) &&
                    (boot_mode != RLK_BOOT_FULL || aligned16(bootstrap));
+  if (truncateds) {
+    VtraceOp<true> op{log_pi_target, log_pi_behavior, values, rewards, terminateds, truncateds,
+                      boot, targets, advantages, boot_mode, gamma, rho_bar, c_bar};
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  }
+  VtraceOp<false> op{log_pi_target, log_pi_behavior, values, rewards, terminateds, nullptr,
+                     boot, targets, advantages, boot_mode, gamma, rho_bar, c_bar};
   return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
 }
 
@@ -219,18 +231,23 @@ int rlk_retrace(const float* action_probs_target, const float* action_probs_beha
                    aligned16(terminateds) && aligned16(truncateds) && aligned16(targets) &&
                    aligned16(advantages);
   const int A = (int)num_actions;
-#define RLK_RETRACE(NA)                                                                         \
-  {                                                                                             \
-    RetraceOp<NA> op{action_probs_target, action_probs_behavior, q_values, next_q_values_all,    \
-                     actions, rewards, terminateds, truncateds, targets, advantages, A, gamma,  \
-                     lambda_, c_bar, rho_bar};                                                  \
-    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);              \
+#define RLK_RETRACE(NA)                                                                          \
+  {                                                                                              \
+    if (truncateds) {                                                                            \
+      RetraceOp<NA, true> op{action_probs_target, action_probs_behavior, q_values,               \
+                             next_q_values_all, actions, rewards, terminateds, truncateds,       \
+                             targets, advantages, A, gamma, lambda_, c_bar, rho_bar};            \
+      return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);             \
+    }                                                                                            \
+    RetraceOp<NA, false> op{action_probs_target, action_probs_behavior, q_values,                \
+                            next_q_values_all, actions, rewards, terminateds, nullptr, targets,  \
+                            advantages, A, gamma, lambda_, c_bar, rho_bar};                      \
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);               \
   }
   switch (A) {
     case 1: RLK_RETRACE(1)
     case 2: RLK_RETRACE(2)
     case 4: RLK_RETRACE(4)
-    case 8: RLK_RETRACE(8)
     default: RLK_RETRACE(0)
   }
 #undef RLK_RETRACE
@@ -243,12 +260,17 @@ int rlk_lambda_returns(const float* rewards, const float* next_values, const flo
   if (is_empty(num_envs, seq_len)) return RLK_OK;
   if (!rewards || !next_values || !terminateds || !returns || !valid_boot(bootstrap, boot_mode))
     return RLK_ERR_INVALID_ARGUMENT;
-  ReturnsOp op{rewards, next_values, terminateds, truncateds,
-               boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap, returns, boot_mode, gamma,
-               gamma * (1.f - lambda_), gamma * lambda_};
+  const float* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
   const bool vec = seq_len % 4 == 0 && aligned16(rewards) && aligned16(next_values) &&
                    aligned16(terminateds) && aligned16(truncateds) && aligned16(returns) &&
                    (boot_mode != RLK_BOOT_FULL || aligned16(bootstrap));
+  if (truncateds) {
+    ReturnsOp<true, true> op{rewards, next_values, terminateds, truncateds, boot, returns,
+                             boot_mode, gamma, gamma * (1.f - lambda_), gamma * lambda_};
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  }
+  ReturnsOp<true, false> op{rewards, next_values, terminateds, nullptr, boot, returns, boot_mode,
+                            gamma, gamma * (1.f - lambda_), gamma * lambda_};
   return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
 }
 
@@ -259,12 +281,17 @@ int rlk_discounted_returns(const float* rewards, const float* terminateds,
   if (is_empty(num_envs, seq_len)) return RLK_OK;
   if (!rewards || !terminateds || !returns || !valid_boot(bootstrap, boot_mode))
     return RLK_ERR_INVALID_ARGUMENT;
-  ReturnsOp op{rewards, nullptr, terminateds, truncateds,
-               boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap, returns, boot_mode, gamma, 0.f,
-               gamma};
+  const float* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
   const bool vec = seq_len % 4 == 0 && aligned16(rewards) && aligned16(terminateds) &&
                    aligned16(truncateds) && aligned16(returns) &&
                    (boot_mode != RLK_BOOT_FULL || aligned16(bootstrap));
+  if (truncateds) {
+    ReturnsOp<false, true> op{rewards, nullptr, terminateds, truncateds, boot, returns, boot_mode,
+                              gamma, 0.f, gamma};
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  }
+  ReturnsOp<false, false> op{rewards, nullptr, terminateds, nullptr, boot, returns, boot_mode,
+                             gamma, 0.f, gamma};
   return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
 }
 

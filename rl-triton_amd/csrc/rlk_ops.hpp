@@ -5,6 +5,11 @@
 // values into the estimator's outputs.  Semantics follow the reference's fused Triton
 // kernels (simonsays1980/rl-triton v0.1.3, src/rl_triton/kernels/*.py); each struct
 // cites the lines it reproduces.  Padding steps (t >= T) are the identity map.
+//
+// Optional operands that change which arrays are read (truncations, TD(lambda)'s next
+// values) are template parameters, and every load is unconditional (load_seg clamps into
+// the row; absent per-row values are read from g_zero): the look-back kernel's data
+// waves keep a prefetch in flight only if no load sits under a runtime branch.
 #pragma once
 #include "rlk_engine.hpp"
 
@@ -22,13 +27,14 @@ __device__ __forceinline__ void fill_regs(float (&v)[S], float x) {
 //   add = r + gamma*v_next*(1-term) - v,   mul = gamma*lambda*(1 - done)
 //   done = min(term + trunc, 1) with truncations, term without;   x[T] = 0
 // ------------------------------------------------------------------------------------------
+template <bool TRUNC>
 struct GaeOp {
   static constexpr bool kForward = false;
   using Halo = float;  // values[t+1]
   const float* r;
   const float* v;
   const float* term;
-  const float* trunc;  // nullable
+  const float* trunc;  // read iff TRUNC
   const float* boot;   // nullable, per boot_mode
   float* out;
   int boot_mode;
@@ -37,48 +43,48 @@ struct GaeOp {
   template <int S>
   struct Regs {
     float r[S], v[S], te[S], tr[S], bt[S];
+    float blast;
   };
 
   template <int S, bool VEC>
   __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
     const int64_t o = row * (int64_t)T;
-    load_seg<S, VEC>(r + o, t0, T, R.r, 0.f);
-    load_seg<S, VEC>(v + o, t0, T, R.v, 0.f);
-    load_seg<S, VEC>(term + o, t0, T, R.te, 1.f);
-    if (trunc) load_seg<S, VEC>(trunc + o, t0, T, R.tr, 0.f);
+    load_seg<S, VEC>(r + o, t0, T, R.r);
+    load_seg<S, VEC>(v + o, t0, T, R.v);
+    load_seg<S, VEC>(term + o, t0, T, R.te);
+    if constexpr (TRUNC) load_seg<S, VEC>(trunc + o, t0, T, R.tr);
     else fill_regs(R.tr, 0.f);
-    load_boot<S, VEC>(boot, boot_mode, row, t0, T, R.bt, trunc != nullptr);
+    boot_load<S, VEC, TRUNC>(boot, boot_mode, row, t0, T, R.bt, R.blast, r + o);
   }
-  template <int S>
-  __device__ void clear(Regs<S>& R) const {
-    fill_regs(R.r, 0.f), fill_regs(R.v, 0.f), fill_regs(R.te, 1.f), fill_regs(R.tr, 0.f),
-        fill_regs(R.bt, 0.f);
+  template <int S, bool VEC>
+  __device__ void prepare(Regs<S>& R, int64_t, int t0, int T) const {
+    boot_prepare<S, TRUNC>(boot_mode, t0, T, R.bt, R.blast);
   }
   template <int S>
   __device__ float export_first(const Regs<S>& R) const { return R.v[0]; }
   __device__ float halo_load(int64_t row, int t, int T) const { return v[row * (int64_t)T + t]; }
 
   template <int S>
-  __device__ void coef(const Regs<S>& R, float vh, int64_t row, int t0, int T, float (&mul)[S],
+  __device__ void coef(const Regs<S>& R, float vh, int64_t, int t0, int T, float (&mul)[S],
                        float (&add)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
       const float raw = (i + 1 < S) ? R.v[i + 1] : vh;
       const float vn = (t == T - 1 || R.tr[i] == 1.f) ? R.bt[i] : raw;
-      const float done = trunc ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
+      const float done = TRUNC ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
       const float a = fmaf(gamma * vn, 1.f - R.te[i], R.r[i]) - R.v[i];
       const bool in = t < T;  // padding steps are the identity map
       add[i] = in ? a : 0.f;
       mul[i] = in ? gl * (1.f - done) : 1.f;
     }
   }
-  __device__ float row_carry(int64_t, int) const { return 0.f; }
+  __device__ const float* row_carry_src(int64_t, int) const { return nullptr; }
 
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>&, float, const float (&xs)[S], float, int64_t row, int t0,
-                       int T) const {
-    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
+                       int T, float* sink) const {
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, sink);
   }
 };
 
@@ -93,6 +99,7 @@ struct GaeOp {
 // The reference passes targets[t+1] through global memory (store, barrier, reload,
 // vtrace_fused.py:149-152); here it is the neighbouring register or lane.
 // ------------------------------------------------------------------------------------------
+template <bool TRUNC>
 struct VtraceOp {
   static constexpr bool kForward = false;
   using Halo = float;  // values[t+1]
@@ -101,7 +108,7 @@ struct VtraceOp {
   const float* v;
   const float* r;
   const float* term;
-  const float* trunc;  // nullable
+  const float* trunc;  // read iff TRUNC
   const float* boot;   // nullable, per boot_mode
   float* targets;
   float* adv;
@@ -110,32 +117,31 @@ struct VtraceOp {
 
   template <int S>
   struct Regs {
-    float rho[S], c[S], v[S], r[S], te[S], tr[S], bt[S];
+    float rho[S], c[S], v[S], r[S], te[S], tr[S], bt[S];  // rho, c: log-probs until prepare()
+    float blast;
   };
 
   template <int S, bool VEC>
   __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
     const int64_t o = row * (int64_t)T;
-    float a[S], b[S];
-    load_seg<S, VEC>(lpt + o, t0, T, a, 0.f);
-    load_seg<S, VEC>(lpb + o, t0, T, b, 0.f);
+    load_seg<S, VEC>(lpt + o, t0, T, R.rho);
+    load_seg<S, VEC>(lpb + o, t0, T, R.c);
+    load_seg<S, VEC>(v + o, t0, T, R.v);
+    load_seg<S, VEC>(r + o, t0, T, R.r);
+    load_seg<S, VEC>(term + o, t0, T, R.te);
+    if constexpr (TRUNC) load_seg<S, VEC>(trunc + o, t0, T, R.tr);
+    else fill_regs(R.tr, 0.f);
+    boot_load<S, VEC, TRUNC>(boot, boot_mode, row, t0, T, R.bt, R.blast, r + o);
+  }
+  template <int S, bool VEC>
+  __device__ void prepare(Regs<S>& R, int64_t, int t0, int T) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
-      const float ratio = expf(a[i] - b[i]);
+      const float ratio = expf(R.rho[i] - R.c[i]);
       R.rho[i] = fminf(ratio, rho_bar);
       R.c[i] = fminf(ratio, c_bar);
     }
-    load_seg<S, VEC>(v + o, t0, T, R.v, 0.f);
-    load_seg<S, VEC>(r + o, t0, T, R.r, 0.f);
-    load_seg<S, VEC>(term + o, t0, T, R.te, 1.f);
-    if (trunc) load_seg<S, VEC>(trunc + o, t0, T, R.tr, 0.f);
-    else fill_regs(R.tr, 0.f);
-    load_boot<S, VEC>(boot, boot_mode, row, t0, T, R.bt, trunc != nullptr);
-  }
-  template <int S>
-  __device__ void clear(Regs<S>& R) const {
-    fill_regs(R.rho, 0.f), fill_regs(R.c, 0.f), fill_regs(R.v, 0.f), fill_regs(R.r, 0.f),
-        fill_regs(R.te, 1.f), fill_regs(R.tr, 0.f), fill_regs(R.bt, 0.f);
+    boot_prepare<S, TRUNC>(boot_mode, t0, T, R.bt, R.blast);
   }
   template <int S>
   __device__ float export_first(const Regs<S>& R) const { return R.v[0]; }
@@ -143,7 +149,7 @@ struct VtraceOp {
 
   // continuation value at step t from the raw next-step value (values or targets)
   __device__ __forceinline__ float next_value(float raw, float tr, float bt, int t, int T) const {
-    if (trunc) return ((t < T - 1 && tr == 0.f) ? raw : 0.f) + bt;
+    if constexpr (TRUNC) return ((t < T - 1 && tr == 0.f) ? raw : 0.f) + bt;
     return (t == T - 1) ? bt : raw;
   }
 
@@ -154,18 +160,18 @@ struct VtraceOp {
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
       const float vn = next_value((i + 1 < S) ? R.v[i + 1] : vh, R.tr[i], R.bt[i], t, T);
-      const float done = trunc ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
+      const float done = TRUNC ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
       const float a = R.rho[i] * (fmaf(gamma * vn, 1.f - R.te[i], R.r[i]) - R.v[i]);
       const bool in = t < T;
       add[i] = in ? a : 0.f;
       mul[i] = in ? gamma * R.c[i] * (1.f - done) : 1.f;
     }
   }
-  __device__ float row_carry(int64_t, int) const { return 0.f; }
+  __device__ const float* row_carry_src(int64_t, int) const { return nullptr; }
 
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>& R, float vh, const float (&xs)[S], float x_next, int64_t row,
-                       int t0, int T) const {
+                       int t0, int T, float* sink) const {
     float tg[S], ad[S];
 #pragma unroll
     for (int i = 0; i < S; ++i) tg[i] = xs[i] + R.v[i];
@@ -176,8 +182,8 @@ struct VtraceOp {
       ad[i] = R.rho[i] * (fmaf(gamma * nt, 1.f - R.te[i], R.r[i]) - R.v[i]);
     }
     const int64_t o = row * (int64_t)T;
-    store_seg<S, VEC>(targets + o, t0, T, tg);
-    store_seg<S, VEC>(adv + o, t0, T, ad);
+    store_seg<S, VEC>(targets + o, t0, T, tg, sink);
+    store_seg<S, VEC>(adv + o, t0, T, ad, sink);
   }
 };
 
@@ -189,7 +195,7 @@ struct VtraceOp {
 //   Q_ret = x + q;  advantages = rho*(r + gamma*Q_ret[t+1]*(1-term) - q),  Q_ret[T] = 0
 // NA > 0: compile-time action count (vector loads of the [S, A] block); NA == 0: runtime A.
 // ------------------------------------------------------------------------------------------
-template <int NA>
+template <int NA, bool TRUNC>
 struct RetraceOp {
   static constexpr bool kForward = false;
   using Halo = Halo2;  // {c[t+1], q[t+1]}
@@ -200,7 +206,7 @@ struct RetraceOp {
   const int64_t* act;  // [E, T]
   const float* r;
   const float* term;
-  const float* trunc;  // nullable
+  const float* trunc;  // read iff TRUNC
   float* targets;
   float* adv;
   int A;
@@ -227,35 +233,36 @@ struct RetraceOp {
     enq = e;
   }
 
+  // Unlike the other ops, the [S, A] action blocks are reduced to (rho, c, E_pi[Q']) here,
+  // at load time, to bound the registers a prefetched tile holds; a Retrace prefetch is
+  // therefore waited for early.
   template <int S, bool VEC>
   __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
     const int64_t o = row * (int64_t)T;
     float m[S];
-    load_seg<S, VEC>(q + o, t0, T, R.q, 0.f);
-    load_seg<S, VEC>(r + o, t0, T, R.r, 0.f);
-    load_seg<S, VEC>(term + o, t0, T, R.te, 1.f);
-    if (trunc) load_seg<S, VEC>(trunc + o, t0, T, R.tr, 0.f);
+    load_seg<S, VEC>(q + o, t0, T, R.q);
+    load_seg<S, VEC>(r + o, t0, T, R.r);
+    load_seg<S, VEC>(term + o, t0, T, R.te);
+    if constexpr (TRUNC) load_seg<S, VEC>(trunc + o, t0, T, R.tr);
     else fill_regs(R.tr, 0.f);
-    load_seg<S, VEC>(mu + o, t0, T, m, 1.f);
+    load_seg<S, VEC>(mu + o, t0, T, m);
     int64_t at[S];
 #pragma unroll
-    for (int i = 0; i < S; ++i) at[i] = (t0 + i < T) ? act[o + t0 + i] : 0;
-    if constexpr (NA > 0 && VEC && (S * NA) % 4 == 0) {
-      // the [S, NA] blocks are contiguous and 16-byte aligned
+    for (int i = 0; i < S; ++i) at[i] = act[o + clamp_step(t0 + i, T)];
+    if constexpr (NA > 0 && VEC && (S * NA) % 4 == 0 && S * NA <= 16) {
+      // the [S, NA] blocks are contiguous and 16-byte aligned; a quad beyond T reads the
+      // row's first quad instead.  (Larger blocks take the per-step path below: two tiles
+      // of them would not fit the register file.)
       float pb[S * NA], nb[S * NA];
       const float* pp = pi + (o + t0) * NA;
       const float* np = nq + (o + t0) * NA;
 #pragma unroll
       for (int qd = 0; qd < S * NA / 4; ++qd) {
-        if (t0 + (4 * qd) / NA < T) {
-          const float4 a4 = *reinterpret_cast<const float4*>(pp + 4 * qd);
-          const float4 b4 = *reinterpret_cast<const float4*>(np + 4 * qd);
-          pb[4 * qd] = a4.x, pb[4 * qd + 1] = a4.y, pb[4 * qd + 2] = a4.z, pb[4 * qd + 3] = a4.w;
-          nb[4 * qd] = b4.x, nb[4 * qd + 1] = b4.y, nb[4 * qd + 2] = b4.z, nb[4 * qd + 3] = b4.w;
-        } else {
-          pb[4 * qd] = pb[4 * qd + 1] = pb[4 * qd + 2] = pb[4 * qd + 3] = 0.f;
-          nb[4 * qd] = nb[4 * qd + 1] = nb[4 * qd + 2] = nb[4 * qd + 3] = 0.f;
-        }
+        const bool in = t0 + (4 * qd) / NA < T;
+        const float4 a4 = *reinterpret_cast<const float4*>(in ? pp + 4 * qd : pi + o * NA);
+        const float4 b4 = *reinterpret_cast<const float4*>(in ? np + 4 * qd : nq + o * NA);
+        pb[4 * qd] = a4.x, pb[4 * qd + 1] = a4.y, pb[4 * qd + 2] = a4.z, pb[4 * qd + 3] = a4.w;
+        nb[4 * qd] = b4.x, nb[4 * qd + 1] = b4.y, nb[4 * qd + 2] = b4.z, nb[4 * qd + 3] = b4.w;
       }
 #pragma unroll
       for (int i = 0; i < S; ++i) step_terms(pb + i * NA, nb + i * NA, at[i], m[i], R.rho[i], R.c[i], R.enq[i]);
@@ -263,20 +270,13 @@ struct RetraceOp {
       const int na = NA > 0 ? NA : A;
 #pragma unroll
       for (int i = 0; i < S; ++i) {
-        if (t0 + i < T) {
-          const int64_t base = (o + t0 + i) * na;
-          step_terms(pi + base, nq + base, at[i], m[i], R.rho[i], R.c[i], R.enq[i]);
-        } else {
-          R.rho[i] = 0.f, R.c[i] = 0.f, R.enq[i] = 0.f;
-        }
+        const int64_t base = (o + clamp_step(t0 + i, T)) * na;
+        step_terms(pi + base, nq + base, at[i], m[i], R.rho[i], R.c[i], R.enq[i]);
       }
     }
   }
-  template <int S>
-  __device__ void clear(Regs<S>& R) const {
-    fill_regs(R.q, 0.f), fill_regs(R.r, 0.f), fill_regs(R.te, 1.f), fill_regs(R.tr, 0.f),
-        fill_regs(R.rho, 0.f), fill_regs(R.c, 0.f), fill_regs(R.enq, 0.f);
-  }
+  template <int S, bool VEC>
+  __device__ void prepare(Regs<S>&, int64_t, int, int) const {}
   template <int S>
   __device__ Halo2 export_first(const Regs<S>& R) const { return Halo2{R.c[0], R.q[0]}; }
   __device__ Halo2 halo_load(int64_t row, int t, int T) const {
@@ -301,11 +301,11 @@ struct RetraceOp {
       mul[i] = in ? gamma * c_next * (1.f - done) : 1.f;
     }
   }
-  __device__ float row_carry(int64_t, int) const { return 0.f; }
+  __device__ const float* row_carry_src(int64_t, int) const { return nullptr; }
 
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>& R, Halo2 h, const float (&xs)[S], float x_next, int64_t row,
-                       int t0, int T) const {
+                       int t0, int T, float* sink) const {
     float tg[S], ad[S];
 #pragma unroll
     for (int i = 0; i < S; ++i) tg[i] = xs[i] + R.q[i];
@@ -316,8 +316,8 @@ struct RetraceOp {
       ad[i] = R.rho[i] * (fmaf(gamma * nxt, 1.f - R.te[i], R.r[i]) - R.q[i]);
     }
     const int64_t o = row * (int64_t)T;
-    store_seg<S, VEC>(targets + o, t0, T, tg);
-    store_seg<S, VEC>(adv + o, t0, T, ad);
+    store_seg<S, VEC>(targets + o, t0, T, tg, sink);
+    store_seg<S, VEC>(adv + o, t0, T, ad, sink);
   }
 };
 
@@ -326,15 +326,16 @@ struct RetraceOp {
 //   nd = 1 - done;  add = r + gamma*(1-lambda)*nd*nv + gamma*trunc*boot(t);  mul = gamma*lambda*nd
 //   x[T] = boot(T-1)
 // Discounted returns: kernels/discounted_returns_fused.py:139-171 -- the same with
-//   add = r + gamma*trunc*boot(t),  mul = gamma*nd  (nv unused, flagged by nv == nullptr).
+//   add = r + gamma*trunc*boot(t),  mul = gamma*nd  (NV = false: no next values).
 // ------------------------------------------------------------------------------------------
+template <bool NV, bool TRUNC>
 struct ReturnsOp {
   static constexpr bool kForward = false;
   using Halo = NoHalo;
   const float* r;
-  const float* nv;     // nullptr: discounted returns
+  const float* nv;     // read iff NV
   const float* term;
-  const float* trunc;  // nullable
+  const float* trunc;  // read iff TRUNC
   const float* boot;   // nullable, per boot_mode
   float* out;
   int boot_mode;
@@ -343,26 +344,27 @@ struct ReturnsOp {
   template <int S>
   struct Regs {
     float r[S], nv[S], te[S], tr[S], bt[S];
+    float blast;
   };
 
   template <int S, bool VEC>
   __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
     const int64_t o = row * (int64_t)T;
-    load_seg<S, VEC>(r + o, t0, T, R.r, 0.f);
-    if (nv) load_seg<S, VEC>(nv + o, t0, T, R.nv, 0.f);
+    load_seg<S, VEC>(r + o, t0, T, R.r);
+    if constexpr (NV) load_seg<S, VEC>(nv + o, t0, T, R.nv);
     else fill_regs(R.nv, 0.f);
-    load_seg<S, VEC>(term + o, t0, T, R.te, 1.f);
-    if (trunc) {
-      load_seg<S, VEC>(trunc + o, t0, T, R.tr, 0.f);
-      load_boot<S, VEC>(boot, boot_mode, row, t0, T, R.bt, trunc != nullptr);
+    load_seg<S, VEC>(term + o, t0, T, R.te);
+    if constexpr (TRUNC) {
+      load_seg<S, VEC>(trunc + o, t0, T, R.tr);
+      boot_load<S, VEC, true>(boot, boot_mode, row, t0, T, R.bt, R.blast, r + o);
     } else {
       fill_regs(R.tr, 0.f), fill_regs(R.bt, 0.f);
+      R.blast = 0.f;
     }
   }
-  template <int S>
-  __device__ void clear(Regs<S>& R) const {
-    fill_regs(R.r, 0.f), fill_regs(R.nv, 0.f), fill_regs(R.te, 1.f), fill_regs(R.tr, 0.f),
-        fill_regs(R.bt, 0.f);
+  template <int S, bool VEC>
+  __device__ void prepare(Regs<S>& R, int64_t, int t0, int T) const {
+    if constexpr (TRUNC) boot_prepare<S, true>(boot_mode, t0, T, R.bt, R.blast);
   }
 
   template <int S>
@@ -371,20 +373,22 @@ struct ReturnsOp {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
-      const float nd = 1.f - (trunc ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i]);
-      float a = nv ? fmaf(g1l * nd, R.nv[i], R.r[i]) : R.r[i];
-      if (trunc) a = fmaf(gamma * R.tr[i], R.bt[i], a);
+      const float nd = 1.f - (TRUNC ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i]);
+      float a = NV ? fmaf(g1l * nd, R.nv[i], R.r[i]) : R.r[i];
+      if constexpr (TRUNC) a = fmaf(gamma * R.tr[i], R.bt[i], a);
       const bool in = t < T;
       add[i] = in ? a : 0.f;
       mul[i] = in ? gl * nd : 1.f;
     }
   }
-  __device__ float row_carry(int64_t row, int T) const { return boot_at(boot, boot_mode, row, T - 1, T); }
+  __device__ const float* row_carry_src(int64_t row, int T) const {
+    return boot_mode == kBootNone ? nullptr : boot_last(boot, boot_mode, row, T);
+  }
 
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>&, NoHalo, const float (&xs)[S], float, int64_t row, int t0,
-                       int T) const {
-    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
+                       int T, float* sink) const {
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, sink);
   }
 };
 
@@ -414,11 +418,11 @@ struct DoneGatedForwardOp {
   template <int S, bool VEC>
   __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
     const int64_t o = row * (int64_t)T;
-    load_seg<S, VEC>(x + o, t0, T, R.x, 0.f);
-    load_seg<S, VEC>(dones + o, t0, T, R.d, 0.f);
+    load_seg<S, VEC>(x + o, t0, T, R.x);
+    load_seg<S, VEC>(dones + o, t0, T, R.d);
   }
-  template <int S>
-  __device__ void clear(Regs<S>& R) const { fill_regs(R.x, 0.f), fill_regs(R.d, 0.f); }
+  template <int S, bool VEC>
+  __device__ void prepare(Regs<S>&, int64_t, int, int) const {}
   template <int S>
   __device__ float export_last(const Regs<S>& R) const { return R.d[S - 1]; }
   __device__ float halo_load(int64_t row, int t, int T) const { return dones[row * (int64_t)T + t]; }
@@ -437,12 +441,12 @@ struct DoneGatedForwardOp {
       add[i] = in ? R.x[i] : 0.f;
     }
   }
-  __device__ float row_carry(int64_t row, int) const { return seed ? seed[row] : 0.f; }
+  __device__ const float* row_carry_src(int64_t row, int) const { return seed ? seed + row : nullptr; }
 
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>&, float, const float (&xs)[S], float, int64_t row, int t0,
-                       int T) const {
-    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
+                       int T, float* sink) const {
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, sink);
   }
 };
 
@@ -466,11 +470,11 @@ struct AffineScanOp {
   template <int S, bool VEC>
   __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
     const int64_t o = row * (int64_t)T;
-    load_seg<S, VEC>(u + o, t0, T, R.u, 0.f);
-    load_seg<S, VEC>(v + o, t0, T, R.v, 1.f);
+    load_seg<S, VEC>(u + o, t0, T, R.u);
+    load_seg<S, VEC>(v + o, t0, T, R.v);
   }
-  template <int S>
-  __device__ void clear(Regs<S>& R) const { fill_regs(R.u, 0.f), fill_regs(R.v, 1.f); }
+  template <int S, bool VEC>
+  __device__ void prepare(Regs<S>&, int64_t, int, int) const {}
   template <int S>
   __device__ void coef(const Regs<S>& R, NoHalo, int64_t, int t0, int T, float (&mul)[S],
                        float (&add)[S]) const {
@@ -481,11 +485,11 @@ struct AffineScanOp {
       add[i] = in ? R.u[i] : 0.f;
     }
   }
-  __device__ float row_carry(int64_t row, int) const { return carry ? carry[row] : 0.f; }
+  __device__ const float* row_carry_src(int64_t row, int) const { return carry ? carry + row : nullptr; }
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>&, NoHalo, const float (&xs)[S], float, int64_t row, int t0,
-                       int T) const {
-    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
+                       int T, float* sink) const {
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, sink);
   }
 };
 
