@@ -63,7 +63,7 @@ const char *rlk_status_string(int status);
 size_t rlk_workspace_bytes(int64_t num_envs, int64_t seq_len);
 
 /* GAE advantages.  Replaces the gae_fused_kernel launch in compute_gae
- * (src/rl_triton/ops/gae.py:164-190; kernel src/rl_triton/kernels/gae.py:200-318), and
+ * (src/rl_triton/ops/gae.py:164-190; kernel src/rl_triton/kernels/gae.py:62-180), and
  * its chunked fallback for seq_len > 131072 (ops/gae.py:192-215).
  * truncateds may be NULL (done = terminateds). */
 int rlk_gae(const float *rewards, const float *values, const float *terminateds,

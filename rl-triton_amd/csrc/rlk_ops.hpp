@@ -22,7 +22,7 @@ __device__ __forceinline__ void fill_regs(float (&v)[S], float x) {
 }
 
 // ------------------------------------------------------------------------------------------
-// GAE: kernels/gae.py:259-318 (gae_fused_kernel), both HAS_TRUNCATIONS branches.
+// GAE: kernels/gae.py:121-180 (gae_fused_kernel), both HAS_TRUNCATIONS branches.
 //   v_next = boot(t)  if t == T-1 or trunc[t] == 1,  values[t+1] otherwise
 //   add = r + gamma*v_next*(1-term) - v,   mul = gamma*lambda*(1 - done)
 //   done = min(term + trunc, 1) with truncations, term without;   x[T] = 0
@@ -188,7 +188,7 @@ struct VtraceOp {
 };
 
 // ------------------------------------------------------------------------------------------
-// Retrace(lambda): kernels/retrace_fused.py:430-515 (retrace_fused_kernel).
+// Retrace(lambda): kernels/retrace_fused.py:116-201 (retrace_fused_kernel).
 //   E_pi[Q'] = sum_a pi[t,a]*nq[t,a];  pi_a = pi[t, a_t] (0 if a_t outside [0, A))
 //   rho = min(pi_a/mu, rho_bar),  c = lambda*min(pi_a/mu, c_bar)
 //   add = r + gamma*E_pi[Q']*(1-term) - q,  mul = gamma*c[t+1]*(1-done),  c[T] = 0
@@ -325,7 +325,7 @@ struct RetraceOp {
 // TD(lambda) returns: kernels/lambda_returns_fused.py:54-89.
 //   nd = 1 - done;  add = r + gamma*(1-lambda)*nd*nv + gamma*trunc*boot(t);  mul = gamma*lambda*nd
 //   x[T] = boot(T-1)
-// Discounted returns: kernels/discounted_returns_fused.py:139-171 -- the same with
+// Discounted returns: kernels/discounted_returns_fused.py:50-82 -- the same with
 //   add = r + gamma*trunc*boot(t),  mul = gamma*nd  (NV = false: no next values).
 // ------------------------------------------------------------------------------------------
 template <bool NV, bool TRUNC>
@@ -394,9 +394,9 @@ struct ReturnsOp {
 
 // ------------------------------------------------------------------------------------------
 // Forward scans gated on done.
-//   eligibility traces (kernels/eligibility_traces_fused.py:238-255):
+//   eligibility traces (kernels/eligibility_traces_fused.py:67-84):
 //       mul = gamma*lambda*(1 - done[t-1]), done[-1] = 0, add = g, x[-1] = seed
-//   episodic prefix sum (kernels/prefix_sum_fused.py:174-195):
+//   episodic prefix sum (kernels/prefix_sum_fused.py:63-84):
 //       ends_at:   mul = 1 - done[t-1];  starts_at: mul = 1 - done[t];  add = x, x[-1] = seed
 // (decay = gamma*lambda for traces, 1 for the prefix sum)
 // ------------------------------------------------------------------------------------------
