@@ -1,6 +1,6 @@
 """Benchmark of the rl_triton return-estimation path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--configs all|none|names]
 
 Workload (BASELINE.json configs[1] and configs[2], the configuration the metric is
 quoted on): one STEP is one compute_gae call on a GAE [4096, 128] batch (terminations
@@ -19,8 +19,12 @@ Printed JSON (one line, stdout):
                  bytes per launch measured by rocprofv3 counters (profiles/traffic_4096x128.json)
   graph_replay   the same steps replayed from a captured HIP graph (no host work per call)
   ops            per-op device time, Gelem/s, GB/s and %-of-peak for both kernels
+  configs        the same figures for every BASELINE configuration (C1-C5,
+                 tests/baseline_configs.py), each its own rotating input sets
   cpu_baseline   the reference's sequential torch loops (restated in
-                 oracle/torch_loops.py) on the host CPU, 1 thread, bounded sample
+                 oracle/torch_loops.py) on the host CPU, 1 thread, bounded sample; this
+                 CPU leg also checks the headline outputs against the float64 oracle
+                 (parity_max_abs_err)
 """
 from __future__ import annotations
 
@@ -32,7 +36,7 @@ import sys
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
-for _p in (os.path.join(ROOT, "rl-triton_amd"), ROOT):
+for _p in (os.path.join(ROOT, "rl-triton_amd"), ROOT, os.path.join(ROOT, "tests")):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
@@ -132,6 +136,44 @@ def time_ops(torch, rl, sets, iters, batch=100):
     return res
 
 
+def time_configs(torch, names, min_launches=200, batch=50):
+    """Average kernel duration of every BASELINE configuration's public-API call (one
+    kernel launch per call), from HIP events around batches of back-to-back launches queued
+    behind a GPU spin, over rotating input sets of more than 3 x 256 MB."""
+    import baseline_configs as bc
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    res = {}
+    for name in names:
+        op, n_env, n_t, bpe = bc.CONFIGS[name]
+        n_sets = min(64, max(2, -(-3 * MALL_BYTES // bc.set_bytes(name)) + 1))
+        sets = [bc.make(name, seed=100 + i, device=dev) for i in range(n_sets)]
+        for i in range(min(n_sets, 8)):
+            bc.call(name, *sets[i])
+        torch.cuda.synchronize()
+        total_ms, n = 0.0, 0
+        while n < min_launches:
+            torch.cuda._sleep(20_000_000)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for i in range(batch):
+                bc.call(name, *sets[(n + i) % n_sets])
+            b.record(stream)
+            torch.cuda.synchronize()
+            total_ms += a.elapsed_time(b)
+            n += batch
+        del sets
+        us = 1e3 * total_ms / n
+        gbs = n_env * n_t * bpe / (us * 1e-6) / 1e9
+        res[name] = {"op": op, "shape": [n_env, n_t], "device_us": round(us, 3),
+                     "gelem_s": round(n_env * n_t / (us * 1e-6) / 1e9, 2), "gb_s": round(gbs, 1),
+                     "pct_peak": round(100 * gbs / PEAK_GBS, 2), "bytes_per_elem": bpe,
+                     "target_pct": (100 * bc.TARGETS[name]) if name in bc.TARGETS else None}
+        log(f"[bench] {name}: {us:.2f} us/launch, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of 8 TB/s)")
+    torch.cuda.empty_cache()
+    return res
+
+
 def time_graph_steps(torch, rl, sets, steps):
     """Steps replayed from a captured HIP graph (the same API calls, captured once per input
     set): the device-bound throughput without per-call host work."""
@@ -194,6 +236,9 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--configs", default="all",
+                    help="comma-separated BASELINE configuration names to time beside the headline "
+                         "(tests/baseline_configs.py), 'all' or 'none'")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain elementwise copy (out = in * 1.0) of MIB MiB 20 times: "
                          "the known-size reference that scales rocprofv3 FETCH_SIZE/WRITE_SIZE")
@@ -225,12 +270,9 @@ def main(argv=None):
     sets = make_sets(torch, dev, n_sets)
     torch.cuda.synchronize()
 
+    # outputs of the seeded CPU-drawn set 0, checked against the float64 oracle in the CPU leg
     outs = (run_gae(rl_triton, sets[0][0]), run_vtrace(rl_triton, sets[0][1]))
-    torch.cuda.synchronize()
-    errs = parity(np, sets[0][2], outs)
-    log(f"[bench] parity vs float64 oracle (max abs err): {errs}")
-    if max(errs.values()) > 1e-4:
-        raise SystemExit(f"parity check failed: {errs}")
+    cpu_sets = sets[0][2]
 
     for i in range(a.warmup):
         s = sets[i % n_sets]
@@ -270,11 +312,27 @@ def main(argv=None):
     graph_ms = time_graph_steps(torch, rl_triton, sets, a.steps)
     log(f"[bench] graph-replayed step: {graph_ms * 1e3:.2f} us "
         f"({2 * E * T / (graph_ms * 1e-3) / 1e9:.1f} Gelem/s)")
+    del sets
+    torch.cuda.empty_cache()
 
-    cpu = None
+    cfg_names = []
+    if a.configs == "all":
+        import baseline_configs
+        cfg_names = list(baseline_configs.CONFIGS)
+    elif a.configs != "none":
+        cfg_names = a.configs.split(",")
+    configs = time_configs(torch, cfg_names) if cfg_names else None
+
+    # CPU leg: the float64 oracle checks set 0's outputs, then the reference's sequential
+    # loops are timed on the host
+    cpu, errs = None, None
     if not a.no_cpu_baseline:
+        errs = parity(np, cpu_sets, outs)
+        log(f"[bench] parity vs float64 oracle (max abs err): {errs}")
+        if max(errs.values()) > 1e-4:
+            raise SystemExit(f"parity check failed: {errs}")
         log(f"[bench] CPU baseline ({a.cpu_seconds:.0f} s sample) ...")
-        cpu = cpu_baseline(torch, sets[0][2], a.cpu_seconds)
+        cpu = cpu_baseline(torch, cpu_sets, a.cpu_seconds)
         log(f"[bench] CPU baseline: {cpu['value']:.4f} Gelem/s ({cpu['ms_per_step']:.1f} ms/step)")
 
     line = {
@@ -287,7 +345,7 @@ def main(argv=None):
                                f"{n_sets} HBM-resident sets",
                    "num_envs": E, "seq_len": T, "gamma": 0.99, "lambda": 0.95,
                    "rho_bar": 1.0, "c_bar": 1.0, "timing": "value: eager public-API calls, HIP events around the timed region"},
-        "roofline": roofline, "ops": ops,
+        "roofline": roofline, "ops": ops, "configs": configs,
         "graph_replay": {"ms_per_step": round(graph_ms, 6),
                          "gelem_s": round(2 * E * T / (graph_ms * 1e-3) / 1e9, 3)},
         "parity_max_abs_err": errs, "cpu_baseline": cpu,

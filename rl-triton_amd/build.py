@@ -1,11 +1,15 @@
-"""Build librl_triton_amd.so (the gfx950 HIP kernels + C ABI) in-tree.
+"""Build the two in-tree libraries of the rl_triton package.
 
-    python rl-triton_amd/build.py            # compile if sources are newer
+    python rl-triton_amd/build.py            # compile what is older than its sources
     python rl-triton_amd/build.py --force    # always compile
 
-The library lands next to the Python package (rl-triton_amd/rl_triton/) so the
-package loads it from its own directory; hipcc cross-compiles for gfx950 on a
-machine without a GPU.
+  librl_triton_amd.so   the gfx950 HIP kernels and their C ABI (include/rl_triton_amd.h),
+                        hipcc, cross-compiled for gfx950 on a machine without a GPU
+  _rlk_torch.so         the PyTorch-ROCm extension module over that C ABI
+                        (csrc/rlk_torch.cpp), host code only, g++ against torch's headers
+
+Both land next to the Python package (rl-triton_amd/rl_triton/), which loads them from
+its own directory.
 """
 from __future__ import annotations
 
@@ -20,6 +24,8 @@ REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 LIB = os.path.join(HERE, "rl_triton", "librl_triton_amd.so")
+EXT = os.path.join(HERE, "rl_triton", "_rlk_torch.so")
+EXT_SRC = os.path.join(CSRC, "rlk_torch.cpp")
 ARCH = os.environ.get("RLK_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [
@@ -43,24 +49,57 @@ def deps() -> list[str]:
         os.path.join(INCLUDE, "rl_triton_amd.h"), os.path.abspath(__file__)]
 
 
-def up_to_date() -> bool:
-    if not os.path.exists(LIB):
+def up_to_date(target: str, inputs: list[str]) -> bool:
+    if not os.path.exists(target):
         return False
-    t = os.path.getmtime(LIB)
-    return all(os.path.getmtime(d) <= t for d in deps())
+    t = os.path.getmtime(target)
+    return all(os.path.getmtime(d) <= t for d in inputs)
 
 
-def build(force: bool = True, verbose: bool = False) -> str:
-    if not force and up_to_date():
-        return LIB
-    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    tmp = LIB + ".tmp"
-    cmd = [hipcc, *FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *sources(), "-o", tmp]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
+
+
+def build_lib(force: bool = True, verbose: bool = False) -> str:
+    if not force and up_to_date(LIB, deps()):
+        return LIB
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    tmp = LIB + ".tmp"
+    _run([hipcc, *FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *sources(), "-o", tmp], verbose)
     os.replace(tmp, LIB)
     return LIB
+
+
+def build_ext(force: bool = True, verbose: bool = False) -> str:
+    """_rlk_torch.so: a CPython extension module (no pybind11) linked against torch's
+    libraries and against librl_triton_amd.so, found next to it at run time."""
+    inputs = [EXT_SRC, os.path.join(INCLUDE, "rl_triton_amd.h"), os.path.abspath(__file__), LIB]
+    if not force and up_to_date(EXT, inputs):
+        return EXT
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+    torch_lib = os.path.join(os.path.dirname(torch.__file__), "lib")
+    incs = [sysconfig.get_paths()["include"], INCLUDE,
+            *cpp_extension.include_paths(device_type="cuda")]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = EXT + ".tmp"
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           *[f"-I{i}" for i in incs], EXT_SRC, "-o", tmp,
+           f"-L{torch_lib}", f"-L{os.path.dirname(LIB)}",
+           "-ltorch_python", "-ltorch", "-ltorch_cpu", "-lc10_hip", "-lc10",
+           "-l:librl_triton_amd.so", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}"]
+    _run(cmd, verbose)
+    os.replace(tmp, EXT)
+    return EXT
+
+
+def build(force: bool = True, verbose: bool = False) -> list[str]:
+    return [build_lib(force, verbose), build_ext(force, verbose)]
 
 
 def main(argv=None) -> int:
@@ -68,7 +107,8 @@ def main(argv=None) -> int:
     ap.add_argument("--force", action="store_true")
     ap.add_argument("-v", "--verbose", action="store_true")
     a = ap.parse_args(argv)
-    print(build(force=a.force, verbose=a.verbose))
+    for path in build(force=a.force, verbose=a.verbose):
+        print(path)
     return 0
 
 

@@ -1,0 +1,314 @@
+// rlk_torch.cpp -- the thin PyTorch-ROCm extension over the C ABI (include/rl_triton_amd.h).
+//
+// Python module rl_triton._rlk_torch.  One function per estimator takes the public API's
+// arguments as they were passed.  When the call can go to the C ABI as it stands, the
+// function allocates the outputs, launches on torch's current stream and returns them.
+// That needs every tensor to be a contiguous tensor of the expected dtype and shape on the
+// current GPU, a row that one workgroup scans whole (no look-back workspace), and
+// RL_TRITON_CORRECTNESS_WARNINGS unset.  Any other call returns None, and the Python
+// wrapper takes its general path: the reference's assertions, contiguous copies and the
+// workspace.  A call that is taken gives the results the general path would give, and a
+// malformed call never reaches a kernel from here.
+//
+// The point is host time.  At [4096, 128] a kernel runs ~5 us, while the Python path costs
+// ~10 us per call (argument checks in Python, ctypes conversion).  This path does the
+// checks in C++ and makes no Python-level calls.
+#include <Python.h>
+
+#include <ATen/ATen.h>
+#include <c10/hip/HIPFunctions.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/csrc/autograd/python_variable.h>
+
+#include <cstdlib>
+#include <cstring>
+
+#include "rl_triton_amd.h"
+
+namespace {
+
+// rows up to this length are scanned whole by one workgroup and need no workspace
+constexpr int64_t kNoWorkspaceMaxT = 2048;
+
+bool correctness_warnings() {
+  const char* v = std::getenv("RL_TRITON_CORRECTNESS_WARNINGS");
+  return v != nullptr && std::strcmp(v, "1") == 0;
+}
+
+// A call this path declines: the Python wrapper handles it.
+PyObject* decline() { Py_RETURN_NONE; }
+
+struct Call {
+  c10::DeviceIndex dev = -1;
+  int64_t E = 0, T = 0;
+  bool ok = true;
+
+  // The leading [E, T] float32 tensor: fixes device and shape for the rest.
+  const at::Tensor* lead(PyObject* o) {
+    if (!ok || !THPVariable_Check(o)) return fail();
+    const at::Tensor& t = THPVariable_Unpack(o);
+    if (!t.is_cuda() || t.dim() != 2 || t.scalar_type() != at::kFloat || !t.is_contiguous())
+      return fail();
+    dev = t.get_device();
+    E = t.size(0);
+    T = t.size(1);
+    if (dev != c10::hip::current_device() || T > kNoWorkspaceMaxT) return fail();
+    return &t;
+  }
+  // A tensor of shape [E, T] (or [E] / [E, T, A]) on the same device.
+  const at::Tensor* need(PyObject* o, int kind = 2, int64_t A = 0, at::ScalarType st = at::kFloat) {
+    if (!ok || !THPVariable_Check(o)) return fail();
+    const at::Tensor& t = THPVariable_Unpack(o);
+    if (!t.is_cuda() || t.get_device() != dev || t.scalar_type() != st || !t.is_contiguous())
+      return fail();
+    const bool shape_ok = kind == 1   ? (t.dim() == 1 && t.size(0) == E)
+                        : kind == 2   ? (t.dim() == 2 && t.size(0) == E && t.size(1) == T)
+                                      : (t.dim() == 3 && t.size(0) == E && t.size(1) == T &&
+                                         t.size(2) == A);
+    if (!shape_ok) return fail();
+    return &t;
+  }
+  const at::Tensor* opt(PyObject* o, int kind = 2) { return o == Py_None ? nullptr : need(o, kind); }
+  float scalar(PyObject* o) {
+    if (!ok) return 0.f;
+    if (PyFloat_CheckExact(o)) return (float)PyFloat_AS_DOUBLE(o);
+    if (PyLong_CheckExact(o) || PyFloat_Check(o)) {
+      const double d = PyFloat_AsDouble(o);
+      if (d == -1.0 && PyErr_Occurred()) {
+        PyErr_Clear();
+        fail();
+        return 0.f;
+      }
+      return (float)d;
+    }
+    fail();
+    return 0.f;
+  }
+  const at::Tensor* fail() {
+    ok = false;
+    return nullptr;
+  }
+  void* stream() const { return c10::hip::getCurrentHIPStream(dev).stream(); }
+  at::Tensor output(const at::Tensor& like) const { return at::empty({E, T}, like.options()); }
+};
+
+const float* fp(const at::Tensor* t) { return t ? t->data_ptr<float>() : nullptr; }
+float* fp_out(at::Tensor& t) { return t.data_ptr<float>(); }
+
+PyObject* finish(int status, const char* what, PyObject* result) {
+  if (status != RLK_OK) {
+    Py_XDECREF(result);
+    PyErr_Format(PyExc_RuntimeError, "%s failed: %s (status %d)", what, rlk_status_string(status),
+                 status);
+    return nullptr;
+  }
+  return result;
+}
+
+PyObject* pair(at::Tensor& a, at::Tensor& b) {
+  PyObject* t = PyTuple_New(2);
+  if (!t) return nullptr;
+  PyTuple_SET_ITEM(t, 0, THPVariable_Wrap(std::move(a)));
+  PyTuple_SET_ITEM(t, 1, THPVariable_Wrap(std::move(b)));
+  return t;
+}
+
+bool nargs_is(Py_ssize_t n, Py_ssize_t want, const char* name) {
+  if (n == want) return true;
+  PyErr_Format(PyExc_TypeError, "%s expects %zd arguments, got %zd", name, want, n);
+  return false;
+}
+
+// gae(rewards, values, terminateds, truncateds, gamma, lambda_, bootstrap_values, last_value)
+PyObject* op_gae(PyObject* const* a, Py_ssize_t n) {
+  if (!nargs_is(n, 8, "gae")) return nullptr;
+  if (correctness_warnings()) return decline();
+  Call c;
+  const at::Tensor* r = c.lead(a[0]);
+  const at::Tensor* v = c.need(a[1]);
+  const at::Tensor* te = c.need(a[2]);
+  const at::Tensor* tr = c.opt(a[3]);
+  const float gamma = c.scalar(a[4]), lam = c.scalar(a[5]);
+  const bool has_bv = a[6] != Py_None, has_lv = a[7] != Py_None;
+  if (has_bv && has_lv) return decline();  // the wrapper raises "not both"
+  if (has_lv && tr) return decline();      // ... and "cannot be combined with truncateds"
+  const at::Tensor* boot = has_lv ? c.need(a[7], 1) : c.opt(a[6]);
+  if (!c.ok) return decline();
+  const int mode = has_lv ? RLK_BOOT_ROW : has_bv ? RLK_BOOT_FULL : RLK_BOOT_NONE;
+  at::Tensor out = c.output(*r);
+  const int st = rlk_gae(fp(r), fp(v), fp(te), fp(tr), fp(boot), mode, fp_out(out), c.E, c.T,
+                         gamma, lam, nullptr, 0, c.stream());
+  return finish(st, "rlk_gae", THPVariable_Wrap(std::move(out)));
+}
+
+// vtrace(log_pi_target, log_pi_behavior, values, rewards, terminateds, truncateds, gamma,
+//        rho_bar, c_bar, bootstrap_values, last_value)
+PyObject* op_vtrace(PyObject* const* a, Py_ssize_t n) {
+  if (!nargs_is(n, 11, "vtrace")) return nullptr;
+  if (correctness_warnings()) return decline();
+  Call c;
+  const at::Tensor* r = c.lead(a[3]);
+  const at::Tensor* lpt = c.need(a[0]);
+  const at::Tensor* lpb = c.need(a[1]);
+  const at::Tensor* v = c.need(a[2]);
+  const at::Tensor* te = c.need(a[4]);
+  const at::Tensor* tr = c.opt(a[5]);
+  const float gamma = c.scalar(a[6]), rho_bar = c.scalar(a[7]), c_bar = c.scalar(a[8]);
+  const bool has_bv = a[9] != Py_None, has_lv = a[10] != Py_None;
+  if (has_bv && has_lv) return decline();
+  const at::Tensor* boot = has_lv ? c.need(a[10], 1) : c.opt(a[9]);
+  if (!c.ok) return decline();
+  const int mode = has_lv ? RLK_BOOT_ROW : has_bv ? RLK_BOOT_FULL : RLK_BOOT_NONE;
+  at::Tensor tg = c.output(*r), adv = c.output(*r);
+  const int st = rlk_vtrace(fp(lpt), fp(lpb), fp(v), fp(r), fp(te), fp(tr), fp(boot), mode,
+                            fp_out(tg), fp_out(adv), c.E, c.T, gamma, rho_bar, c_bar, nullptr, 0,
+                            c.stream());
+  return finish(st, "rlk_vtrace", pair(tg, adv));
+}
+
+// retrace(action_probs_target, action_probs_behavior, q_values, next_q_values_all, actions,
+//         rewards, terminateds, truncateds, gamma, lambda_, c_bar, rho_bar)
+PyObject* op_retrace(PyObject* const* a, Py_ssize_t n) {
+  if (!nargs_is(n, 12, "retrace")) return nullptr;
+  if (correctness_warnings()) return decline();
+  Call c;
+  const at::Tensor* r = c.lead(a[5]);
+  int64_t A = 0;
+  if (c.ok && THPVariable_Check(a[0])) {
+    const at::Tensor& pi = THPVariable_Unpack(a[0]);
+    if (pi.dim() == 3) A = pi.size(2);
+  }
+  if (A <= 0 || A > (1 << 20)) return decline();
+  const at::Tensor* pi = c.need(a[0], 3, A);
+  const at::Tensor* mu = c.need(a[1]);
+  const at::Tensor* q = c.need(a[2]);
+  const at::Tensor* nq = c.need(a[3], 3, A);
+  const at::Tensor* act = c.need(a[4], 2, 0, at::kLong);
+  const at::Tensor* te = c.need(a[6]);
+  const at::Tensor* tr = c.need(a[7]);
+  const float gamma = c.scalar(a[8]), lam = c.scalar(a[9]), c_bar = c.scalar(a[10]),
+              rho_bar = c.scalar(a[11]);
+  if (!c.ok) return decline();
+  at::Tensor tg = c.output(*r), adv = c.output(*r);
+  const int st = rlk_retrace(fp(pi), fp(mu), fp(q), fp(nq), act->data_ptr<int64_t>(), fp(r),
+                             fp(te), fp(tr), fp_out(tg), fp_out(adv), c.E, c.T, A, gamma, lam,
+                             c_bar, rho_bar, nullptr, 0, c.stream());
+  return finish(st, "rlk_retrace", pair(tg, adv));
+}
+
+// lambda_returns(rewards, next_values, terminateds, truncateds, gamma, lambda_, bootstrap_values)
+PyObject* op_lambda_returns(PyObject* const* a, Py_ssize_t n) {
+  if (!nargs_is(n, 7, "lambda_returns")) return nullptr;
+  if (correctness_warnings()) return decline();
+  Call c;
+  const at::Tensor* r = c.lead(a[0]);
+  const at::Tensor* nv = c.need(a[1]);
+  const at::Tensor* te = c.need(a[2]);
+  const at::Tensor* tr = c.opt(a[3]);
+  const float gamma = c.scalar(a[4]), lam = c.scalar(a[5]);
+  const at::Tensor* boot = c.opt(a[6]);
+  if (!c.ok) return decline();
+  at::Tensor out = c.output(*r);
+  const int st = rlk_lambda_returns(fp(r), fp(nv), fp(te), fp(tr), fp(boot),
+                                    boot ? RLK_BOOT_FULL : RLK_BOOT_NONE, fp_out(out), c.E, c.T,
+                                    gamma, lam, nullptr, 0, c.stream());
+  return finish(st, "rlk_lambda_returns", THPVariable_Wrap(std::move(out)));
+}
+
+// discounted_returns(rewards, terminateds, truncateds, gamma, bootstrap_values)
+PyObject* op_discounted_returns(PyObject* const* a, Py_ssize_t n) {
+  if (!nargs_is(n, 5, "discounted_returns")) return nullptr;
+  if (correctness_warnings()) return decline();
+  Call c;
+  const at::Tensor* r = c.lead(a[0]);
+  const at::Tensor* te = c.need(a[1]);
+  const at::Tensor* tr = c.opt(a[2]);
+  const float gamma = c.scalar(a[3]);
+  const at::Tensor* boot = c.opt(a[4]);
+  if (!c.ok) return decline();
+  at::Tensor out = c.output(*r);
+  const int st = rlk_discounted_returns(fp(r), fp(te), fp(tr), fp(boot),
+                                        boot ? RLK_BOOT_FULL : RLK_BOOT_NONE, fp_out(out), c.E,
+                                        c.T, gamma, nullptr, 0, c.stream());
+  return finish(st, "rlk_discounted_returns", THPVariable_Wrap(std::move(out)));
+}
+
+// eligibility_traces(gradients, dones, gamma, lambda_, seed_values)
+PyObject* op_eligibility_traces(PyObject* const* a, Py_ssize_t n) {
+  if (!nargs_is(n, 5, "eligibility_traces")) return nullptr;
+  if (correctness_warnings()) return decline();
+  Call c;
+  const at::Tensor* g = c.lead(a[0]);
+  const at::Tensor* d = c.need(a[1]);
+  const float gamma = c.scalar(a[2]), lam = c.scalar(a[3]);
+  const at::Tensor* seed = c.opt(a[4], 1);
+  if (!c.ok) return decline();
+  at::Tensor out = c.output(*g);
+  const int st = rlk_eligibility_traces(fp(g), fp(d), fp(seed), fp_out(out), c.E, c.T, gamma,
+                                        lam, nullptr, 0, c.stream());
+  return finish(st, "rlk_eligibility_traces", THPVariable_Wrap(std::move(out)));
+}
+
+// prefix_sum(inputs, dones, seed_values, ends_at)   (ends_at: the boundary, already checked)
+PyObject* op_prefix_sum(PyObject* const* a, Py_ssize_t n) {
+  if (!nargs_is(n, 4, "prefix_sum")) return nullptr;
+  if (correctness_warnings()) return decline();
+  Call c;
+  const at::Tensor* x = c.lead(a[0]);
+  const at::Tensor* d = c.need(a[1]);
+  const at::Tensor* seed = c.opt(a[2], 1);
+  if (!c.ok || !PyBool_Check(a[3])) return decline();
+  at::Tensor out = c.output(*x);
+  const int st = rlk_prefix_sum(fp(x), fp(d), fp(seed), fp_out(out), c.E, c.T,
+                                a[3] == Py_True ? 1 : 0, nullptr, 0, c.stream());
+  return finish(st, "rlk_prefix_sum", THPVariable_Wrap(std::move(out)));
+}
+
+// affine_scan(u, v, carry, direction)
+PyObject* op_affine_scan(PyObject* const* a, Py_ssize_t n) {
+  if (!nargs_is(n, 4, "affine_scan")) return nullptr;
+  if (correctness_warnings()) return decline();
+  Call c;
+  const at::Tensor* u = c.lead(a[0]);
+  const at::Tensor* v = c.need(a[1]);
+  const at::Tensor* carry = c.opt(a[2], 1);
+  const long dir = PyLong_CheckExact(a[3]) ? PyLong_AsLong(a[3]) : -1;
+  if (!c.ok || (dir != RLK_BACKWARD && dir != RLK_FORWARD)) return decline();
+  at::Tensor out = c.output(*u);
+  const int st = rlk_affine_scan(fp(u), fp(v), fp(carry), fp_out(out), c.E, c.T, (int)dir,
+                                 nullptr, 0, c.stream());
+  return finish(st, "rlk_affine_scan", THPVariable_Wrap(std::move(out)));
+}
+
+// C++ exceptions (an allocation that fails, say) must not cross into the interpreter: such
+// a call is declined, and the Python path raises torch's own exception for it.
+template <PyObject* (*F)(PyObject* const*, Py_ssize_t)>
+PyObject* guarded(PyObject*, PyObject* const* a, Py_ssize_t n) {
+  try {
+    return F(a, n);
+  } catch (...) {
+    return decline();
+  }
+}
+
+#define RLK_METHOD(name) \
+  { #name, (PyCFunction)(void (*)(void))guarded<op_##name>, METH_FASTCALL, nullptr }
+
+PyMethodDef kMethods[] = {
+    RLK_METHOD(gae),
+    RLK_METHOD(vtrace),
+    RLK_METHOD(retrace),
+    RLK_METHOD(lambda_returns),
+    RLK_METHOD(discounted_returns),
+    RLK_METHOD(eligibility_traces),
+    RLK_METHOD(prefix_sum),
+    RLK_METHOD(affine_scan),
+    {nullptr, nullptr, 0, nullptr}};
+
+PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_rlk_torch",
+                       "Tensor-level fast path of rl_triton over librl_triton_amd.so's C ABI.", -1,
+                       kMethods};
+
+}  // namespace
+
+PyMODINIT_FUNC PyInit__rlk_torch(void) { return PyModule_Create(&kModule); }

@@ -50,6 +50,17 @@ _RESTYPES = {"rlk_workspace_bytes": _SZ, "rlk_status_string": ctypes.c_char_p}
 _lib = None
 _lock = threading.Lock()
 
+# The tensor-level fast path (csrc/rlk_torch.cpp, built next to this file): a well-formed
+# call goes from the API straight to the C ABI with its checks done in C++; it returns None
+# for any call it does not take, and the op's Python path handles that call.  None here if
+# the module is not built (the Python path then serves every call, through ctypes); a
+# module that is built but does not load is an error.
+_FAST_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_rlk_torch.so")
+if os.path.exists(_FAST_PATH):
+    from rl_triton import _rlk_torch as fast
+else:
+    fast = None
+
 
 class NativeLibraryError(RuntimeError):
     """The HIP library is missing or failed to load; there is no other backend."""

@@ -66,6 +66,13 @@ def _run_scan(
     Returns:
         out: A[t], shape [num_envs, seq_len], float32.
     """
+    # fast path: a well-formed call goes straight to the C ABI (rl_triton._rlk_torch)
+    fast = _native.fast
+    if fast is not None:
+        res = fast.affine_scan(u, v, bootstrap, _native.BACKWARD)
+        if res is not None:
+            return res
+
     if not u.is_contiguous():
         _perf_warn("u is not contiguous; a copy will be made. Call .contiguous() before the hot loop to avoid this overhead.")
     if not v.is_contiguous():
@@ -108,6 +115,13 @@ def _run_scan_forward(
     Returns:
         out: e[t], shape [num_envs, seq_len], float32.
     """
+    # fast path: a well-formed call goes straight to the C ABI (rl_triton._rlk_torch)
+    fast = _native.fast
+    if fast is not None:
+        res = fast.affine_scan(u, v, seed, _native.FORWARD)
+        if res is not None:
+            return res
+
     if not u.is_contiguous():
         _perf_warn("u is not contiguous; a copy will be made. Call .contiguous() before the hot loop to avoid this overhead.")
     if not v.is_contiguous():

@@ -48,6 +48,13 @@ def compute_gae(
     Returns:
         advantages: A[t], shape [num_envs, seq_len], float32.
     """
+    # fast path: a well-formed call goes straight to the C ABI (rl_triton._rlk_torch)
+    fast = _native.fast
+    if fast is not None:
+        res = fast.gae(rewards, values, terminateds, truncateds, gamma, lambda_, bootstrap_values, last_value)
+        if res is not None:
+            return res
+
     num_envs, seq_len = rewards.shape
     has_truncations   = truncateds is not None
 

@@ -28,6 +28,13 @@ def compute_episodic_prefix_sum(
     Returns:
         prefix_sums: C[t], [num_envs, seq_len], float32.
     """
+    # fast path: a well-formed call goes straight to the C ABI (rl_triton._rlk_torch)
+    fast = _native.fast
+    if fast is not None and (boundary == "ends_at" or boundary == "starts_at"):
+        res = fast.prefix_sum(inputs, dones, seed_values, boundary == "ends_at")
+        if res is not None:
+            return res
+
     num_envs, seq_len = inputs.shape
 
     if _CORRECTNESS_WARNINGS():

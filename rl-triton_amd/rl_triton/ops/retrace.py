@@ -1,5 +1,6 @@
 import torch
 
+from rl_triton import _native
 from rl_triton.ops._scan import _CORRECTNESS_WARNINGS
 from rl_triton.ops.retrace_fused import _retrace_launch, compute_retrace_fused
 
@@ -42,6 +43,13 @@ def compute_retrace(
         retrace_targets: Q_ret[t], [num_envs, seq_len], float32.
         advantages:      A[t],     [num_envs, seq_len], float32.
     """
+    # fast path: a well-formed call goes straight to the C ABI (rl_triton._rlk_torch)
+    fast = _native.fast
+    if fast is not None:
+        res = fast.retrace(action_probs_target, action_probs_behavior, q_values, next_q_values_all, actions, rewards, terminateds, truncateds, gamma, lambda_, c_bar, rho_bar)
+        if res is not None:
+            return res
+
     # Cheap structural checks -- always-on (ops/retrace.py:116-141).
     for name, t in [
         ("action_probs_behavior", action_probs_behavior),

@@ -39,6 +39,13 @@ def compute_retrace_fused(
         retrace_targets: Q_ret[t], [num_envs, seq_len], float32.
         advantages:      A[t],     [num_envs, seq_len], float32.
     """
+    # fast path: a well-formed call goes straight to the C ABI (rl_triton._rlk_torch)
+    fast = _native.fast
+    if fast is not None:
+        res = fast.retrace(action_probs_target, action_probs_behavior, q_values, next_q_values_all, actions, rewards, terminated, truncateds, gamma, lambda_, c_bar, rho_bar)
+        if res is not None:
+            return res
+
     num_envs, seq_len = rewards.shape
 
     assert seq_len <= _FLAT_MAX_SEQ_LEN, (

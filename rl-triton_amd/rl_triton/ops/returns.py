@@ -28,6 +28,13 @@ def compute_lambda_returns(
     Returns:
         lambda_returns: G[t], [num_envs, seq_len], float32.
     """
+    # fast path: a well-formed call goes straight to the C ABI (rl_triton._rlk_torch)
+    fast = _native.fast
+    if fast is not None:
+        res = fast.lambda_returns(rewards, next_values, terminateds, truncateds, gamma, lambda_, bootstrap_values)
+        if res is not None:
+            return res
+
     num_envs, seq_len = rewards.shape
     has_truncations   = truncateds is not None
 
@@ -85,6 +92,13 @@ def compute_discounted_returns(
     Returns:
         returns: G[t], [num_envs, seq_len], float32.
     """
+    # fast path: a well-formed call goes straight to the C ABI (rl_triton._rlk_torch)
+    fast = _native.fast
+    if fast is not None:
+        res = fast.discounted_returns(rewards, terminateds, truncateds, gamma, bootstrap_values)
+        if res is not None:
+            return res
+
     num_envs, seq_len = rewards.shape
     has_truncations   = truncateds is not None
 
@@ -143,6 +157,13 @@ def compute_eligibility_traces(
     Returns:
         traces: z[t], [num_envs, seq_len], float32.
     """
+    # fast path: a well-formed call goes straight to the C ABI (rl_triton._rlk_torch)
+    fast = _native.fast
+    if fast is not None:
+        res = fast.eligibility_traces(gradients, dones, gamma, lambda_, seed_values)
+        if res is not None:
+            return res
+
     num_envs, seq_len = gradients.shape
 
     # Cheap structural checks -- always-on (ops/returns.py:309-317).

@@ -1,5 +1,6 @@
 import torch
 
+from rl_triton import _native
 from rl_triton.ops._scan import _FLAT_MAX_SEQ_LEN, _CORRECTNESS_WARNINGS
 from rl_triton.ops.vtrace_fused import _vtrace_launch, compute_vtrace_fused
 
@@ -30,6 +31,13 @@ def compute_vtrace(
         vtrace_targets:    vs[t], [num_envs, seq_len], float32.
         vtrace_advantages: A[t],  [num_envs, seq_len], float32.
     """
+    # fast path: a well-formed call goes straight to the C ABI (rl_triton._rlk_torch)
+    fast = _native.fast
+    if fast is not None:
+        res = fast.vtrace(log_pi_target, log_pi_behavior, values, rewards, terminateds, truncateds, gamma, rho_bar, c_bar, bootstrap_values, last_value)
+        if res is not None:
+            return res
+
     num_envs, seq_len = rewards.shape
     has_truncations   = truncateds is not None
 

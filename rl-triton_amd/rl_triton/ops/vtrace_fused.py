@@ -39,6 +39,13 @@ def compute_vtrace_fused(
         vtrace_targets:    [num_envs, seq_len], float32.
         vtrace_advantages: [num_envs, seq_len], float32.
     """
+    # fast path: a well-formed call goes straight to the C ABI (rl_triton._rlk_torch)
+    fast = _native.fast
+    if fast is not None:
+        res = fast.vtrace(log_pi_target, log_pi_behavior, values, rewards, terminateds, truncateds, gamma, rho_bar, c_bar, bootstrap_values, last_value)
+        if res is not None:
+            return res
+
     num_envs, seq_len = rewards.shape
     has_truncations   = truncateds is not None
 

@@ -122,3 +122,22 @@ def test_public_surface_matches_reference():
         "compute_gae", "compute_lambda_returns", "compute_retrace", "compute_vtrace"])
     assert _FLAT_MAX_SEQ_LEN == 131072
     assert callable(compute_retrace_fused)
+
+
+def test_fast_path_declines_cpu_tensors():
+    """The C++ fast path takes GPU tensors only; CPU calls reach the Python path and its
+    reference assertions."""
+    from rl_triton import _native
+    if _native.fast is None:
+        pytest.skip("rl_triton._rlk_torch is not built")
+    x = torch.zeros(4, 8)
+    f = _native.fast
+    assert f.gae(x, x, x, None, 0.99, 0.95, None, None) is None
+    assert f.vtrace(x, x, x, x, x, None, 0.99, 1.0, 1.0, None, None) is None
+    assert f.prefix_sum(x, x, None, True) is None
+    assert f.affine_scan(x, x, None, 0) is None
+    with pytest.raises(TypeError):
+        f.gae(x)
+    import rl_triton
+    with pytest.raises(AssertionError, match="must be on CUDA"):
+        rl_triton.compute_gae(x, x, x)

@@ -17,6 +17,7 @@ import numpy as np
 import pytest
 import torch
 
+import baseline_configs
 from _common import OUTPUTS, assert_close, golden_cases, make_inputs, max_abs_err, run_api, run_oracle
 
 pytestmark = pytest.mark.gpu
@@ -120,6 +121,30 @@ def test_parity_long_rows(op, shape, device):
     for name, g, e in zip(OUTPUTS[op], got, exp):
         atol = _long_atol(op, inp, e)
         assert_close(g.cpu().numpy(), e, 1e-5, atol, f"{op}{shape}:{name}")
+
+
+@pytest.mark.parametrize("name", list(baseline_configs.CONFIGS))
+def test_baseline_configs_full_size(name, device):
+    """Every BASELINE.json configuration at its full size and distributions, against the
+    float64 oracle.  seq_len <= 2048: rtol = 1e-5, atol = 1e-5 * max(1, max|expected|);
+    longer rows (look-back path): the horizon-scaled atol of baseline_configs.horizon_atol.
+    Also asserts that no look-back wait gave up."""
+    from rl_triton import _native
+    op, E, T, _ = baseline_configs.CONFIGS[name]
+    inp, params = baseline_configs.make(name, seed=0)
+    print(f"[case] {name} [{E},{T}]", flush=True)
+    got = baseline_configs.call(name, {k: v.to(device) for k, v in inp.items()}, params)
+    exp = run_oracle(op, {k: v.numpy() for k, v in inp.items()}, params)
+    torch.cuda.synchronize()
+    assert not _native.workspace_error(device)
+    for out_name, g, e in zip(OUTPUTS[op], got, exp):
+        g = g.cpu().numpy()
+        if T <= 2048:
+            atol = 1e-5 * max(1.0, float(np.max(np.abs(e))))
+        else:
+            atol = baseline_configs.horizon_atol(name, e, inp.get("dones"))
+        print(f"{name}:{out_name} max abs err {max_abs_err(g, e):.3e} (atol {atol:.2e})")
+        assert_close(g, e, 1e-5, atol, f"{name}:{out_name}")
 
 
 def test_lookback_deterministic_and_clean(device):
@@ -231,3 +256,64 @@ def test_max_abs_error_report(device):
                   f"(float32 sequential loop: {err_loop:.3e})")
             assert err < 1e-4
             assert err <= 2.0 * err_loop + 1e-7
+
+
+# ---------------------------------------------------------------------------------------
+# the tensor-level fast path (rl_triton._rlk_torch) against the general Python path
+# ---------------------------------------------------------------------------------------
+FAST_OPS = ["gae", "vtrace", "retrace", "lambda_returns", "discounted_returns",
+            "eligibility_traces", "prefix_sum", "backward_scan", "forward_scan"]
+
+
+@pytest.mark.parametrize("op", FAST_OPS)
+@pytest.mark.parametrize("shape", [(1, 1), (33, 257), (4096, 128), (16, 2048)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_fast_path_matches_python_path(op, shape, device, monkeypatch):
+    """With RL_TRITON_CORRECTNESS_WARNINGS unset a well-formed call takes the C++ fast path;
+    with it set, the Python path.  Both launch the same kernel with the same arguments, so
+    the results are bit-identical."""
+    from rl_triton import _native
+    assert _native.fast is not None, "rl_triton._rlk_torch is not built"
+    boot = "full" if op in ("gae", "vtrace", "lambda_returns", "discounted_returns") else "row"
+    inp, params = make_inputs(op, *shape, seed=21, p_trunc=0.02 if op != "retrace" else 0.0,
+                              boot=boot)
+    slow = run_api(op, inp, params, device)
+    monkeypatch.delenv("RL_TRITON_CORRECTNESS_WARNINGS")
+    calls = []
+    real = _native.fast
+    monkeypatch.setattr(_native, "fast", _Spy(real, calls))
+    fast = run_api(op, inp, params, device)
+    assert calls and all(taken for _, taken in calls), f"fast path declined: {calls}"
+    for s, f in zip(slow, fast):
+        assert torch.equal(s, f)
+
+
+class _Spy:
+    """Wraps the fast-path module and records (function, taken) per call."""
+
+    def __init__(self, mod, calls):
+        self._mod, self._calls = mod, calls
+
+    def __getattr__(self, name):
+        fn = getattr(self._mod, name)
+
+        def wrapped(*a):
+            res = fn(*a)
+            self._calls.append((name, res is not None))
+            return res
+        return wrapped
+
+
+def test_fast_path_declines_what_it_cannot_take(device, monkeypatch):
+    """Non-contiguous inputs, long rows and the correctness flag go to the Python path."""
+    from rl_triton import _native
+    f = _native.fast
+    x = torch.zeros(8, 64, device=device)
+    assert f.gae(x, x, x, None, 0.99, 0.95, None, None) is None  # flag set by the fixture
+    monkeypatch.delenv("RL_TRITON_CORRECTNESS_WARNINGS")
+    assert f.gae(x, x, x, None, 0.99, 0.95, None, None) is not None
+    assert f.gae(x.t(), x.t(), x.t(), None, 0.99, 0.95, None, None) is None
+    long = torch.zeros(2, 4096, device=device)
+    assert f.gae(long, long, long, None, 0.99, 0.95, None, None) is None
+    assert f.gae(x, x, x, None, 0.99, 0.95, x, torch.zeros(8, device=device)) is None
+    assert f.gae(x, x, x.double(), None, 0.99, 0.95, None, None) is None
