@@ -2,38 +2,20 @@
 // include/rl_triton_amd.h): argument checks, launch planning and kernel launches.
 #include <hip/hip_runtime.h>
 
-#include <map>
-#include <mutex>
-#include <utility>
-
 #include "rl_triton_amd.h"
 #include "rlk_ops.hpp"
 
 namespace rlk {
 namespace {
 
-// Launch geometry.  The macros only exist so that tuning sweeps can rebuild the library
-// with other values; the defaults are the shipped configuration.
-#ifndef RLK_LB_NTD
-#define RLK_LB_NTD 512
-#endif
-#ifndef RLK_LB_S
-#define RLK_LB_S 8
-#endif
-constexpr int kNT = 256;             // short rows: threads per workgroup (4 wavefronts)
-constexpr int kShortMaxT = 2048;     // rows up to this length are kept whole in one workgroup
-constexpr int kLbNTD = RLK_LB_NTD;   // look-back path: data threads per workgroup
-constexpr int kLbBlock = kLbNTD + kWave;  // ... plus the coordinator wave
-constexpr int kTileS = RLK_LB_S;     // look-back path: steps per data thread
-constexpr int kTile = kLbNTD * kTileS;
-
-struct Plan {
-  bool lookback;
-  int S;
-  int log2L;
-  int tiles_per_row;
-  int64_t grid;
-};
+// Launch geometry.
+constexpr int kNT = 256;          // short rows: threads per workgroup (4 wavefronts)
+constexpr int kShortMaxT = 2048;  // rows up to this length are kept whole in one workgroup
+// Long rows: each op fixes its threads per workgroup (kLongThreads) and the most 4-step
+// segments per thread its registers hold without spilling (kLongMaxSegments, 2..8).  The
+// smallest tile any op uses sizes the workspace.
+constexpr int kMinQ = 2;
+constexpr int64_t kMinTile = (int64_t)512 * kSeg * kMinQ;  // 4096 steps
 
 int ceil_log2(int64_t x) {
   int k = 0;
@@ -41,73 +23,79 @@ int ceil_log2(int64_t x) {
   return k;
 }
 
-// Short rows: S steps per thread, L = 2^ceil(log2(ceil(T/S))) threads per row, 256/L
-// rows per workgroup.  Long rows: tiles of kTile steps, drawn by a persistent grid of
-// min(E, 64) * k workgroups (see lookback_kernel in rlk_engine.hpp).
-Plan make_plan(int64_t E, int64_t T) {
-  Plan p{};
-  if (T <= kShortMaxT) {
-    p.lookback = false;
-    p.S = (T <= 1024) ? 4 : 8;
-    p.log2L = ceil_log2((T + p.S - 1) / p.S);
-    p.tiles_per_row = 1;
-    const int64_t rows_per_block = kNT >> p.log2L;
-    p.grid = (E + rows_per_block - 1) / rows_per_block;
-  } else {
-    p.lookback = true;
-    p.S = kTileS;
-    p.log2L = 0;
-    p.tiles_per_row = (int)((T + kTile - 1) / kTile);
-    p.grid = E * p.tiles_per_row;  // upper bound; the persistent grid is smaller
+// Compute units of the current device (cached; 256 on MI355X).
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
   }
-  return p;
+  return cached[dev];
 }
 
+// Long rows: segments per thread.  Tiles are as large as the op's registers allow while
+// the call still has one tile per compute unit: a longer tile shortens the look-back
+// chain along a row, and a tile per CU keeps every CU streaming.
+template <class Op>
+int long_segments(int64_t E, int64_t T) {
+  const int64_t cus = device_cus();
+  for (int q = Op::kLongMaxSegments; q > kMinQ; q /= 2) {
+    const int64_t tile = (int64_t)Op::kLongThreads * kSeg * q;
+    if (E * ((T + tile - 1) / tile) >= cus) return q;
+  }
+  return kMinQ;
+}
+
+// Workspace for a long-row call: status words for its tiles, counted at the smallest tile.
 size_t workspace_bytes(int64_t E, int64_t T) {
   if (E <= 0 || T <= kShortMaxT) return 0;
-  const int64_t tiles = E * ((T + kTile - 1) / kTile);
+  const int64_t tiles = E * ((T + kMinTile - 1) / kMinTile);
   return (size_t)(kStatusOffset + 2 * tiles) * sizeof(uint64_t);
 }
 
 bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Resident workgroups of `kernel` on the current device (occupancy x compute units),
-// cached per kernel and device: the persistent look-back grid is sized to it.
-int resident_workgroups(const void* kernel, int nt) {
-  static std::mutex mu;
-  static std::map<std::pair<const void*, int>, int> cache;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  std::lock_guard<std::mutex> lock(mu);
-  auto it = cache.find({kernel, dev});
-  if (it != cache.end()) return it->second;
-  int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, nt, 0) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return 0;
-  const int n = per_cu * cus;
-  cache[{kernel, dev}] = n;
-  return n;
-}
-
+// Short rows: S steps per thread, L = 2^ceil(log2(ceil(T/S))) threads per row, 256/L rows
+// per workgroup, grid = ceil(E / (256/L)).
 template <class Op, int S, bool VEC>
-hipError_t launch_rows(const Op& op, int64_t E, int T, int log2L, int64_t grid, hipStream_t stream) {
+hipError_t launch_rows(const Op& op, int64_t E, int T, hipStream_t stream) {
+  int log2L = ceil_log2((T + S - 1) / S);
+  const int64_t rows_per_block = kNT >> log2L;
+  const int64_t grid = (E + rows_per_block - 1) / rows_per_block;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   void* args[] = {const_cast<Op*>(&op), &E, &T, &log2L};
   return hipLaunchKernel(reinterpret_cast<const void*>(&rows_kernel<Op, kNT, S, VEC>),
                          dim3((unsigned)grid), dim3(kNT), args, 0, stream);
 }
 
-template <class Op, bool VEC>
-hipError_t launch_lookback(const Op& op, int64_t E, int T, int tpr, uint64_t* ws, hipStream_t stream) {
-  const void* kernel = reinterpret_cast<const void*>(&lookback_kernel<Op, kLbNTD, kTileS, VEC>);
+// Long rows: one tile of kLongThreads * 4 * Q steps per workgroup, grid = nslots * (tiles
+// of the fullest slot) (see chain_kernel in rlk_engine.hpp).
+template <class Op, int Q, bool VEC>
+hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_t stream) {
+  constexpr int NT = Op::kLongThreads;
+  static_assert(NT * kSeg * Q >= kMinTile, "the workspace is sized for the smallest tile");
+  constexpr int64_t tile = (int64_t)NT * kSeg * Q;
+  int tpr = (int)((T + tile - 1) / tile);
   const int64_t nslots = lookback_slots(E);
-  const int64_t tiles_per_slot = ((E + nslots - 1) / nslots) * (int64_t)tpr;
-  int64_t wgs = resident_workgroups(kernel, kLbBlock) / nslots;
-  if (wgs < 1) wgs = 1;
-  if (wgs > tiles_per_slot) wgs = tiles_per_slot;
-  const int64_t grid = nslots * wgs;
+  const int64_t grid = nslots * (((E + nslots - 1) / nslots) * (int64_t)tpr);
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   void* args[] = {const_cast<Op*>(&op), &E, &T, &tpr, &ws};
-  return hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(kLbBlock), args, 0, stream);
+  return hipLaunchKernel(reinterpret_cast<const void*>(&chain_kernel<Op, NT, Q, VEC>),
+                         dim3((unsigned)grid), dim3(NT), args, 0, stream);
+}
+
+template <class Op, bool VEC>
+hipError_t launch_long(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_t stream) {
+  const int q = long_segments<Op>(E, T);
+  if constexpr (Op::kLongMaxSegments >= 8)
+    if (q == 8) return launch_chain<Op, 8, VEC>(op, E, T, ws, stream);
+  if constexpr (Op::kLongMaxSegments >= 4)
+    if (q == 4) return launch_chain<Op, 4, VEC>(op, E, T, ws, stream);
+  return launch_chain<Op, 2, VEC>(op, E, T, ws, stream);
 }
 
 template <class Op>
@@ -115,23 +103,18 @@ int launch(const Op& op, int64_t E, int64_t T, bool vec, void* workspace, size_t
            void* stream) {
   if (E < 0 || T < 0 || T > (int64_t{1} << 30)) return RLK_ERR_INVALID_ARGUMENT;
   if (E == 0 || T == 0) return RLK_OK;
-  const Plan p = make_plan(E, T);
-  if (p.grid > 0x7fffffffLL) return RLK_ERR_INVALID_ARGUMENT;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  uint64_t* ws = reinterpret_cast<uint64_t*>(workspace);
   const int Ti = (int)T;
   hipError_t e;
-  if (p.lookback) {
+  if (T > kShortMaxT) {
+    uint64_t* ws = reinterpret_cast<uint64_t*>(workspace);
     if (ws == nullptr || workspace_bytes_given < workspace_bytes(E, T) || !aligned16(ws))
       return RLK_ERR_WORKSPACE;
-    e = vec ? launch_lookback<Op, true>(op, E, Ti, p.tiles_per_row, ws, s)
-            : launch_lookback<Op, false>(op, E, Ti, p.tiles_per_row, ws, s);
-  } else if (p.S == 4) {
-    e = vec ? launch_rows<Op, 4, true>(op, E, Ti, p.log2L, p.grid, s)
-            : launch_rows<Op, 4, false>(op, E, Ti, p.log2L, p.grid, s);
+    e = vec ? launch_long<Op, true>(op, E, Ti, ws, s) : launch_long<Op, false>(op, E, Ti, ws, s);
+  } else if (T <= 1024) {
+    e = vec ? launch_rows<Op, 4, true>(op, E, Ti, s) : launch_rows<Op, 4, false>(op, E, Ti, s);
   } else {
-    e = vec ? launch_rows<Op, 8, true>(op, E, Ti, p.log2L, p.grid, s)
-            : launch_rows<Op, 8, false>(op, E, Ti, p.log2L, p.grid, s);
+    e = vec ? launch_rows<Op, 8, true>(op, E, Ti, s) : launch_rows<Op, 8, false>(op, E, Ti, s);
   }
   return e == hipSuccess ? RLK_OK : RLK_ERR_LAUNCH;
 }

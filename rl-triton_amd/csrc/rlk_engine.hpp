@@ -13,17 +13,15 @@
 //     wavefront shuffle scan (width min(L, 64)) and, when L > 64, through LDS;
 //   * short rows: a workgroup of NT threads holds NT/L whole rows, no inter-workgroup
 //     traffic;
-//   * long rows: a row is split into tiles of NTD*S steps, handed out by per-slot atomic
-//     tickets in scan order to a persistent grid and chained by a decoupled look-back over
-//     per-tile status words in a caller-provided workspace; a coordinator wave per
-//     workgroup does the look-back while the data waves prefetch the next tile.
+//   * long rows: a row is split into tiles, one per workgroup, handed out by per-slot
+//     atomic tickets in scan order and chained by a decoupled look-back over per-tile
+//     status words in a caller-provided workspace.
 //
 // An estimator ("Op") supplies:
 //   Regs                      per-thread registers for S steps
-//   load(row, t0, T, R)       issue the segment's loads: unconditional, raw, nothing
-//                             computed from them (see load_seg)
+//   load(row, t0, T, R)       issue the segment's loads, clamped into the row
 //   prepare(R, row, t0, T)    everything derived from the loaded values (exp, ratios,
-//                             bootstrap selection), run when the tile is processed
+//                             bootstrap selection)
 //   Halo / export / halo_load the one-step neighbour data the producer needs (values[t+1]
 //                             for GAE, done[t-1] for forward traces), passed lane to lane
 //                             and read from global memory at wave/tile edges
@@ -57,13 +55,9 @@ struct NoHalo {};
 // Segment loads / stores.  VEC: T % 4 == 0 and every base pointer 16-byte aligned, so a
 // segment start t0 (a multiple of 4) is 16-byte aligned and each quad is all-in or all-out.
 //
-// Loads are unconditional and raw: a step beyond T reads the row's last quad (or step),
-// and nothing is computed from the loaded values until the op's prepare() -- padding
-// steps are masked to the identity map in coef() and their stores go to the sink, so
-// their register contents never matter.  Every lane then issues the same memory
-// instructions in every tile, and no instruction touches a prefetched register before the
-// tile is processed, so the look-back kernel's prefetch really stays in flight (vector
-// loads return in order; a load under a branch, or an early use, forces an early wait).
+// Loads are unconditional: a step beyond T reads the row's last quad (or step).  Padding
+// steps are masked to the identity map in coef() and are not stored, so their register
+// contents never matter.
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ int clamp_step(int t, int T) { return t < 0 ? 0 : (t < T ? t : T - 1); }
 
@@ -86,34 +80,26 @@ __device__ __forceinline__ void load_seg(const float* __restrict__ p, int t0, in
   }
 }
 
-// sink == nullptr: steps beyond T are skipped.  Otherwise every quad (step) is stored and
-// those beyond T go to the lane's own 16-byte slot of `sink` (kSinkWords of scratch), so
-// that the number of memory instructions does not depend on the tile either.
+// Steps beyond T are not stored.
 template <int S, bool VEC>
-__device__ __forceinline__ void store_seg(float* __restrict__ p, int t0, int T, const float (&v)[S],
-                                          float* sink) {
-  float* const slot = sink ? sink + 4 * __lane_id() : nullptr;
+__device__ __forceinline__ void store_seg(float* __restrict__ p, int t0, int T, const float (&v)[S]) {
   if constexpr (VEC) {
 #pragma unroll
     for (int q = 0; q < S / 4; ++q) {
       const int t = t0 + 4 * q;
-      const float4 f = make_float4(v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-      if (slot) *reinterpret_cast<float4*>(t < T ? p + t : slot) = f;
-      else if (t < T) *reinterpret_cast<float4*>(p + t) = f;
+      if (t < T)
+        *reinterpret_cast<float4*>(p + t) = make_float4(v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < S; ++i) {
-      if (slot) *(t0 + i < T ? p + t0 + i : slot) = v[i];
-      else if (t0 + i < T) p[t0 + i] = v[i];
-    }
+    for (int i = 0; i < S; ++i)
+      if (t0 + i < T) p[t0 + i] = v[i];
   }
 }
 
 // A 0.0f that is never written: the source of an unconditional load whose operand is absent.
 // Global (not __constant__) memory, so that selecting between it and a global operand keeps
-// a global load: a flat load would count against the LDS counter too and make the next LDS
-// wait drain the whole prefetch.
+// a global load (a flat load would also count against the LDS counter).
 __device__ float g_zero[4] = {0.f, 0.f, 0.f, 0.f};
 
 // Bootstrap argument shared by the backward estimators: none, one value per row, or
@@ -205,21 +191,19 @@ __device__ __forceinline__ Affine group_scan(Affine m, int W) {
 //                                 [3] error flag (a bounded wait gave up, or counters were
 //                                 not at rest); others reserved
 //   slots    [8 + 32*s], s < 64   ticket counter slot s (256 bytes each): +0 ticket,
-//                                 +16 finished-workgroup counter (its own 128-byte line)
-//   sink     [8 + 32*64, +128)    1 KB that takes the stores of steps beyond T (garbage)
-//   status   [8 + 32*64 + 128...] two words per tile, tiles of row r at r*tiles_per_row
+//                                 +16 drawn-workgroup counter (its own 128-byte line)
+//   status   [8 + 32*64 ...]      two words per tile, tiles of row r at r*tiles_per_row
 // Device-scope atomics on one address serialise (~12 ns each on MI355X), so tickets come
 // from up to 64 counters: row r draws from slot r % 64, and since a tile only ever waits
 // on tiles of its own row, handing out each slot's tiles in scan order is enough for
-// forward progress.  The epoch is global and advances once per call, after every slot
-// has finished, so a status word left by any earlier call never matches the current one.
+// forward progress.  The epoch is global and advances once per call, after every
+// workgroup has read it, so a status word left by any earlier call never matches the
+// current one.
 // ---------------------------------------------------------------------------------------
 constexpr int kHeaderWords = 8;
 constexpr int kSlots = 64;
 constexpr int kSlotWords = 32;
-constexpr int kSinkOffset = kHeaderWords + kSlots * kSlotWords;
-constexpr int kSinkWords = 128;  // 64 lanes x 16 bytes
-constexpr int kStatusOffset = kSinkOffset + kSinkWords;
+constexpr int kStatusOffset = kHeaderWords + kSlots * kSlotWords;
 constexpr uint32_t kAgg = 1, kInc = 2;
 constexpr uint32_t kEpochMask = 0x3fffffffu;
 constexpr int kSpinLimit = 1 << 20;  // polls before a wait gives up (~1 s), never reached when correct
@@ -241,19 +225,14 @@ __device__ __forceinline__ uint64_t pack(uint32_t tag, float v) {
 // Issue the loads of this thread's segment, and of the neighbour step for the edge lane
 // whose neighbour lives outside its wave, together: the edge lane must not pay a second
 // memory round trip after its segment has arrived.
-//   UNIFORM = false: only the edge lane loads the neighbour step, when it exists.
-//   UNIFORM = true:  every lane loads it (one wave-uniform address, clamped into the row),
-//                    so the instruction stream does not depend on the lane or the tile.
-template <class Op, int S, bool VEC, bool UNIFORM>
+template <class Op, int S, bool VEC>
 __device__ __forceinline__ void load_segment(const Op& op, int64_t row, int t0, int T, int lane,
                                              typename Op::template Regs<S>& R,
                                              typename Op::Halo& edge) {
   if constexpr (!std::is_same<typename Op::Halo, NoHalo>::value) {
-    if constexpr (UNIFORM) {
-      const int te = Op::kForward ? t0 - lane * S - 1 : t0 + (kWave - lane) * S;
-      edge = op.halo_load(row, clamp_step(te, T), T);
-    } else if constexpr (Op::kForward) {
-      if (lane == 0 && t0 > 0) edge = op.halo_load(row, t0 - 1, T);
+    if constexpr (Op::kForward) {
+      // a padding wave (t0 > T) still reads inside the row; its value is never used
+      if (lane == 0 && t0 > 0) edge = op.halo_load(row, clamp_step(t0 - 1, T), T);
     } else {
       if (lane == kWave - 1 && t0 + S < T) edge = op.halo_load(row, t0 + S, T);
     }
@@ -350,7 +329,7 @@ __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T,
 
   Regs R;
   Halo edge{};
-  load_segment<Op, S, VEC, false>(op, row, t0, T, lane, R, edge);
+  load_segment<Op, S, VEC>(op, row, t0, T, lane, R, edge);
   float carry = row_carry(op, row, T);
   op.template prepare<S, VEC>(R, row, t0, T);
   const Halo h = neighbour<Op, S>(op, R, edge, lane, t0, T);
@@ -377,56 +356,23 @@ __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T,
   const float x_in = lane_input<FWD>(m, carry, lane, W);
   float xs[S];
   replay<FWD, S>(mul, add, x_in, xs);
-  if (active) op.template emit<S, VEC>(R, h, xs, x_in, row, t0, T, nullptr);
+  if (active) op.template emit<S, VEC>(R, h, xs, x_in, row, t0, T);
 }
 
 // ---------------------------------------------------------------------------------------
-// Long rows: rows split into tiles of NTD*S steps chained by a decoupled look-back.
-//
-// Persistent and software-pipelined: a workgroup keeps drawing tiles from its slot's
-// ticket counter (slot = blockIdx % nslots, nslots = min(E, 64); each slot hands out the
-// tiles of rows r = slot (mod nslots) in scan order) and works one tile ahead.  A
-// workgroup only ever waits on tiles with smaller tickets of its own slot, whose holders
-// are running, so any grid size makes progress.  Launch: grid = nslots * wgs_per_slot,
-// block = NTD + 64.
-//
-// Roles.  Vector loads of one wave complete in order, so a wave that polls status words
-// behind its own prefetch waits for the prefetch too.  Wave 0 is therefore a coordinator
-// that holds no tile data: it draws tickets, publishes the tile's status and looks back,
-// and its memory queue holds nothing else.  The NTD/64 data waves prefetch the next tile,
-// scan the current one, and replay and store it once the coordinator has its carry; all
-// their loads and stores are unconditional (clamped, or sent to the sink), so the next
-// tile's loads stay in flight across the look-back.
+// Long rows: the decoupled look-back.
 // ---------------------------------------------------------------------------------------
 __host__ __device__ inline int lookback_slots(int64_t E) { return E < kSlots ? (int)E : kSlots; }
-
-// Last act of a look-back workgroup: count it finished in its slot; the slot's last one
-// leaves the slot at rest, and the last slot to finish advances the epoch.
-__device__ __forceinline__ void lookback_finish(uint64_t* ws, uint64_t* sc, uint64_t wgs_per_slot,
-                                                int nslots, uint32_t epoch) {
-  const uint64_t fin =
-      __hip_atomic_fetch_add(sc + 16, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (fin == wgs_per_slot - 1) {
-    atomic_st(sc + 0, 0);
-    atomic_st(sc + 16, 0);
-    const uint64_t slots_done =
-        __hip_atomic_fetch_add(ws + 1, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (slots_done == (uint64_t)nslots - 1) {
-      atomic_st(ws + 1, 0);
-      atomic_st(ws + 2, (uint64_t)((epoch + 1) & kEpochMask));
-    }
-  }
-}
 
 __device__ __forceinline__ uint64_t draw_ticket(uint64_t* sc) {
   return __hip_atomic_fetch_add(sc, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// s_waitcnt vmcnt(0): the coordinator's own traffic is complete before its path rejoins
-// the data waves', so nothing it issued looks pending to the compiler afterwards.
+// s_waitcnt vmcnt(0): the look-back wave's own traffic is complete before its path rejoins
+// the other waves', so nothing it issued looks pending to the compiler afterwards.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// Carry entering tile k of `row` (the coordinator wave, all 64 lanes): publish the tile's
+// Carry entering tile k of `row` (one wave, all 64 lanes): publish the tile's
 // map and look back.  Predecessors are read 64 at a time (lane i <-> i+1 tiles away).
 // Once the nearest published inclusive value X has only aggregates between it and this
 // tile, they are applied to X one at a time, nearest last, so every published X equals the
@@ -498,130 +444,190 @@ __device__ __forceinline__ float tile_carry(Affine tm, float row_c, int64_t row,
   return c;
 }
 
-template <class Op, int NTD, int S, bool VEC>
-__global__ __launch_bounds__(NTD + kWave) void lookback_kernel(const Op op, int64_t E, int T,
-                                                               int tiles_per_row,
-                                                               uint64_t* __restrict__ ws) {
+// ---------------------------------------------------------------------------------------
+// Long rows, one tile per workgroup.
+//
+// Tile = NT threads x Q segments of 4 steps, held in registers.  The segments are strided
+// by the wave so that every vector load and store of a wave covers 1 KB of consecutive
+// memory: in wave w's chunk of Q*256 steps, segment q of lane l starts at step
+// (q*64 + l)*4.  Scan order within the chunk is therefore (q, lane, step): each of the Q
+// "segment rows" is scanned across the 64 lanes, and the rows are chained in order.
+//
+// A workgroup draws one ticket from its slot's counter (slot = blockIdx % nslots), which
+// names the tile (row, position) in scan order; it loads and scans the tile, wave 0
+// publishes the tile's map and looks back for the carry, then every thread replays and
+// stores.  A tile only waits on earlier tickets of its slot, held by workgroups that have
+// started, so any residency makes progress.  Large tiles keep the look-back chain along a
+// row short for the shapes this path serves (a few rows of 10^4..10^6 steps).
+// Launch: grid = nslots * (tiles of the fullest slot), block = NT.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ float lane_bcast(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ Halo2 lane_bcast(Halo2 h, int l) { return Halo2{lane_bcast(h.a, l), lane_bcast(h.b, l)}; }
+__device__ __forceinline__ NoHalo lane_bcast(NoHalo h, int) { return h; }
+
+constexpr int kSeg = 4;  // steps per segment of the long-row path
+
+template <class Op, int NT, int Q, bool VEC>
+__global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T, int tiles_per_row,
+                                                   uint64_t* __restrict__ ws) {
   constexpr bool FWD = Op::kForward;
-  constexpr int NWD = NTD / kWave;  // data waves
-  static_assert(NTD % kWave == 0, "whole data waves");
-  using Regs = typename Op::template Regs<S>;
+  constexpr int NW = NT / kWave;
+  constexpr int WSTEPS = Q * kWave * kSeg;  // steps per wave chunk
+  static_assert(NT % kWave == 0, "whole waves");
+  using Regs = typename Op::template Regs<kSeg>;
   using Halo = typename Op::Halo;
-  // wave aggregates, double-buffered by tile parity: a data wave may write the next tile's
-  // while a slower one still reads this tile's
-  __shared__ float s_mul[2][NWD], s_add[2][NWD];
+  constexpr bool HAS_HALO = !std::is_same<Halo, NoHalo>::value;
+  __shared__ float s_mul[NW], s_add[NW];
   __shared__ float s_carry;
-  __shared__ uint64_t s_q;  // the workgroup's next ticket
+  __shared__ uint64_t s_q;
+  __shared__ uint32_t s_epoch;
 
   const int tid = threadIdx.x;
   const int lane = __lane_id();
-  // wave-uniform as far as the compiler knows: role branches become scalar branches, and a
-  // wave never executes (or waits in) the other role's code
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const bool coord = wave == 0;
-  const int wd = wave - 1;      // data wave index
-  const int d = tid - kWave;    // data thread index
   const int nslots = lookback_slots(E);
   const int slot = (int)(blockIdx.x % (unsigned)nslots);
   const uint64_t wgs_per_slot = gridDim.x / (unsigned)nslots;
   uint64_t* sc = ws + kHeaderWords + kSlotWords * slot;
   const int64_t rows_in_slot = (E - slot + nslots - 1) / nslots;
   const uint64_t tiles_in_slot = (uint64_t)rows_in_slot * (uint64_t)tiles_per_row;
-  float* const sink = reinterpret_cast<float*>(ws + kSinkOffset);
 
-  uint32_t epoch = 0;
-  if (coord) {
-    if (lane == 0) s_q = draw_ticket(sc);
-    epoch = (uint32_t)atomic_ld(ws + 2) & kEpochMask;
+  if (tid == 0) {
+    s_q = draw_ticket(sc);
+    s_epoch = (uint32_t)atomic_ld(ws + 2) & kEpochMask;
   }
   __syncthreads();
-  uint64_t q = s_q;
-  // every workgroup draws exactly one ticket beyond the slot's tiles
-  if (tid == 0 && q >= tiles_in_slot + wgs_per_slot) atomic_st(ws + 3, (uint64_t)1);  // not at rest
-
-  // ticket -> (row, tile index in scan order -> tile position k)
-  auto decode = [&](uint64_t qq, int64_t& row, int& k) {
-    const int64_t lr = (int64_t)(qq / (uint64_t)tiles_per_row);
-    const int j = (int)(qq - (uint64_t)lr * tiles_per_row);
-    row = slot + (int64_t)nslots * lr;
-    k = FWD ? j : tiles_per_row - 1 - j;
-  };
-
-  // The two roles run separate loops over the same ticket sequence and meet at two
-  // barriers per tile: A (the data waves' aggregates and the next ticket are in LDS) and B
-  // (the carry is in LDS).  Neither loop contains the other's memory traffic.  Tickets are
-  // drawn one tile ahead, at the top of the coordinator's iteration, so a workgroup holds
-  // at most one tile it has not started (a deeper lead lets one slow tile hold up the
-  // tiles after it); the next tile's loads are issued right after A and stay in flight
-  // across the look-back and this tile's stores.
-  int64_t row = 0;
-  int k = 0;
-  if (q < tiles_in_slot) decode(q, row, k);
-  if (coord) {
-    for (int parity = 0; q < tiles_in_slot; parity ^= 1) {
-      uint64_t qn = ~(uint64_t)0;
-      if (lane == 0) qn = draw_ticket(sc);
-      const bool first = FWD ? (k == 0) : (k == tiles_per_row - 1);
-      const float rc = first ? row_carry(op, row, T) : 0.f;
-      wait_vmem();
-      if (lane == 0) s_q = qn;
-      __syncthreads();  // A
-      Affine tm{1.f, 0.f};
-      if constexpr (FWD) {
-        for (int v = 0; v < NWD; ++v) tm = compose(Affine{s_mul[parity][v], s_add[parity][v]}, tm);
-      } else {
-        for (int v = NWD - 1; v >= 0; --v) tm = compose(Affine{s_mul[parity][v], s_add[parity][v]}, tm);
-      }
-      const uint64_t q_next = s_q;
-      const float c = tile_carry<FWD>(tm, rc, row, k, tiles_per_row, epoch, ws, lane);
-      if (lane == 0) s_carry = c;
-      __syncthreads();  // B
-      q = q_next;
-      if (q < tiles_in_slot) decode(q, row, k);
-    }
-    if (lane == 0) lookback_finish(ws, sc, wgs_per_slot, nslots, epoch);
-    return;
+  const uint64_t q_t = s_q;
+  const uint32_t epoch = s_epoch;
+  // Each workgroup draws exactly one ticket, so the slot's last drawer is known the moment
+  // it draws: having read the epoch (above), every workgroup counts itself drawn, and the
+  // one that completes the count resets the slot (and, last of all slots, advances the
+  // epoch) when it finishes.  The count's result is only read at the end, by which time
+  // it has returned, so no workgroup waits on an atomic on its way out.
+  uint64_t drawn = 0;
+  if (tid == 0) {
+    if (q_t >= wgs_per_slot) atomic_st(ws + 3, (uint64_t)1);  // counters were not at rest
+    drawn = __hip_atomic_fetch_add(sc + 16, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
-  Regs cur;
-  Halo ecur{};
-  if (q < tiles_in_slot) load_segment<Op, S, VEC, true>(op, row, (k * NTD + d) * S, T, lane, cur, ecur);
-  for (int parity = 0; q < tiles_in_slot; parity ^= 1) {
-    const int t0 = (k * NTD + d) * S;
-    op.template prepare<S, VEC>(cur, row, t0, T);
-    const Halo h = neighbour<Op, S>(op, cur, ecur, lane, t0, T);
-    float mul[S], add[S];
-    op.template coef<S>(cur, h, row, t0, T, mul, add);
-    const Affine m = group_scan<FWD>(fold_segment<FWD, S>(mul, add), kWave);
-    if (lane == (FWD ? kWave - 1 : 0)) {
-      s_mul[parity][wd] = m.mul;
-      s_add[parity][wd] = m.add;
+  if (q_t < tiles_in_slot) {
+    const int64_t lr = (int64_t)(q_t / (uint64_t)tiles_per_row);
+    const int j = (int)(q_t - (uint64_t)lr * tiles_per_row);
+    const int64_t row = slot + (int64_t)nslots * lr;
+    const int k = FWD ? j : tiles_per_row - 1 - j;
+    const int wbase = (k * NW + wave) * WSTEPS;  // first step of this wave's chunk
+
+    // loads: Q segments, plus the one neighbour step outside the chunk
+    Regs R[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) op.template load<kSeg, VEC>(row, wbase + (q * kWave + lane) * kSeg, T, R[q]);
+    Halo edge{};
+    if constexpr (HAS_HALO) {
+      if constexpr (FWD) {
+        if (lane == 0 && wbase > 0) edge = op.halo_load(row, clamp_step(wbase - 1, T), T);
+      } else {
+        if (lane == kWave - 1 && wbase + WSTEPS < T) edge = op.halo_load(row, wbase + WSTEPS, T);
+      }
     }
-    __syncthreads();  // A
-    // prefetch the next tile (this one again when there is none)
-    const uint64_t qn = s_q;
-    int64_t nrow = row;
-    int nk = k;
-    if (qn < tiles_in_slot) decode(qn, nrow, nk);
-    Regs nxt;
-    Halo enxt{};
-    load_segment<Op, S, VEC, true>(op, nrow, (nk * NTD + d) * S, T, lane, nxt, enxt);
-    __syncthreads();  // B
+    const bool first = FWD ? (k == 0) : (k == tiles_per_row - 1);
+    const float rc = (first && wave == 0) ? row_carry(op, row, T) : 0.f;
+
+#pragma unroll
+    for (int q = 0; q < Q; ++q) op.template prepare<kSeg, VEC>(R[q], row, wbase + (q * kWave + lane) * kSeg, T);
+
+    // neighbour step of each segment: the adjacent lane, the next/previous segment row's
+    // edge lane, or the edge load
+    Halo h[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      if constexpr (HAS_HALO) {
+        if constexpr (FWD) {
+          const Halo up = shfl_prev(op.template export_last<kSeg>(R[q]));
+          const Halo wrap = q > 0 ? lane_bcast(op.template export_last<kSeg>(R[q > 0 ? q - 1 : 0]), kWave - 1) : edge;
+          h[q] = lane == 0 ? wrap : up;
+        } else {
+          const Halo dn = shfl_next(op.template export_first<kSeg>(R[q]));
+          const Halo wrap = q + 1 < Q ? lane_bcast(op.template export_first<kSeg>(R[q + 1 < Q ? q + 1 : q]), 0) : edge;
+          h[q] = lane == kWave - 1 ? wrap : dn;
+        }
+      }
+    }
+
+    float mul[Q][kSeg], add[Q][kSeg];
+    Affine m[Q];
+    Affine rowagg[Q];  // map of each segment row (wave-uniform)
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      op.template coef<kSeg>(R[q], h[q], row, wbase + (q * kWave + lane) * kSeg, T, mul[q], add[q]);
+      m[q] = group_scan<FWD>(fold_segment<FWD, kSeg>(mul[q], add[q]), kWave);
+      const int src = FWD ? kWave - 1 : 0;
+      rowagg[q] = Affine{lane_bcast(m[q].mul, src), lane_bcast(m[q].add, src)};
+    }
+    // the chunk's map: segment rows composed in scan order
+    Affine wm{1.f, 0.f};
+    if constexpr (FWD) {
+#pragma unroll
+      for (int q = 0; q < Q; ++q) wm = compose(rowagg[q], wm);
+    } else {
+#pragma unroll
+      for (int q = Q - 1; q >= 0; --q) wm = compose(rowagg[q], wm);
+    }
+    if (lane == 0) {
+      s_mul[wave] = wm.mul;
+      s_add[wave] = wm.add;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      Affine tm{1.f, 0.f};
+      if constexpr (FWD) {
+        for (int v = 0; v < NW; ++v) tm = compose(Affine{s_mul[v], s_add[v]}, tm);
+      } else {
+        for (int v = NW - 1; v >= 0; --v) tm = compose(Affine{s_mul[v], s_add[v]}, tm);
+      }
+      const float c = tile_carry<FWD>(tm, rc, row, k, tiles_per_row, epoch, ws, lane);
+      if (lane == 0) s_carry = c;
+    }
+    __syncthreads();
+    // value entering this wave's chunk, then each segment row, then each lane
     float carry = s_carry;
     if constexpr (FWD) {
-      for (int v = 0; v < wd; ++v) carry = fmaf(s_mul[parity][v], carry, s_add[parity][v]);
+      for (int v = 0; v < wave; ++v) carry = fmaf(s_mul[v], carry, s_add[v]);
     } else {
-      for (int v = NWD - 1; v > wd; --v) carry = fmaf(s_mul[parity][v], carry, s_add[parity][v]);
+      for (int v = NW - 1; v > wave; --v) carry = fmaf(s_mul[v], carry, s_add[v]);
     }
-    const float x_in = lane_input<FWD>(m, carry, lane, kWave);
-    float xs[S];
-    replay<FWD, S>(mul, add, x_in, xs);
-    op.template emit<S, VEC>(cur, h, xs, x_in, row, t0, T, sink);
-    cur = nxt;
-    ecur = enxt;
-    q = qn;
-    row = nrow;
-    k = nk;
+    float rowin[Q];
+    if constexpr (FWD) {
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        rowin[q] = carry;
+        carry = fmaf(rowagg[q].mul, carry, rowagg[q].add);
+      }
+    } else {
+#pragma unroll
+      for (int q = Q - 1; q >= 0; --q) {
+        rowin[q] = carry;
+        carry = fmaf(rowagg[q].mul, carry, rowagg[q].add);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const float x_in = lane_input<FWD>(m[q], rowin[q], lane, kWave);
+      float xs[kSeg];
+      replay<FWD, kSeg>(mul[q], add[q], x_in, xs);
+      op.template emit<kSeg, VEC>(R[q], h[q], xs, x_in, row, wbase + (q * kWave + lane) * kSeg, T);
+    }
+  }
+  if (tid == 0 && drawn == wgs_per_slot - 1) {
+    atomic_st(sc + 0, 0);
+    atomic_st(sc + 16, 0);
+    const uint64_t slots_done =
+        __hip_atomic_fetch_add(ws + 1, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (slots_done == (uint64_t)nslots - 1) {
+      atomic_st(ws + 1, 0);
+      atomic_st(ws + 2, (uint64_t)((epoch + 1) & kEpochMask));
+    }
   }
 }
 

@@ -7,9 +7,8 @@
 // cites the lines it reproduces.  Padding steps (t >= T) are the identity map.
 //
 // Optional operands that change which arrays are read (truncations, TD(lambda)'s next
-// values) are template parameters, and every load is unconditional (load_seg clamps into
-// the row; absent per-row values are read from g_zero): the look-back kernel's data
-// waves keep a prefetch in flight only if no load sits under a runtime branch.
+// values) are template parameters; loads are clamped into the row and absent per-row
+// values are read from g_zero.
 #pragma once
 #include "rlk_engine.hpp"
 
@@ -30,6 +29,9 @@ __device__ __forceinline__ void fill_regs(float (&v)[S], float x) {
 template <bool TRUNC>
 struct GaeOp {
   static constexpr bool kForward = false;
+  // long-row tiles: threads per workgroup and most 4-step segments per thread that stay
+  // in registers (no spills at 1024 threads, whose cap is 128 VGPRs)
+  static constexpr int kLongThreads = 1024, kLongMaxSegments = 4;
   using Halo = float;  // values[t+1]
   const float* r;
   const float* v;
@@ -83,8 +85,8 @@ struct GaeOp {
 
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>&, float, const float (&xs)[S], float, int64_t row, int t0,
-                       int T, float* sink) const {
-    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, sink);
+                       int T) const {
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
   }
 };
 
@@ -102,6 +104,7 @@ struct GaeOp {
 template <bool TRUNC>
 struct VtraceOp {
   static constexpr bool kForward = false;
+  static constexpr int kLongThreads = 1024, kLongMaxSegments = 2;
   using Halo = float;  // values[t+1]
   const float* lpt;
   const float* lpb;
@@ -171,7 +174,7 @@ struct VtraceOp {
 
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>& R, float vh, const float (&xs)[S], float x_next, int64_t row,
-                       int t0, int T, float* sink) const {
+                       int t0, int T) const {
     float tg[S], ad[S];
 #pragma unroll
     for (int i = 0; i < S; ++i) tg[i] = xs[i] + R.v[i];
@@ -182,8 +185,8 @@ struct VtraceOp {
       ad[i] = R.rho[i] * (fmaf(gamma * nt, 1.f - R.te[i], R.r[i]) - R.v[i]);
     }
     const int64_t o = row * (int64_t)T;
-    store_seg<S, VEC>(targets + o, t0, T, tg, sink);
-    store_seg<S, VEC>(adv + o, t0, T, ad, sink);
+    store_seg<S, VEC>(targets + o, t0, T, tg);
+    store_seg<S, VEC>(adv + o, t0, T, ad);
   }
 };
 
@@ -198,6 +201,7 @@ struct VtraceOp {
 template <int NA, bool TRUNC>
 struct RetraceOp {
   static constexpr bool kForward = false;
+  static constexpr int kLongThreads = 512, kLongMaxSegments = 2;  // 256 VGPRs: the A-wide rows
   using Halo = Halo2;  // {c[t+1], q[t+1]}
   const float* pi;     // [E, T, A]
   const float* mu;     // [E, T]
@@ -234,8 +238,7 @@ struct RetraceOp {
   }
 
   // Unlike the other ops, the [S, A] action blocks are reduced to (rho, c, E_pi[Q']) here,
-  // at load time, to bound the registers a prefetched tile holds; a Retrace prefetch is
-  // therefore waited for early.
+  // at load time, so a segment holds three values per step instead of 2A.
   template <int S, bool VEC>
   __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
     const int64_t o = row * (int64_t)T;
@@ -305,7 +308,7 @@ struct RetraceOp {
 
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>& R, Halo2 h, const float (&xs)[S], float x_next, int64_t row,
-                       int t0, int T, float* sink) const {
+                       int t0, int T) const {
     float tg[S], ad[S];
 #pragma unroll
     for (int i = 0; i < S; ++i) tg[i] = xs[i] + R.q[i];
@@ -316,8 +319,8 @@ struct RetraceOp {
       ad[i] = R.rho[i] * (fmaf(gamma * nxt, 1.f - R.te[i], R.r[i]) - R.q[i]);
     }
     const int64_t o = row * (int64_t)T;
-    store_seg<S, VEC>(targets + o, t0, T, tg, sink);
-    store_seg<S, VEC>(adv + o, t0, T, ad, sink);
+    store_seg<S, VEC>(targets + o, t0, T, tg);
+    store_seg<S, VEC>(adv + o, t0, T, ad);
   }
 };
 
@@ -331,6 +334,7 @@ struct RetraceOp {
 template <bool NV, bool TRUNC>
 struct ReturnsOp {
   static constexpr bool kForward = false;
+  static constexpr int kLongThreads = 1024, kLongMaxSegments = (NV || TRUNC) ? 4 : 8;
   using Halo = NoHalo;
   const float* r;
   const float* nv;     // read iff NV
@@ -387,8 +391,8 @@ struct ReturnsOp {
 
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>&, NoHalo, const float (&xs)[S], float, int64_t row, int t0,
-                       int T, float* sink) const {
-    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, sink);
+                       int T) const {
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
   }
 };
 
@@ -402,6 +406,7 @@ struct ReturnsOp {
 // ------------------------------------------------------------------------------------------
 struct DoneGatedForwardOp {
   static constexpr bool kForward = true;
+  static constexpr int kLongThreads = 1024, kLongMaxSegments = 8;
   using Halo = float;  // done[t-1]
   const float* x;
   const float* dones;
@@ -445,8 +450,8 @@ struct DoneGatedForwardOp {
 
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>&, float, const float (&xs)[S], float, int64_t row, int t0,
-                       int T, float* sink) const {
-    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, sink);
+                       int T) const {
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
   }
 };
 
@@ -457,6 +462,7 @@ struct DoneGatedForwardOp {
 template <bool FWD>
 struct AffineScanOp {
   static constexpr bool kForward = FWD;
+  static constexpr int kLongThreads = 1024, kLongMaxSegments = 8;
   using Halo = NoHalo;
   const float* u;
   const float* v;
@@ -488,8 +494,8 @@ struct AffineScanOp {
   __device__ const float* row_carry_src(int64_t row, int) const { return carry ? carry + row : nullptr; }
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>&, NoHalo, const float (&xs)[S], float, int64_t row, int t0,
-                       int T, float* sink) const {
-    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, sink);
+                       int T) const {
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
   }
 };
 

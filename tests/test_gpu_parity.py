@@ -87,6 +87,17 @@ def test_prefix_sum_boundaries(boundary, seed_row, shape, device):
     _check("prefix_sum", inp, params, device, 1e-5, 1e-4, f"prefix {boundary}{shape}")
 
 
+@pytest.mark.parametrize("op", ["eligibility_traces", "prefix_sum", "forward_scan"])
+@pytest.mark.parametrize("shape", [(3, 1100), (2, 1537), (5, 2047)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_forward_scans_with_padding_waves(op, shape, device):
+    """Rows whose last wave starts beyond seq_len (a padding wave): its neighbour-step read
+    stays inside the row, and results match the oracle."""
+    inp, params = make_inputs(op, *shape, seed=13, boot="row")
+    if op == "prefix_sum":
+        params = {"boundary": "ends_at"}
+    _check(op, inp, params, device, 1e-5, 1e-5, f"{op}{shape}")
+
+
 # ---------------------------------------------------------------------------------------
 # long rows: the decoupled look-back path
 # ---------------------------------------------------------------------------------------
