@@ -16,7 +16,8 @@ Printed JSON (one line, stdout):
                  (28 B/elem: 5 reads + 2 writes) / its average launch duration, timed with
                  HIP events on the launch stream around batches of launches that the GPU
                  runs back to back (queued behind a GPU spin), vs 8 TB/s; traffic = HBM
-                 bytes per launch measured by rocprofv3 counters (profiles/traffic_4096x128.json)
+                 bytes per launch measured by rocprofv3 counters
+                 (profiles/traffic_baseline_configs.json)
   graph_replay   the same steps replayed from a captured HIP graph (no host work per call)
   ops            per-op device time, Gelem/s, GB/s and %-of-peak for both kernels
   configs        the same figures for every BASELINE configuration (C1-C5,
@@ -88,13 +89,14 @@ def run_vtrace(rl, s):
                              last_value=s["last_value"])
 
 
-def measured_traffic(op):
-    """HBM bytes per launch of `op`'s kernel from the committed rocprofv3 counter passes
-    (FETCH_SIZE and WRITE_SIZE scaled by a known-size copy), or None if absent."""
-    path = os.path.join(ROOT, "profiles", "traffic_4096x128.json")
+def measured_traffic(config):
+    """HBM bytes per launch of `config`'s kernel (a name of tests/baseline_configs.py) from
+    the committed rocprofv3 counter passes (FETCH_SIZE and WRITE_SIZE scaled by a known-size
+    copy), or None if absent."""
+    path = os.path.join(ROOT, "profiles", "traffic_baseline_configs.json")
     try:
         with open(path) as f:
-            return json.load(f)["traffic_bytes_per_launch"][op]
+            return json.load(f)["traffic_bytes_per_launch"][config]
     except (OSError, KeyError, ValueError):
         return None
 
@@ -168,7 +170,8 @@ def time_configs(torch, names, min_launches=200, batch=50):
         res[name] = {"op": op, "shape": [n_env, n_t], "device_us": round(us, 3),
                      "gelem_s": round(n_env * n_t / (us * 1e-6) / 1e9, 2), "gb_s": round(gbs, 1),
                      "pct_peak": round(100 * gbs / PEAK_GBS, 2), "bytes_per_elem": bpe,
-                     "target_pct": (100 * bc.TARGETS[name]) if name in bc.TARGETS else None}
+                     "target_pct": (100 * bc.TARGETS[name]) if name in bc.TARGETS else None,
+                     "traffic": measured_traffic(name)}
         log(f"[bench] {name}: {us:.2f} us/launch, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of 8 TB/s)")
     torch.cuda.empty_cache()
     return res
@@ -307,7 +310,7 @@ def main(argv=None):
     dom = max(ops, key=lambda k: ops[k]["device_us"])
     roofline = {"bound": "hbm", "kernel": dom, "achieved": ops[dom]["gb_s"], "peak": PEAK_GBS,
                 "unit": "GB/s", "frac": round(ops[dom]["gb_s"] / PEAK_GBS, 4),
-                "traffic": measured_traffic(dom)}
+                "traffic": measured_traffic({"gae": "C2_gae_4096x128", "vtrace": "C3_vtrace_4096x128"}[dom])}
 
     graph_ms = time_graph_steps(torch, rl_triton, sets, a.steps)
     log(f"[bench] graph-replayed step: {graph_ms * 1e3:.2f} us "
