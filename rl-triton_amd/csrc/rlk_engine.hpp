@@ -222,43 +222,6 @@ __device__ __forceinline__ uint64_t pack(uint32_t tag, float v) {
 // Segment pieces shared by both kernels.
 // ---------------------------------------------------------------------------------------
 
-// Issue the loads of this thread's segment, and of the neighbour step for the edge lane
-// whose neighbour lives outside its wave, together: the edge lane must not pay a second
-// memory round trip after its segment has arrived.
-template <class Op, int S, bool VEC>
-__device__ __forceinline__ void load_segment(const Op& op, int64_t row, int t0, int T, int lane,
-                                             typename Op::template Regs<S>& R,
-                                             typename Op::Halo& edge) {
-  if constexpr (!std::is_same<typename Op::Halo, NoHalo>::value) {
-    if constexpr (Op::kForward) {
-      // a padding wave (t0 > T) still reads inside the row; its value is never used
-      if (lane == 0 && t0 > 0) edge = op.halo_load(row, clamp_step(t0 - 1, T), T);
-    } else {
-      if (lane == kWave - 1 && t0 + S < T) edge = op.halo_load(row, t0 + S, T);
-    }
-  }
-  op.template load<S, VEC>(row, t0, T, R);
-}
-
-// The neighbour step's data: from the adjacent lane, or the edge load.
-template <class Op, int S>
-__device__ __forceinline__ typename Op::Halo neighbour(const Op& op,
-                                                       const typename Op::template Regs<S>& R,
-                                                       typename Op::Halo edge, int lane, int t0,
-                                                       int T) {
-  typename Op::Halo h{};
-  if constexpr (!std::is_same<typename Op::Halo, NoHalo>::value) {
-    if constexpr (Op::kForward) {
-      h = shfl_prev(op.template export_last<S>(R));
-      if (lane == 0 && t0 > 0) h = edge;
-    } else {
-      h = shfl_next(op.template export_first<S>(R));
-      if (lane == kWave - 1 && t0 + S < T) h = edge;
-    }
-  }
-  return h;
-}
-
 // The segment's map: steps composed in scan order.
 template <bool FWD, int S>
 __device__ __forceinline__ Affine fold_segment(const float (&mul)[S], const float (&add)[S]) {
@@ -305,8 +268,62 @@ __device__ __forceinline__ float lane_input(Affine m, float carry, int lane, int
 }
 
 // ---------------------------------------------------------------------------------------
+// Cross-lane moves by DPP (gfx9 data-parallel primitives): a VALU modifier, no trip through
+// the LDS crossbar.  update_dpp(old, src): a lane whose source lane is invalid, or whose
+// row is masked off, keeps `old`.
+// ---------------------------------------------------------------------------------------
+constexpr int kDppRowShr = 0x110;     // + n: lane i <- lane i-n within its row of 16
+constexpr int kDppWaveShr1 = 0x138;   // lane i <- lane i-1 across the wave
+constexpr int kDppRowBcast15 = 0x142; // lane 15 of each row -> the next row
+constexpr int kDppRowBcast31 = 0x143; // lane 31 -> rows 2 and 3
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp(float src, float old) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(src), CTRL,
+                                                    ROW_MASK, 0xf, false));
+}
+
+// The previous lane's value (lane 0 keeps its own).
+__device__ __forceinline__ float lane_prev(float v) { return dpp<kDppWaveShr1, 0xf>(v, v); }
+__device__ __forceinline__ Halo2 lane_prev(Halo2 h) { return Halo2{lane_prev(h.a), lane_prev(h.b)}; }
+__device__ __forceinline__ NoHalo lane_prev(NoHalo h) { return h; }
+
+template <int D>
+__device__ __forceinline__ Affine scan_step_rows(Affine m, int li) {
+  float pm = dpp<kDppRowShr + D, 0xf>(m.mul, 1.f);
+  float pa = dpp<kDppRowShr + D, 0xf>(m.add, 0.f);
+  if (li < D) {  // groups narrower than a DPP row: the source lane is in another group
+    pm = 1.f;
+    pa = 0.f;
+  }
+  return compose(m, Affine{pm, pa});
+}
+
+// Inclusive scan of affine maps towards higher lanes, in groups of W lanes (W a power of
+// two <= 64, wave-uniform): lane i ends up with m_i o m_{i-1} o ... o m_0 of its group.
+// Kogge-Stone within rows of 16 lanes, then row_bcast to join rows.
+__device__ __forceinline__ Affine lane_scan(Affine m, int W) {
+  const int li = __lane_id() & (W - 1);
+  if (W > 1) m = scan_step_rows<1>(m, li);
+  if (W > 2) m = scan_step_rows<2>(m, li);
+  if (W > 4) m = scan_step_rows<4>(m, li);
+  if (W > 8) m = scan_step_rows<8>(m, li);
+  if (W > 16) m = compose(m, Affine{dpp<kDppRowBcast15, 0xa>(m.mul, 1.f), dpp<kDppRowBcast15, 0xa>(m.add, 0.f)});
+  if (W > 32) m = compose(m, Affine{dpp<kDppRowBcast31, 0xc>(m.mul, 1.f), dpp<kDppRowBcast31, 0xc>(m.add, 0.f)});
+  return m;
+}
+
+// ---------------------------------------------------------------------------------------
 // Short rows: a workgroup of NT threads holds NT/L whole rows of L threads each
 // (L = 2^log2L, L*S >= T).  Launch: grid = ceil(E / (NT/L)).
+//
+// Lane space.  A row's segments are assigned to its L threads in scan order: in time order
+// for forward scans, reversed for backward scans (thread i of the row holds segment L-1-i).
+// Every scan then runs towards higher lanes whatever the op's direction, which is the
+// direction DPP row broadcasts go; memory accesses stay coalesced (lane order within a
+// wave does not matter to them).  The segment before a thread's own in scan order is in
+// the previous lane, so the neighbour step's data, and the value entering the segment,
+// come from there.
 // ---------------------------------------------------------------------------------------
 template <class Op, int NT, int S, bool VEC>
 __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T, int log2L) {
@@ -314,6 +331,7 @@ __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T,
   constexpr int NW = NT / kWave;
   using Regs = typename Op::template Regs<S>;
   using Halo = typename Op::Halo;
+  constexpr bool HAS_HALO = !std::is_same<Halo, NoHalo>::value;
   __shared__ float s_mul[NW], s_add[NW];
 
   const int tid = threadIdx.x;
@@ -321,39 +339,45 @@ __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T,
   const int wave = tid / kWave;
   const int L = 1 << log2L;
   const int W = L < kWave ? L : kWave;
-  const int li = tid & (L - 1);
+  const int li = tid & (L - 1);  // position in scan order
   const int64_t row_id = (int64_t)blockIdx.x * (NT >> log2L) + (tid >> log2L);
   const bool active = row_id < E;
   const int64_t row = active ? row_id : E - 1;  // idle lanes of the last workgroup read a real row
-  const int t0 = li * S;
+  const int t0 = (FWD ? li : L - 1 - li) * S;
 
-  Regs R;
+  // the first lane of a wave that is not the first of its row reads the neighbour step
   Halo edge{};
-  load_segment<Op, S, VEC>(op, row, t0, T, lane, R, edge);
+  if constexpr (HAS_HALO) {
+    if (lane == 0 && li > 0) edge = op.halo_load(row, clamp_step(FWD ? t0 - 1 : t0 + S, T), T);
+  }
+  Regs R;
+  op.template load<S, VEC>(row, t0, T, R);
   float carry = row_carry(op, row, T);
   op.template prepare<S, VEC>(R, row, t0, T);
-  const Halo h = neighbour<Op, S>(op, R, edge, lane, t0, T);
+  Halo h{};
+  if constexpr (HAS_HALO) {
+    if constexpr (FWD) h = lane_prev(op.template export_last<S>(R));
+    else h = lane_prev(op.template export_first<S>(R));
+    if (lane == 0) h = edge;  // unused when li == 0: the row's first segment in scan order
+  }
 
   float mul[S], add[S];
   op.template coef<S>(R, h, row, t0, T, mul, add);
-  const Affine m = group_scan<FWD>(fold_segment<FWD, S>(mul, add), W);
+  const Affine m = lane_scan(fold_segment<FWD, S>(mul, add), W);
 
   if (L > kWave) {
     // rows spanning several waves: combine the wave aggregates of the row through LDS
-    if (lane == (FWD ? kWave - 1 : 0)) {
+    if (lane == kWave - 1) {
       s_mul[wave] = m.mul;
       s_add[wave] = m.add;
     }
     __syncthreads();
-    const int wpr = L / kWave;
-    const int first = (wave / wpr) * wpr, last = first + wpr - 1;
-    if constexpr (FWD) {
-      for (int v = first; v < wave; ++v) carry = fmaf(s_mul[v], carry, s_add[v]);
-    } else {
-      for (int v = last; v > wave; --v) carry = fmaf(s_mul[v], carry, s_add[v]);
-    }
+    const int first = (wave / (L / kWave)) * (L / kWave);
+    for (int v = first; v < wave; ++v) carry = fmaf(s_mul[v], carry, s_add[v]);
   }
-  const float x_in = lane_input<FWD>(m, carry, lane, W);
+  // value entering the segment: the previous lane's outgoing value, or the carry
+  float x_in = lane_prev(fmaf(m.mul, carry, m.add));
+  if ((li & (W - 1)) == 0) x_in = carry;
   float xs[S];
   replay<FWD, S>(mul, add, x_in, xs);
   if (active) op.template emit<S, VEC>(R, h, xs, x_in, row, t0, T);
