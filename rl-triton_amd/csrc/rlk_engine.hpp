@@ -143,40 +143,10 @@ __device__ __forceinline__ float row_carry(const Op& op, int64_t row, int T) {
   return src ? *src : 0.f;
 }
 
-// ---------------------------------------------------------------------------------------
-// Lane shuffles of a halo value (float or a small struct of floats).
-// ---------------------------------------------------------------------------------------
-__device__ __forceinline__ float shfl_next(float v) { return __shfl_down(v, 1, kWave); }
-__device__ __forceinline__ float shfl_prev(float v) { return __shfl_up(v, 1, kWave); }
-
+// A halo value of two floats (Retrace: c[t+1] and q[t+1]).
 struct Halo2 {
   float a, b;
 };
-__device__ __forceinline__ Halo2 shfl_next(Halo2 h) { return Halo2{shfl_next(h.a), shfl_next(h.b)}; }
-__device__ __forceinline__ Halo2 shfl_prev(Halo2 h) { return Halo2{shfl_prev(h.a), shfl_prev(h.b)}; }
-
-// Inclusive scan of affine maps across groups of W lanes (W a power of two <= 64).
-// Backward (FWD=false): lane i ends up with m_i o m_{i+1} o ... o m_{W-1} of its group.
-// Forward  (FWD=true):  lane i ends up with m_i o m_{i-1} o ... o m_0.
-template <bool FWD>
-__device__ __forceinline__ Affine group_scan(Affine m, int W) {
-  const int li = __lane_id() & (W - 1);
-  for (int d = 1; d < W; d <<= 1) {
-    float omul, oadd;
-    bool ok;
-    if constexpr (FWD) {
-      omul = __shfl_up(m.mul, d, W);
-      oadd = __shfl_up(m.add, d, W);
-      ok = li >= d;
-    } else {
-      omul = __shfl_down(m.mul, d, W);
-      oadd = __shfl_down(m.add, d, W);
-      ok = li + d < W;
-    }
-    if (ok) m = compose(m, Affine{omul, oadd});
-  }
-  return m;
-}
 
 // ---------------------------------------------------------------------------------------
 // Decoupled look-back status words.  Per tile two 64-bit words {tag:32 | value:32}:
@@ -250,23 +220,6 @@ __device__ __forceinline__ void replay(const float (&mul)[S], const float (&add)
   }
 }
 
-// The value entering each lane's segment, given the value entering its group of W lanes
-// (`carry`) and the lane's inclusive group-scan map `m`: the neighbour lane's outgoing value.
-template <bool FWD>
-__device__ __forceinline__ float lane_input(Affine m, float carry, int lane, int W) {
-  const float y = fmaf(m.mul, carry, m.add);
-  const int gl = lane & (W - 1);
-  float x_in;
-  if constexpr (FWD) {
-    x_in = __shfl_up(y, 1, kWave);
-    if (gl == 0) x_in = carry;
-  } else {
-    x_in = __shfl_down(y, 1, kWave);
-    if (gl == W - 1) x_in = carry;
-  }
-  return x_in;
-}
-
 // ---------------------------------------------------------------------------------------
 // Cross-lane moves by DPP (gfx9 data-parallel primitives): a VALU modifier, no trip through
 // the LDS crossbar.  update_dpp(old, src): a lane whose source lane is invalid, or whose
@@ -287,6 +240,14 @@ __device__ __forceinline__ float dpp(float src, float old) {
 __device__ __forceinline__ float lane_prev(float v) { return dpp<kDppWaveShr1, 0xf>(v, v); }
 __device__ __forceinline__ Halo2 lane_prev(Halo2 h) { return Halo2{lane_prev(h.a), lane_prev(h.b)}; }
 __device__ __forceinline__ NoHalo lane_prev(NoHalo h) { return h; }
+
+// The data of a segment that the next segment in scan order needs: its last step (forward
+// scans: done[t-1]) or its first step (backward scans: values[t+1], ...).
+template <class Op, int S>
+__device__ __forceinline__ typename Op::Halo scan_export(const Op& op, const typename Op::template Regs<S>& R) {
+  if constexpr (Op::kForward) return op.template export_last<S>(R);
+  else return op.template export_first<S>(R);
+}
 
 template <int D>
 __device__ __forceinline__ Affine scan_step_rows(Affine m, int li) {
@@ -356,8 +317,7 @@ __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T,
   op.template prepare<S, VEC>(R, row, t0, T);
   Halo h{};
   if constexpr (HAS_HALO) {
-    if constexpr (FWD) h = lane_prev(op.template export_last<S>(R));
-    else h = lane_prev(op.template export_first<S>(R));
+    h = lane_prev(scan_export<Op, S>(op, R));
     if (lane == 0) h = edge;  // unused when li == 0: the row's first segment in scan order
   }
 
@@ -474,8 +434,10 @@ __device__ __forceinline__ float tile_carry(Affine tm, float row_c, int64_t row,
 // Tile = NT threads x Q segments of 4 steps, held in registers.  The segments are strided
 // by the wave so that every vector load and store of a wave covers 1 KB of consecutive
 // memory: in wave w's chunk of Q*256 steps, segment q of lane l starts at step
-// (q*64 + l)*4.  Scan order within the chunk is therefore (q, lane, step): each of the Q
-// "segment rows" is scanned across the 64 lanes, and the rows are chained in order.
+// (q*64 + l)*4.  Like the short-row kernel the tile is laid out in lane space, so that
+// every scan runs towards higher lanes: for backward ops the waves, the segment rows and
+// the lanes are all taken in reverse.  Each of the Q segment rows is scanned across the 64
+// lanes by DPP, and the rows are chained in scan order.
 //
 // A workgroup draws one ticket from its slot's counter (slot = blockIdx % nslots), which
 // names the tile (row, position) in scan order; it loads and scans the tile, wave 0
@@ -541,41 +503,35 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
     const int j = (int)(q_t - (uint64_t)lr * tiles_per_row);
     const int64_t row = slot + (int64_t)nslots * lr;
     const int k = FWD ? j : tiles_per_row - 1 - j;
-    const int wbase = (k * NW + wave) * WSTEPS;  // first step of this wave's chunk
+    // lane space -> time: this wave's chunk, and the first step of segment row r
+    const int wbase = (k * NW + (FWD ? wave : NW - 1 - wave)) * WSTEPS;
+    const int lt = FWD ? lane : kWave - 1 - lane;
+    auto seg_t0 = [&](int r) { return wbase + ((FWD ? r : Q - 1 - r) * kWave + lt) * kSeg; };
 
-    // loads: Q segments, plus the one neighbour step outside the chunk
+    // loads: Q segments, plus the neighbour step before the chunk in scan order
     Regs R[Q];
 #pragma unroll
-    for (int q = 0; q < Q; ++q) op.template load<kSeg, VEC>(row, wbase + (q * kWave + lane) * kSeg, T, R[q]);
+    for (int r = 0; r < Q; ++r) op.template load<kSeg, VEC>(row, seg_t0(r), T, R[r]);
     Halo edge{};
     if constexpr (HAS_HALO) {
-      if constexpr (FWD) {
-        if (lane == 0 && wbase > 0) edge = op.halo_load(row, clamp_step(wbase - 1, T), T);
-      } else {
-        if (lane == kWave - 1 && wbase + WSTEPS < T) edge = op.halo_load(row, wbase + WSTEPS, T);
-      }
+      if (lane == 0 && (FWD ? wbase > 0 : wbase + WSTEPS < T))
+        edge = op.halo_load(row, clamp_step(FWD ? wbase - 1 : wbase + WSTEPS, T), T);
     }
     const bool first = FWD ? (k == 0) : (k == tiles_per_row - 1);
     const float rc = (first && wave == 0) ? row_carry(op, row, T) : 0.f;
 
 #pragma unroll
-    for (int q = 0; q < Q; ++q) op.template prepare<kSeg, VEC>(R[q], row, wbase + (q * kWave + lane) * kSeg, T);
+    for (int r = 0; r < Q; ++r) op.template prepare<kSeg, VEC>(R[r], row, seg_t0(r), T);
 
-    // neighbour step of each segment: the adjacent lane, the next/previous segment row's
-    // edge lane, or the edge load
+    // neighbour step of each segment (the one before it in scan order): the previous lane,
+    // lane 63 of the previous segment row, or the edge load
     Halo h[Q];
 #pragma unroll
-    for (int q = 0; q < Q; ++q) {
+    for (int r = 0; r < Q; ++r) {
       if constexpr (HAS_HALO) {
-        if constexpr (FWD) {
-          const Halo up = shfl_prev(op.template export_last<kSeg>(R[q]));
-          const Halo wrap = q > 0 ? lane_bcast(op.template export_last<kSeg>(R[q > 0 ? q - 1 : 0]), kWave - 1) : edge;
-          h[q] = lane == 0 ? wrap : up;
-        } else {
-          const Halo dn = shfl_next(op.template export_first<kSeg>(R[q]));
-          const Halo wrap = q + 1 < Q ? lane_bcast(op.template export_first<kSeg>(R[q + 1 < Q ? q + 1 : q]), 0) : edge;
-          h[q] = lane == kWave - 1 ? wrap : dn;
-        }
+        const Halo prev = lane_prev(scan_export<Op, kSeg>(op, R[r]));
+        const Halo wrap = r > 0 ? lane_bcast(scan_export<Op, kSeg>(op, R[r > 0 ? r - 1 : 0]), kWave - 1) : edge;
+        h[r] = lane == 0 ? wrap : prev;
       }
     }
 
@@ -583,21 +539,15 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
     Affine m[Q];
     Affine rowagg[Q];  // map of each segment row (wave-uniform)
 #pragma unroll
-    for (int q = 0; q < Q; ++q) {
-      op.template coef<kSeg>(R[q], h[q], row, wbase + (q * kWave + lane) * kSeg, T, mul[q], add[q]);
-      m[q] = group_scan<FWD>(fold_segment<FWD, kSeg>(mul[q], add[q]), kWave);
-      const int src = FWD ? kWave - 1 : 0;
-      rowagg[q] = Affine{lane_bcast(m[q].mul, src), lane_bcast(m[q].add, src)};
+    for (int r = 0; r < Q; ++r) {
+      op.template coef<kSeg>(R[r], h[r], row, seg_t0(r), T, mul[r], add[r]);
+      m[r] = lane_scan(fold_segment<FWD, kSeg>(mul[r], add[r]), kWave);
+      rowagg[r] = Affine{lane_bcast(m[r].mul, kWave - 1), lane_bcast(m[r].add, kWave - 1)};
     }
     // the chunk's map: segment rows composed in scan order
     Affine wm{1.f, 0.f};
-    if constexpr (FWD) {
 #pragma unroll
-      for (int q = 0; q < Q; ++q) wm = compose(rowagg[q], wm);
-    } else {
-#pragma unroll
-      for (int q = Q - 1; q >= 0; --q) wm = compose(rowagg[q], wm);
-    }
+    for (int r = 0; r < Q; ++r) wm = compose(rowagg[r], wm);
     if (lane == 0) {
       s_mul[wave] = wm.mul;
       s_add[wave] = wm.add;
@@ -605,42 +555,22 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
     __syncthreads();
     if (wave == 0) {
       Affine tm{1.f, 0.f};
-      if constexpr (FWD) {
-        for (int v = 0; v < NW; ++v) tm = compose(Affine{s_mul[v], s_add[v]}, tm);
-      } else {
-        for (int v = NW - 1; v >= 0; --v) tm = compose(Affine{s_mul[v], s_add[v]}, tm);
-      }
+      for (int v = 0; v < NW; ++v) tm = compose(Affine{s_mul[v], s_add[v]}, tm);
       const float c = tile_carry<FWD>(tm, rc, row, k, tiles_per_row, epoch, ws, lane);
       if (lane == 0) s_carry = c;
     }
     __syncthreads();
     // value entering this wave's chunk, then each segment row, then each lane
     float carry = s_carry;
-    if constexpr (FWD) {
-      for (int v = 0; v < wave; ++v) carry = fmaf(s_mul[v], carry, s_add[v]);
-    } else {
-      for (int v = NW - 1; v > wave; --v) carry = fmaf(s_mul[v], carry, s_add[v]);
-    }
-    float rowin[Q];
-    if constexpr (FWD) {
+    for (int v = 0; v < wave; ++v) carry = fmaf(s_mul[v], carry, s_add[v]);
 #pragma unroll
-      for (int q = 0; q < Q; ++q) {
-        rowin[q] = carry;
-        carry = fmaf(rowagg[q].mul, carry, rowagg[q].add);
-      }
-    } else {
-#pragma unroll
-      for (int q = Q - 1; q >= 0; --q) {
-        rowin[q] = carry;
-        carry = fmaf(rowagg[q].mul, carry, rowagg[q].add);
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < Q; ++q) {
-      const float x_in = lane_input<FWD>(m[q], rowin[q], lane, kWave);
+    for (int r = 0; r < Q; ++r) {
+      float x_in = lane_prev(fmaf(m[r].mul, carry, m[r].add));
+      if (lane == 0) x_in = carry;
+      carry = fmaf(rowagg[r].mul, carry, rowagg[r].add);
       float xs[kSeg];
-      replay<FWD, kSeg>(mul[q], add[q], x_in, xs);
-      op.template emit<kSeg, VEC>(R[q], h[q], xs, x_in, row, wbase + (q * kWave + lane) * kSeg, T);
+      replay<FWD, kSeg>(mul[r], add[r], x_in, xs);
+      op.template emit<kSeg, VEC>(R[r], h[r], xs, x_in, row, seg_t0(r), T);
     }
   }
   if (tid == 0 && drawn == wgs_per_slot - 1) {
