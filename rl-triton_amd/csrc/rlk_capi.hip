@@ -11,6 +11,7 @@ namespace {
 // Launch geometry.
 constexpr int kNT = 256;          // short rows: threads per workgroup (4 wavefronts)
 constexpr int kShortMaxT = 2048;  // rows up to this length are kept whole in one workgroup
+static_assert(kNT >= kShortMaxT / 8, "a short row (up to 256 threads of 8 steps) fits one workgroup");
 // Long rows: each op fixes its threads per workgroup (kLongThreads) and the most 4-step
 // segments per thread its registers hold without spilling (kLongMaxSegments, 2..8).  The
 // smallest tile any op uses sizes the workspace.

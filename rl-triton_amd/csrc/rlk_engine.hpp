@@ -123,8 +123,13 @@ template <int S, bool VEC, bool PER_STEP>
 __device__ __forceinline__ void boot_load(const float* __restrict__ boot, int mode, int64_t row,
                                           int t0, int T, float (&seg)[S], float& last,
                                           const float* any_row) {
-  last = *boot_last(boot, mode, row, T);
-  if constexpr (PER_STEP) load_seg<S, VEC>(mode == kBootFull ? boot + row * (int64_t)T : any_row, t0, T, seg);
+  if constexpr (PER_STEP) {
+    load_seg<S, VEC>(mode == kBootFull ? boot + row * (int64_t)T : any_row, t0, T, seg);
+    // a per-step array already holds boot(T-1) in the segment that contains T-1
+    last = mode == kBootFull ? 0.f : *boot_last(boot, mode, row, T);
+  } else {
+    last = *boot_last(boot, mode, row, T);
+  }
 }
 template <int S, bool PER_STEP>
 __device__ __forceinline__ void boot_prepare(int mode, int t0, int T, float (&bt)[S], float last) {
