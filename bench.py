@@ -22,6 +22,8 @@ Printed JSON (one line, stdout):
   ops            per-op device time, Gelem/s, GB/s and %-of-peak for both kernels
   configs        the same figures for every BASELINE configuration (C1-C5,
                  tests/baseline_configs.py), each its own rotating input sets
+  extensions     compute_gae_normalized (fused GAE + returns + advantage normalisation) at
+                 [4096,128] against the torch composition it replaces
   cpu_baseline   the reference's sequential torch loops (restated in
                  oracle/torch_loops.py) on the host CPU, 1 thread, bounded sample; this
                  CPU leg also checks the headline outputs against the float64 oracle
@@ -177,6 +179,61 @@ def time_configs(torch, names, min_launches=200, batch=50):
     return res
 
 
+def time_extensions(torch, min_launches=200, batch=50):
+    """compute_gae_normalized (GAE + returns + batch-normalised advantages, the reference's
+    ROADMAP.md:75-81 item) at the C2 shape, against the composition it replaces:
+    compute_gae, then returns = A + values, then (A - A.mean()) / (A.std() + 1e-8) in torch.
+    Device time per call from HIP events around batches queued behind a GPU spin."""
+    import baseline_configs as bc
+    import rl_triton
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    name = "C2_gae_4096x128"
+    _, n_env, n_t, _ = bc.CONFIGS[name]
+    n_sets = min(64, -(-3 * MALL_BYTES // (n_env * n_t * 4 * 7)) + 1)
+    sets = [bc.make(name, seed=200 + i, device=dev) for i in range(n_sets)]
+
+    def fused(inp, params):
+        return rl_triton.compute_gae_normalized(inp["rewards"], inp["values"], inp["terminateds"],
+                                                inp["truncateds"],
+                                                bootstrap_values=inp["bootstrap_values"], **params)
+
+    def composed(inp, params):
+        a = rl_triton.compute_gae(inp["rewards"], inp["values"], inp["terminateds"], inp["truncateds"],
+                                  bootstrap_values=inp["bootstrap_values"], **params)
+        ret = a + inp["values"]
+        return (a - a.mean()) / (a.std() + 1e-8), ret
+
+    res = {}
+    for label, fn in (("fused", fused), ("torch_composition", composed)):
+        for i in range(min(n_sets, 8)):
+            fn(*sets[i])
+        torch.cuda.synchronize()
+        total_ms, n = 0.0, 0
+        while n < min_launches:
+            torch.cuda._sleep(20_000_000)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for i in range(batch):
+                fn(*sets[(n + i) % n_sets])
+            b.record(stream)
+            torch.cuda.synchronize()
+            total_ms += a.elapsed_time(b)
+            n += batch
+        res[label] = round(1e3 * total_ms / n, 3)
+    del sets
+    torch.cuda.empty_cache()
+    elems = n_env * n_t
+    out = {"shape": [n_env, n_t], "device_us": res["fused"],
+           "torch_composition_us": res["torch_composition"],
+           "speedup": round(res["torch_composition"] / res["fused"], 2),
+           "bytes_per_elem": 28,  # 5 inputs read, advantages and returns written, once each
+           "gb_s": round(elems * 28 / (res["fused"] * 1e-6) / 1e9, 1)}
+    log(f"[bench] gae_normalized [{n_env},{n_t}]: {res['fused']:.2f} us/call fused vs "
+        f"{res['torch_composition']:.2f} us composed in torch")
+    return {"gae_normalized_4096x128": out}
+
+
 def time_graph_steps(torch, rl, sets, steps):
     """Steps replayed from a captured HIP graph (the same API calls, captured once per input
     set): the device-bound throughput without per-call host work."""
@@ -325,6 +382,7 @@ def main(argv=None):
     elif a.configs != "none":
         cfg_names = a.configs.split(",")
     configs = time_configs(torch, cfg_names) if cfg_names else None
+    extensions = time_extensions(torch) if a.configs != "none" else None
 
     # CPU leg: the float64 oracle checks set 0's outputs, then the reference's sequential
     # loops are timed on the host
@@ -348,7 +406,7 @@ def main(argv=None):
                                f"{n_sets} HBM-resident sets",
                    "num_envs": E, "seq_len": T, "gamma": 0.99, "lambda": 0.95,
                    "rho_bar": 1.0, "c_bar": 1.0, "timing": "value: eager public-API calls, HIP events around the timed region"},
-        "roofline": roofline, "ops": ops, "configs": configs,
+        "roofline": roofline, "ops": ops, "configs": configs, "extensions": extensions,
         "graph_replay": {"ms_per_step": round(graph_ms, 6),
                          "gelem_s": round(2 * E * T / (graph_ms * 1e-3) / 1e9, 3)},
         "parity_max_abs_err": errs, "cpu_baseline": cpu,

@@ -71,6 +71,25 @@ int rlk_gae(const float *rewards, const float *values, const float *terminateds,
             int64_t num_envs, int64_t seq_len, float gamma, float lambda_, void *workspace,
             size_t workspace_bytes, void *stream);
 
+/* GAE with returns and batch-normalised advantages (no counterpart in the reference: the
+ * "fused GAE + advantage normalisation" item of its ROADMAP.md:75-81).  Writes
+ *   returns    = A + values
+ *   advantages = (A - mean(A)) / (std(A) + eps)
+ * with A the advantages of rlk_gae on the same arguments, mean and std over all
+ * num_envs * seq_len elements (std unbiased, as torch's Tensor.std()), computed in float64
+ * in a fixed order.  Two launches: the scan writes A, the returns and one float64
+ * (sum, sum of squares) pair per workgroup into `partials` (at least
+ * rlk_gae_normalized_partials_bytes(num_envs, seq_len) bytes, 8-byte aligned, no
+ * initialisation needed); a second kernel normalises A in place.  `workspace` as for
+ * rlk_gae. */
+size_t rlk_gae_normalized_partials_bytes(int64_t num_envs, int64_t seq_len);
+int rlk_gae_normalized(const float *rewards, const float *values, const float *terminateds,
+                       const float *truncateds, const float *bootstrap, int boot_mode,
+                       float *advantages, float *returns, int64_t num_envs, int64_t seq_len,
+                       float gamma, float lambda_, float eps, void *workspace,
+                       size_t workspace_bytes, void *partials, size_t partials_bytes,
+                       void *stream);
+
 /* V-trace targets and advantages.  Replaces vtrace_fused_kernel in compute_vtrace_fused
  * (src/rl_triton/ops/vtrace_fused.py:161-219; kernel kernels/vtrace_fused.py:7-196) and
  * the torch + chunked-scan path of compute_vtrace (ops/vtrace.py:161-201).

@@ -62,11 +62,28 @@ bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr
 
 // Short rows: S steps per thread, L = 2^ceil(log2(ceil(T/S))) threads per row, 256/L rows
 // per workgroup, grid = ceil(E / (256/L)).
+int64_t rows_grid(int64_t E, int64_t T, int S) {
+  const int64_t rows_per_block = kNT >> ceil_log2((T + S - 1) / S);
+  return (E + rows_per_block - 1) / rows_per_block;
+}
+
+int64_t chain_grid(int64_t E, int64_t T, int NT, int Q) {
+  const int64_t tile = (int64_t)NT * kSeg * Q;
+  const int64_t nslots = lookback_slots(E);
+  return nslots * (((E + nslots - 1) / nslots) * ((T + tile - 1) / tile));
+}
+
+// Workgroups of the launch that launch() makes for Op at [E, T] (E, T > 0).
+template <class Op>
+int64_t launch_grid(int64_t E, int64_t T) {
+  if (T > kShortMaxT) return chain_grid(E, T, Op::kLongThreads, long_segments<Op>(E, T));
+  return rows_grid(E, T, T <= 1024 ? 4 : 8);
+}
+
 template <class Op, int S, bool VEC>
 hipError_t launch_rows(const Op& op, int64_t E, int T, hipStream_t stream) {
   int log2L = ceil_log2((T + S - 1) / S);
-  const int64_t rows_per_block = kNT >> log2L;
-  const int64_t grid = (E + rows_per_block - 1) / rows_per_block;
+  const int64_t grid = rows_grid(E, T, S);
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   void* args[] = {const_cast<Op*>(&op), &E, &T, &log2L};
   return hipLaunchKernel(reinterpret_cast<const void*>(&rows_kernel<Op, kNT, S, VEC>),
@@ -81,8 +98,7 @@ hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_
   static_assert(NT * kSeg * Q >= kMinTile, "the workspace is sized for the smallest tile");
   constexpr int64_t tile = (int64_t)NT * kSeg * Q;
   int tpr = (int)((T + tile - 1) / tile);
-  const int64_t nslots = lookback_slots(E);
-  const int64_t grid = nslots * (((E + nslots - 1) / nslots) * (int64_t)tpr);
+  const int64_t grid = chain_grid(E, T, NT, Q);
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   void* args[] = {const_cast<Op*>(&op), &E, &T, &tpr, &ws};
   return hipLaunchKernel(reinterpret_cast<const void*>(&chain_kernel<Op, NT, Q, VEC>),
@@ -172,6 +188,60 @@ int rlk_gae(const float* rewards, const float* values, const float* terminateds,
   GaeOp<false> op{rewards, values, terminateds, nullptr, boot, advantages, boot_mode, gamma,
                   gamma * lambda_};
   return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+}
+
+size_t rlk_gae_normalized_partials_bytes(int64_t num_envs, int64_t seq_len) {
+  if (num_envs <= 0 || seq_len <= 0) return 0;
+  return (size_t)launch_grid<GaeStatsOp<true>>(num_envs, seq_len) * 2 * sizeof(double);
+}
+
+int rlk_gae_normalized(const float* rewards, const float* values, const float* terminateds,
+                       const float* truncateds, const float* bootstrap, int boot_mode,
+                       float* advantages, float* returns, int64_t num_envs, int64_t seq_len,
+                       float gamma, float lambda_, float eps, void* workspace,
+                       size_t workspace_bytes, void* partials, size_t partials_bytes,
+                       void* stream) {
+  if (is_empty(num_envs, seq_len)) return RLK_OK;
+  if (!rewards || !values || !terminateds || !advantages || !returns ||
+      !valid_boot(bootstrap, boot_mode))
+    return RLK_ERR_INVALID_ARGUMENT;
+  if (num_envs < 0 || seq_len < 0 || seq_len > (int64_t{1} << 30)) return RLK_ERR_INVALID_ARGUMENT;
+  double* parts = reinterpret_cast<double*>(partials);
+  const int64_t nparts = launch_grid<GaeStatsOp<true>>(num_envs, seq_len);
+  if (parts == nullptr || (reinterpret_cast<uintptr_t>(parts) & 7u) != 0 ||
+      partials_bytes < (size_t)nparts * 2 * sizeof(double) || nparts > 0x7fffffffLL)
+    return RLK_ERR_WORKSPACE;
+  const float* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
+  const bool vec = seq_len % 4 == 0 && aligned16(rewards) && aligned16(values) &&
+                   aligned16(terminateds) && aligned16(truncateds) && aligned16(advantages) &&
+                   aligned16(returns) && (boot_mode != RLK_BOOT_FULL || aligned16(bootstrap));
+  int st;
+  if (truncateds) {
+    GaeStatsOp<true> op{{rewards, values, terminateds, truncateds, boot, advantages, boot_mode,
+                         gamma, gamma * lambda_},
+                        returns, parts};
+    st = launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  } else {
+    GaeStatsOp<false> op{{rewards, values, terminateds, nullptr, boot, advantages, boot_mode,
+                          gamma, gamma * lambda_},
+                         returns, parts};
+    st = launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  }
+  if (st != RLK_OK) return st;
+  // second launch: the statistics, then (A - mean) / (std + eps) in place
+  constexpr int kNormNT = 256;
+  int64_t n = num_envs * seq_len;
+  int np = (int)nparts;
+  const int64_t units = n % 4 == 0 && aligned16(advantages) ? n / 4 : n;
+  int64_t grid = (units + kNormNT - 1) / kNormNT;
+  if (grid > 2048) grid = 2048;
+  void* args[] = {&advantages, &parts, &np, &n, &eps};
+  const void* kernel = (n % 4 == 0 && aligned16(advantages))
+                           ? reinterpret_cast<const void*>(&normalize_kernel<kNormNT, true>)
+                           : reinterpret_cast<const void*>(&normalize_kernel<kNormNT, false>);
+  const hipError_t e = hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(kNormNT), args, 0,
+                                       reinterpret_cast<hipStream_t>(stream));
+  return e == hipSuccess ? RLK_OK : RLK_ERR_LAUNCH;
 }
 
 int rlk_vtrace(const float* log_pi_target, const float* log_pi_behavior, const float* values,

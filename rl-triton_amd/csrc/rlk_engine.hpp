@@ -226,6 +226,96 @@ __device__ __forceinline__ void replay(const float (&mul)[S], const float (&add)
 }
 
 // ---------------------------------------------------------------------------------------
+// Per-workgroup output statistics (ops with kBlockStats): float64 sum and sum of squares of
+// the valid outputs, reduced in a fixed order (lanes by a fixed butterfly, waves in index
+// order), so the partial a workgroup writes is the same bit pattern on every run.
+// ---------------------------------------------------------------------------------------
+template <int S>
+__device__ __forceinline__ void accumulate_stats(const float (&xs)[S], int t0, int T, bool ok,
+                                                 double& sum, double& sq) {
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const double x = (ok && t0 + i < T) ? (double)xs[i] : 0.0;
+    sum += x;
+    sq = fma(x, x, sq);
+  }
+}
+
+// Every thread of the workgroup calls this once; thread 0 writes partials[2*blockIdx.x + {0,1}].
+template <int NT>
+__device__ __forceinline__ void block_stats(double sum, double sq, double* __restrict__ partials) {
+  constexpr int NW = NT / kWave;
+  __shared__ double s_sum[NW], s_sq[NW];
+#pragma unroll
+  for (int off = kWave / 2; off >= 1; off >>= 1) {
+    sum += __shfl_xor(sum, off, kWave);
+    sq += __shfl_xor(sq, off, kWave);
+  }
+  const int wave = threadIdx.x / kWave;
+  if (__lane_id() == 0) {
+    s_sum[wave] = sum;
+    s_sq[wave] = sq;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double a = 0.0, b = 0.0;
+    for (int w = 0; w < NW; ++w) {
+      a += s_sum[w];
+      b += s_sq[w];
+    }
+    partials[2 * blockIdx.x] = a;
+    partials[2 * blockIdx.x + 1] = b;
+  }
+}
+
+// Second launch of the normalisation: every workgroup combines the per-workgroup partials
+// of the first launch in one fixed order (thread i sums partials i, i+NT, ...; then an LDS
+// tree), so all agree on the statistics, then rewrites its share of x as
+// (x - mean) / (std + eps), std unbiased (n - 1), as torch computes x.std().
+template <int NT, bool VEC>
+__global__ __launch_bounds__(NT) void normalize_kernel(float* __restrict__ x,
+                                                       const double* __restrict__ partials,
+                                                       int nparts, int64_t n, float eps) {
+  __shared__ double s_a[NT], s_b[NT];
+  const int tid = threadIdx.x;
+  double a = 0.0, b = 0.0;
+  for (int i = tid; i < nparts; i += NT) {
+    a += partials[2 * i];
+    b += partials[2 * i + 1];
+  }
+  s_a[tid] = a;
+  s_b[tid] = b;
+  __syncthreads();
+  for (int h = NT / 2; h > 0; h >>= 1) {
+    if (tid < h) {
+      s_a[tid] += s_a[tid + h];
+      s_b[tid] += s_b[tid + h];
+    }
+    __syncthreads();
+  }
+  const double mean = s_a[0] / (double)n;
+  double var = (s_b[0] - s_a[0] * mean) / (double)(n - 1);
+  var = var > 0.0 ? var : 0.0;
+  if (n < 2) var = __builtin_nan("");  // torch: the unbiased std of one element is nan
+  const float m = (float)mean;
+  const float d = (float)sqrt(var) + eps;
+  const int64_t stride = (int64_t)gridDim.x * NT;
+  if constexpr (VEC) {
+    float4* x4 = reinterpret_cast<float4*>(x);
+    for (int64_t i = (int64_t)blockIdx.x * NT + tid; i < n / 4; i += stride) {
+      float4 v = x4[i];
+      v.x = (v.x - m) / d;
+      v.y = (v.y - m) / d;
+      v.z = (v.z - m) / d;
+      v.w = (v.w - m) / d;
+      x4[i] = v;
+    }
+  } else {
+    for (int64_t i = (int64_t)blockIdx.x * NT + tid; i < n; i += stride) x[i] = (x[i] - m) / d;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Cross-lane moves by DPP (gfx9 data-parallel primitives): a VALU modifier, no trip through
 // the LDS crossbar.  update_dpp(old, src): a lane whose source lane is invalid, or whose
 // row is masked off, keeps `old`.
@@ -346,6 +436,11 @@ __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T,
   float xs[S];
   replay<FWD, S>(mul, add, x_in, xs);
   if (active) op.template emit<S, VEC>(R, h, xs, x_in, row, t0, T);
+  if constexpr (Op::kBlockStats) {
+    double sum = 0.0, sq = 0.0;
+    accumulate_stats<S>(xs, t0, T, active, sum, sq);
+    block_stats<NT>(sum, sq, op.partials);
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -503,6 +598,7 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
     drawn = __hip_atomic_fetch_add(sc + 16, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
+  double st_sum = 0.0, st_sq = 0.0;  // output statistics (ops with kBlockStats)
   if (q_t < tiles_in_slot) {
     const int64_t lr = (int64_t)(q_t / (uint64_t)tiles_per_row);
     const int j = (int)(q_t - (uint64_t)lr * tiles_per_row);
@@ -576,8 +672,10 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
       float xs[kSeg];
       replay<FWD, kSeg>(mul[r], add[r], x_in, xs);
       op.template emit<kSeg, VEC>(R[r], h[r], xs, x_in, row, seg_t0(r), T);
+      if constexpr (Op::kBlockStats) accumulate_stats<kSeg>(xs, seg_t0(r), T, true, st_sum, st_sq);
     }
   }
+  if constexpr (Op::kBlockStats) block_stats<NT>(st_sum, st_sq, op.partials);
   if (tid == 0 && drawn == wgs_per_slot - 1) {
     atomic_st(sc + 0, 0);
     atomic_st(sc + 16, 0);

@@ -29,6 +29,7 @@ __device__ __forceinline__ void fill_regs(float (&v)[S], float x) {
 template <bool TRUNC>
 struct GaeOp {
   static constexpr bool kForward = false;
+  static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
   // long-row tiles: threads per workgroup and most 4-step segments per thread that stay
   // in registers (no spills at 1024 threads, whose cap is 128 VGPRs)
   static constexpr int kLongThreads = 1024, kLongMaxSegments = 4;
@@ -91,6 +92,35 @@ struct GaeOp {
 };
 
 // ------------------------------------------------------------------------------------------
+// GAE with returns and batch statistics: the first half of compute_gae_normalized (no
+// counterpart in the reference, which has none of this; it is the "fused GAE + advantage
+// normalisation" item of its ROADMAP.md:75-81).  The scan is GaeOp's; the epilogue writes
+// the raw advantages A and the returns A + values, and each workgroup reduces the sum and
+// the sum of squares of its A in float64 into partials[2*blockIdx.x .. +1] (see
+// block_stats in rlk_engine.hpp).  normalize_kernel then turns A into
+// (A - mean) / (std + eps) in place.
+// ------------------------------------------------------------------------------------------
+template <bool TRUNC>
+struct GaeStatsOp : GaeOp<TRUNC> {
+  static constexpr bool kBlockStats = true;
+  float* returns;
+  double* partials;
+  template <int S>
+  using Regs = typename GaeOp<TRUNC>::template Regs<S>;
+
+  template <int S, bool VEC>
+  __device__ void emit(const Regs<S>& R, float, const float (&xs)[S], float, int64_t row, int t0,
+                       int T) const {
+    float rt[S];
+#pragma unroll
+    for (int i = 0; i < S; ++i) rt[i] = xs[i] + R.v[i];
+    const int64_t o = row * (int64_t)T;
+    store_seg<S, VEC>(this->out + o, t0, T, xs);
+    store_seg<S, VEC>(returns + o, t0, T, rt);
+  }
+};
+
+// ------------------------------------------------------------------------------------------
 // V-trace: kernels/vtrace_fused.py:90-196 (vtrace_fused_kernel).
 //   rho = min(exp(lpt - lpb), rho_bar),  c = min(exp(lpt - lpb), c_bar)
 //   truncations:  v_next = values[t+1]*[t < T-1 and trunc == 0] + boot(t)   (additive)
@@ -104,6 +134,7 @@ struct GaeOp {
 template <bool TRUNC>
 struct VtraceOp {
   static constexpr bool kForward = false;
+  static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
   static constexpr int kLongThreads = 1024, kLongMaxSegments = 2;
   using Halo = float;  // values[t+1]
   const float* lpt;
@@ -201,6 +232,7 @@ struct VtraceOp {
 template <int NA, bool TRUNC>
 struct RetraceOp {
   static constexpr bool kForward = false;
+  static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
   static constexpr int kLongThreads = 512, kLongMaxSegments = 2;  // 256 VGPRs: the A-wide rows
   using Halo = Halo2;  // {c[t+1], q[t+1]}
   const float* pi;     // [E, T, A]
@@ -334,6 +366,7 @@ struct RetraceOp {
 template <bool NV, bool TRUNC>
 struct ReturnsOp {
   static constexpr bool kForward = false;
+  static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
   static constexpr int kLongThreads = 1024, kLongMaxSegments = (NV || TRUNC) ? 4 : 8;
   using Halo = NoHalo;
   const float* r;
@@ -406,6 +439,7 @@ struct ReturnsOp {
 // ------------------------------------------------------------------------------------------
 struct DoneGatedForwardOp {
   static constexpr bool kForward = true;
+  static constexpr bool kBlockStats = false;
   static constexpr int kLongThreads = 1024, kLongMaxSegments = 8;
   using Halo = float;  // done[t-1]
   const float* x;
@@ -462,6 +496,7 @@ struct DoneGatedForwardOp {
 template <bool FWD>
 struct AffineScanOp {
   static constexpr bool kForward = FWD;
+  static constexpr bool kBlockStats = false;
   static constexpr int kLongThreads = 1024, kLongMaxSegments = 8;
   using Halo = NoHalo;
   const float* u;

@@ -141,6 +141,32 @@ PyObject* op_gae(PyObject* const* a, Py_ssize_t n) {
   return finish(st, "rlk_gae", THPVariable_Wrap(std::move(out)));
 }
 
+// gae_normalized(rewards, values, terminateds, truncateds, gamma, lambda_, bootstrap_values,
+//                last_value, eps) -> (advantages, returns)
+PyObject* op_gae_normalized(PyObject* const* a, Py_ssize_t n) {
+  if (!nargs_is(n, 9, "gae_normalized")) return nullptr;
+  if (correctness_warnings()) return decline();
+  Call c;
+  const at::Tensor* r = c.lead(a[0]);
+  const at::Tensor* v = c.need(a[1]);
+  const at::Tensor* te = c.need(a[2]);
+  const at::Tensor* tr = c.opt(a[3]);
+  const float gamma = c.scalar(a[4]), lam = c.scalar(a[5]), eps = c.scalar(a[8]);
+  const bool has_bv = a[6] != Py_None, has_lv = a[7] != Py_None;
+  if (has_bv && has_lv) return decline();
+  if (has_lv && tr) return decline();
+  const at::Tensor* boot = has_lv ? c.need(a[7], 1) : c.opt(a[6]);
+  if (!c.ok) return decline();
+  const int mode = has_lv ? RLK_BOOT_ROW : has_bv ? RLK_BOOT_FULL : RLK_BOOT_NONE;
+  at::Tensor adv = c.output(*r), ret = c.output(*r);
+  const size_t pb = rlk_gae_normalized_partials_bytes(c.E, c.T);
+  at::Tensor parts = at::empty({(int64_t)(pb > 0 ? pb : 8)}, r->options().dtype(at::kByte));
+  const int st = rlk_gae_normalized(fp(r), fp(v), fp(te), fp(tr), fp(boot), mode, fp_out(adv),
+                                    fp_out(ret), c.E, c.T, gamma, lam, eps, nullptr, 0,
+                                    parts.data_ptr(), pb, c.stream());
+  return finish(st, "rlk_gae_normalized", pair(adv, ret));
+}
+
 // vtrace(log_pi_target, log_pi_behavior, values, rewards, terminateds, truncateds, gamma,
 //        rho_bar, c_bar, bootstrap_values, last_value)
 PyObject* op_vtrace(PyObject* const* a, Py_ssize_t n) {
@@ -296,6 +322,7 @@ PyObject* guarded(PyObject*, PyObject* const* a, Py_ssize_t n) {
 
 PyMethodDef kMethods[] = {
     RLK_METHOD(gae),
+    RLK_METHOD(gae_normalized),
     RLK_METHOD(vtrace),
     RLK_METHOD(retrace),
     RLK_METHOD(lambda_returns),

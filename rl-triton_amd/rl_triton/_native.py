@@ -33,6 +33,9 @@ _SZ = ctypes.c_size_t
 # name -> argtypes (must match include/rl_triton_amd.h)
 SIGNATURES = {
     "rlk_gae": [_P, _P, _P, _P, _P, _INT, _P, _I64, _I64, _F, _F, _P, _SZ, _P],
+    "rlk_gae_normalized": [_P, _P, _P, _P, _P, _INT, _P, _P, _I64, _I64, _F, _F, _F, _P, _SZ, _P,
+                           _SZ, _P],
+    "rlk_gae_normalized_partials_bytes": [_I64, _I64],
     "rlk_vtrace": [_P, _P, _P, _P, _P, _P, _P, _INT, _P, _P, _I64, _I64, _F, _F, _F, _P, _SZ, _P],
     "rlk_retrace": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _F, _F, _P,
                     _SZ, _P],
@@ -45,7 +48,8 @@ SIGNATURES = {
     "rlk_status_string": [_INT],
     "rlk_version": [],
 }
-_RESTYPES = {"rlk_workspace_bytes": _SZ, "rlk_status_string": ctypes.c_char_p}
+_RESTYPES = {"rlk_workspace_bytes": _SZ, "rlk_gae_normalized_partials_bytes": _SZ,
+             "rlk_status_string": ctypes.c_char_p}
 
 _lib = None
 _lock = threading.Lock()
@@ -170,6 +174,22 @@ def workspace_error(device=None) -> bool:
     return False
 
 
+# per-workgroup partial sums of compute_gae_normalized: one uninitialised buffer per
+# (device, stream), grown on demand (every workgroup writes its own entry before the second
+# launch reads them; calls on one stream are ordered).
+_partials: dict = {}
+
+
+def _partials_buffer(dev: int, stream: int, n_env: int, n_t: int):
+    need = load().rlk_gae_normalized_partials_bytes(n_env, n_t)
+    buf = _partials.get((dev, stream))
+    if buf is None or buf.numel() < need:
+        size = max(need, 2 * buf.numel() if buf is not None else 0, 256)
+        buf = torch.empty(size, dtype=torch.uint8, device=torch.device("cuda", dev))
+        _partials[(dev, stream)] = buf
+    return buf.data_ptr(), buf.numel()
+
+
 def _launch(fn, what, dev, n_env, n_t, *args):
     """Call C entry `fn` with `args` + (workspace, bytes, stream) on the current stream of
     device `dev` (made current for the call if it is not)."""
@@ -205,6 +225,30 @@ def gae(rewards, values, terminateds, truncateds, bootstrap, out, gamma, lambda_
             _ptr(terminateds, "terminateds", shape, dev), _opt(truncateds, "truncateds", shape, dev),
             bp, mode, _ptr(out, "out", shape, dev), n_env, n_t, gamma, lambda_)
     return out
+
+
+def gae_normalized(rewards, values, terminateds, truncateds, bootstrap, advantages, returns, gamma,
+                   lambda_, eps):
+    dev = _device_of(rewards)
+    shape = rewards.shape
+    n_env, n_t = shape
+    lib = _lib or load()
+    bp, mode = _boot_args(bootstrap, n_env, n_t, dev)
+    args = (_ptr(rewards, "rewards", shape, dev), _ptr(values, "values", shape, dev),
+            _ptr(terminateds, "terminateds", shape, dev), _opt(truncateds, "truncateds", shape, dev),
+            bp, mode, _ptr(advantages, "advantages", shape, dev), _ptr(returns, "returns", shape, dev),
+            n_env, n_t, gamma, lambda_, eps)
+    if dev != _cur_device():
+        with torch.cuda.device(dev):
+            return gae_normalized(rewards, values, terminateds, truncateds, bootstrap, advantages,
+                                  returns, gamma, lambda_, eps)
+    stream = _raw_stream(dev)
+    ws, wsb = _workspace(dev, stream, n_env, n_t)
+    pp, ppb = _partials_buffer(dev, stream, n_env, n_t) if n_env * n_t > 0 else (None, 0)
+    status = lib.rlk_gae_normalized(*args, ws, wsb, pp, ppb, stream)
+    if status != 0:
+        _check(status, "rlk_gae_normalized")
+    return advantages, returns
 
 
 def vtrace(log_pi_target, log_pi_behavior, values, rewards, terminateds, truncateds, bootstrap,

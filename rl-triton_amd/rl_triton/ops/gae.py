@@ -4,6 +4,56 @@ from rl_triton import _native
 from rl_triton.ops._scan import _CORRECTNESS_WARNINGS
 
 
+def _check_gae_args(rewards, values, terminateds, truncateds, bootstrap_values, last_value):
+    """The reference's compute_gae checks (ops/gae.py:106-145), in its order and with its
+    messages: always-on structural checks, then the expensive ones under
+    RL_TRITON_CORRECTNESS_WARNINGS=1."""
+    num_envs, seq_len = rewards.shape
+    has_truncations   = truncateds is not None
+
+    # Cheap structural checks -- always-on (ops/gae.py:106-129).
+    for name, t in [("rewards", rewards), ("values", values), ("terminateds", terminateds)]:
+        assert t.is_cuda,                f"{name} must be on CUDA"
+        assert t.dtype == torch.float32, f"{name}: expected float32, got {t.dtype}"
+        assert t.shape == rewards.shape, f"{name} shape {t.shape} != rewards shape {rewards.shape}"
+    if has_truncations:
+        assert truncateds.is_cuda,                "truncateds must be on CUDA"
+        assert truncateds.dtype == torch.float32, "truncateds: expected float32"
+        assert truncateds.shape == rewards.shape, \
+            f"truncateds shape {truncateds.shape} != rewards shape {rewards.shape}"
+    if last_value is not None:
+        assert bootstrap_values is None, \
+            "pass either last_value (shape [num_envs], convenience for the " \
+            "window boundary) or bootstrap_values (shape [num_envs, seq_len], " \
+            "full per-step control), not both."
+        assert last_value.shape == (num_envs,), \
+            f"last_value must have shape [{num_envs}], got {last_value.shape}"
+        assert not has_truncations, \
+            "last_value cannot be combined with truncateds; use bootstrap_values instead."
+    if bootstrap_values is not None:
+        assert bootstrap_values.is_cuda,                "bootstrap_values must be on CUDA"
+        assert bootstrap_values.dtype == torch.float32, "bootstrap_values: expected float32"
+        assert bootstrap_values.shape == rewards.shape, \
+            f"bootstrap_values shape {bootstrap_values.shape} != rewards shape {rewards.shape}"
+
+    # Expensive tensor scans -- correctness-warning path only (ops/gae.py:132-145).
+    if _CORRECTNESS_WARNINGS():
+        if has_truncations:
+            assert not (terminateds.bool() & truncateds.bool()).any(), \
+                "terminated and truncated are mutually exclusive: a step cannot be both"
+        if has_truncations and bootstrap_values is not None:
+            interior = torch.ones_like(truncateds, dtype=torch.bool)
+            interior[:, -1] = False
+            stray = (bootstrap_values != 0) & (truncateds == 0) & interior
+            assert not stray.any(), (
+                "bootstrap_values must be zero at non-truncated interior steps. "
+                "Nonzero entries there double-count via the additive v_next trick "
+                "and corrupt delta. Populate bootstrap_values only at truncated "
+                "steps and at the final column (window boundary)."
+            )
+
+
+
 def compute_gae(
     rewards: torch.Tensor,
     values: torch.Tensor,
@@ -55,49 +105,8 @@ def compute_gae(
         if res is not None:
             return res
 
-    num_envs, seq_len = rewards.shape
-    has_truncations   = truncateds is not None
-
-    # Cheap structural checks -- always-on (ops/gae.py:106-129).
-    for name, t in [("rewards", rewards), ("values", values), ("terminateds", terminateds)]:
-        assert t.is_cuda,                f"{name} must be on CUDA"
-        assert t.dtype == torch.float32, f"{name}: expected float32, got {t.dtype}"
-        assert t.shape == rewards.shape, f"{name} shape {t.shape} != rewards shape {rewards.shape}"
-    if has_truncations:
-        assert truncateds.is_cuda,                "truncateds must be on CUDA"
-        assert truncateds.dtype == torch.float32, "truncateds: expected float32"
-        assert truncateds.shape == rewards.shape, \
-            f"truncateds shape {truncateds.shape} != rewards shape {rewards.shape}"
-    if last_value is not None:
-        assert bootstrap_values is None, \
-            "pass either last_value (shape [num_envs], convenience for the " \
-            "window boundary) or bootstrap_values (shape [num_envs, seq_len], " \
-            "full per-step control), not both."
-        assert last_value.shape == (num_envs,), \
-            f"last_value must have shape [{num_envs}], got {last_value.shape}"
-        assert not has_truncations, \
-            "last_value cannot be combined with truncateds; use bootstrap_values instead."
-    if bootstrap_values is not None:
-        assert bootstrap_values.is_cuda,                "bootstrap_values must be on CUDA"
-        assert bootstrap_values.dtype == torch.float32, "bootstrap_values: expected float32"
-        assert bootstrap_values.shape == rewards.shape, \
-            f"bootstrap_values shape {bootstrap_values.shape} != rewards shape {rewards.shape}"
-
-    # Expensive tensor scans -- correctness-warning path only (ops/gae.py:132-145).
-    if _CORRECTNESS_WARNINGS():
-        if has_truncations:
-            assert not (terminateds.bool() & truncateds.bool()).any(), \
-                "terminated and truncated are mutually exclusive: a step cannot be both"
-        if has_truncations and bootstrap_values is not None:
-            interior = torch.ones_like(truncateds, dtype=torch.bool)
-            interior[:, -1] = False
-            stray = (bootstrap_values != 0) & (truncateds == 0) & interior
-            assert not stray.any(), (
-                "bootstrap_values must be zero at non-truncated interior steps. "
-                "Nonzero entries there double-count via the additive v_next trick "
-                "and corrupt delta. Populate bootstrap_values only at truncated "
-                "steps and at the final column (window boundary)."
-            )
+    has_truncations = truncateds is not None
+    _check_gae_args(rewards, values, terminateds, truncateds, bootstrap_values, last_value)
 
     rewards     = rewards.contiguous()
     values      = values.contiguous()

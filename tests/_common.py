@@ -30,7 +30,17 @@ OUTPUTS = {
     "retrace": ("targets", "advantages"), "lambda_returns": ("returns",),
     "discounted_returns": ("returns",), "eligibility_traces": ("traces",),
     "prefix_sum": ("prefix_sums",), "backward_scan": ("out",), "forward_scan": ("out",),
+    "gae_normalized": ("advantages", "returns"),
 }
+
+
+def normalized_from_oracle(adv, values, eps):
+    """The float64 composition compute_gae_normalized fuses: returns = A + values and
+    (A - mean) / (std + eps), std unbiased -- numpy's ddof=1, torch's Tensor.std()."""
+    a = np.asarray(adv, dtype=np.float64)
+    ret = a + np.asarray(values, dtype=np.float64)
+    std = a.std(ddof=1) if a.size > 1 else np.nan
+    return (a - a.mean()) / (std + eps), ret
 
 
 def run_oracle(op, inp, params):
@@ -39,6 +49,12 @@ def run_oracle(op, inp, params):
         boot = g("last_value") if g("last_value") is not None else g("bootstrap_values")
         return (orc.gae(g("rewards"), g("values"), g("terminateds"), g("truncateds"),
                         bootstrap=boot, **params),)
+    if op == "gae_normalized":
+        boot = g("last_value") if g("last_value") is not None else g("bootstrap_values")
+        p = dict(params)
+        eps = p.pop("eps", 1e-8)
+        adv = orc.gae(g("rewards"), g("values"), g("terminateds"), g("truncateds"), bootstrap=boot, **p)
+        return normalized_from_oracle(adv, g("values"), eps)
     if op == "vtrace":
         boot = g("last_value") if g("last_value") is not None else g("bootstrap_values")
         return orc.vtrace(g("log_pi_target"), g("log_pi_behavior"), g("values"), g("rewards"),
@@ -88,6 +104,11 @@ def run_api(op, inp, params, device):
         return (rl_triton.compute_gae(g("rewards"), g("values"), g("terminateds"), g("truncateds"),
                                       bootstrap_values=g("bootstrap_values"),
                                       last_value=g("last_value"), **params),)
+    if op == "gae_normalized":
+        return rl_triton.compute_gae_normalized(g("rewards"), g("values"), g("terminateds"),
+                                                g("truncateds"),
+                                                bootstrap_values=g("bootstrap_values"),
+                                                last_value=g("last_value"), **params)
     if op == "vtrace":
         return rl_triton.compute_vtrace(g("log_pi_target"), g("log_pi_behavior"), g("values"),
                                         g("rewards"), g("terminateds"), g("truncateds"),
@@ -141,7 +162,7 @@ def make_inputs(op, n_env, n_t, seed=0, p_term=0.05, p_trunc=0.0, boot="none", n
     if p_trunc > 0:
         trunc = (ru(*shape) < p_trunc).float() * (1.0 - term)
     inp = {}
-    if op in ("gae", "vtrace", "lambda_returns", "discounted_returns"):
+    if op in ("gae", "gae_normalized", "vtrace", "lambda_returns", "discounted_returns"):
         if boot == "row":
             inp["last_value"] = rn(n_env)
         elif boot == "full":
@@ -150,7 +171,7 @@ def make_inputs(op, n_env, n_t, seed=0, p_term=0.05, p_trunc=0.0, boot="none", n
                 bv = torch.where(trunc.bool(), rn(*shape), bv)
             bv[:, -1] = rn(n_env)
             inp["bootstrap_values"] = bv
-    if op == "gae":
+    if op in ("gae", "gae_normalized"):
         inp.update(rewards=rn(*shape), values=rn(*shape), terminateds=term, truncateds=trunc)
         params = {"gamma": 0.99, "lambda_": 0.95}
     elif op == "vtrace":

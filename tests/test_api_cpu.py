@@ -117,9 +117,11 @@ def test_flag_gated_paths_still_refuse_cpu_tensors(monkeypatch):
 
 def test_public_surface_matches_reference():
     assert rl_triton.__version__ == "0.1.3"
-    assert sorted(rl_triton.__all__) == sorted([
-        "compute_discounted_returns", "compute_eligibility_traces", "compute_episodic_prefix_sum",
-        "compute_gae", "compute_lambda_returns", "compute_retrace", "compute_vtrace"])
+    reference = ["compute_discounted_returns", "compute_eligibility_traces",
+                 "compute_episodic_prefix_sum", "compute_gae", "compute_lambda_returns",
+                 "compute_retrace", "compute_vtrace"]
+    # the reference's seven functions, plus one extension it lists on its ROADMAP.md:75-81
+    assert sorted(rl_triton.__all__) == sorted(reference + ["compute_gae_normalized"])
     assert _FLAT_MAX_SEQ_LEN == 131072
     assert callable(compute_retrace_fused)
 
@@ -141,3 +143,22 @@ def test_fast_path_declines_cpu_tensors():
     import rl_triton
     with pytest.raises(AssertionError, match="must be on CUDA"):
         rl_triton.compute_gae(x, x, x)
+
+
+def test_gae_normalized_checks_match_compute_gae():
+    """compute_gae_normalized raises compute_gae's assertions: both call one check helper."""
+    from rl_triton.ops.gae import _check_gae_args
+
+    class _Gpu:  # passes the device, dtype and shape checks without a GPU
+        def __init__(self, *shape):
+            self.shape, self.is_cuda, self.dtype = torch.Size(shape), True, torch.float32
+
+    x = torch.zeros(4, 8)
+    for fn in (rl_triton.compute_gae, rl_triton.compute_gae_normalized):
+        with pytest.raises(AssertionError, match="rewards must be on CUDA"):
+            fn(x, x, x)
+    t = _Gpu(4, 8)
+    with pytest.raises(AssertionError, match="not both"):
+        _check_gae_args(t, t, t, None, t, _Gpu(4))
+    with pytest.raises(AssertionError, match="cannot be combined with truncateds"):
+        _check_gae_args(t, t, t, t, None, _Gpu(4))

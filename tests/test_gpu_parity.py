@@ -272,7 +272,7 @@ def test_max_abs_error_report(device):
 # ---------------------------------------------------------------------------------------
 # the tensor-level fast path (rl_triton._rlk_torch) against the general Python path
 # ---------------------------------------------------------------------------------------
-FAST_OPS = ["gae", "vtrace", "retrace", "lambda_returns", "discounted_returns",
+FAST_OPS = ["gae", "gae_normalized", "vtrace", "retrace", "lambda_returns", "discounted_returns",
             "eligibility_traces", "prefix_sum", "backward_scan", "forward_scan"]
 
 
@@ -285,7 +285,8 @@ def test_fast_path_matches_python_path(op, shape, device, monkeypatch):
     the results are bit-identical."""
     from rl_triton import _native
     assert _native.fast is not None, "rl_triton._rlk_torch is not built"
-    boot = "full" if op in ("gae", "vtrace", "lambda_returns", "discounted_returns") else "row"
+    boot = ("full" if op in ("gae", "gae_normalized", "vtrace", "lambda_returns", "discounted_returns")
+            else "row")
     inp, params = make_inputs(op, *shape, seed=21, p_trunc=0.02 if op != "retrace" else 0.0,
                               boot=boot)
     slow = run_api(op, inp, params, device)
@@ -295,8 +296,8 @@ def test_fast_path_matches_python_path(op, shape, device, monkeypatch):
     monkeypatch.setattr(_native, "fast", _Spy(real, calls))
     fast = run_api(op, inp, params, device)
     assert calls and all(taken for _, taken in calls), f"fast path declined: {calls}"
-    for s, f in zip(slow, fast):
-        assert torch.equal(s, f)
+    for s, f in zip(slow, fast):  # bit-identical (nan where both are: one-element batch std)
+        torch.testing.assert_close(s, f, rtol=0, atol=0, equal_nan=True)
 
 
 class _Spy:
@@ -328,3 +329,62 @@ def test_fast_path_declines_what_it_cannot_take(device, monkeypatch):
     assert f.gae(long, long, long, None, 0.99, 0.95, None, None) is None
     assert f.gae(x, x, x, None, 0.99, 0.95, x, torch.zeros(8, device=device)) is None
     assert f.gae(x, x, x.double(), None, 0.99, 0.95, None, None) is None
+
+
+# ---------------------------------------------------------------------------------------
+# compute_gae_normalized: GAE + returns + batch-normalised advantages (the reference's
+# ROADMAP.md:75-81 item; no reference implementation, so the oracle is the float64 GAE
+# oracle composed with the textbook formulas, tests/_common.normalized_from_oracle)
+# ---------------------------------------------------------------------------------------
+def _check_normalized(inp, params, device, what, long_rows=False):
+    got = run_api("gae_normalized", inp, params, device)
+    adv_exp, ret_exp = run_oracle("gae_normalized", inp, params)
+    torch.cuda.synchronize()
+    raw = run_oracle("gae", inp, {k: v for k, v in params.items() if k != "eps"})[0]
+    std = float(np.std(raw, ddof=1))
+    scale = max(1.0, float(np.max(np.abs(ret_exp))))
+    if long_rows:
+        base = _long_atol("gae", inp, raw)
+    else:
+        base = 1e-5 * max(1.0, float(np.max(np.abs(raw))))
+    # returns carry A's error; normalised advantages carry it divided by std
+    assert_close(got[1].cpu().numpy(), ret_exp, 1e-5, base + 1e-6 * scale, f"{what}:returns")
+    assert_close(got[0].cpu().numpy(), adv_exp, 1e-5, base / min(std, 1.0) + 1e-6,
+                 f"{what}:advantages")
+    return got
+
+
+@pytest.mark.parametrize("boot", ["none", "row", "full"])
+@pytest.mark.parametrize("trunc", [0.0, 0.05])
+@pytest.mark.parametrize("shape", [(2, 3), (4, 128), (33, 257), (16, 2048), (3, 5000), (2, 40000)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_gae_normalized_parity(boot, trunc, shape, device):
+    if boot == "row" and trunc > 0:
+        pytest.skip("last_value cannot be combined with truncateds (reference contract)")
+    inp, params = make_inputs("gae_normalized", *shape, seed=17, p_trunc=trunc, boot=boot)
+    params = dict(params, eps=1e-8)
+    _check_normalized(inp, params, device, f"gae_normalized{shape} boot={boot} trunc={trunc}",
+                      long_rows=shape[1] > 2048)
+
+
+def test_gae_normalized_full_size_and_repeatable(device):
+    """BASELINE C2 at full size: against the float64 composition; the advantages come out
+    with mean 0 and std 1 (to float32 rounding); repeated calls are bit-identical."""
+    import baseline_configs
+    inp, params = baseline_configs.make("C2_gae_4096x128", seed=0)
+    np_inp = {k: v.numpy() for k, v in inp.items()}
+    got = _check_normalized(np_inp, dict(params, eps=1e-8), device, "C2 normalized")
+    a = got[0].double()
+    assert abs(float(a.mean())) < 1e-6 and abs(float(a.std()) - 1.0) < 1e-5
+    again = run_api("gae_normalized", np_inp, dict(params, eps=1e-8), device)
+    assert torch.equal(got[0], again[0]) and torch.equal(got[1], again[1])
+
+
+def test_gae_normalized_single_element_is_nan_like_torch(device):
+    """The unbiased std of one element is nan in torch; so are the normalised advantages."""
+    import rl_triton
+    x = torch.ones(1, 1, device=device)
+    adv, ret = rl_triton.compute_gae_normalized(x, x, torch.zeros_like(x))
+    ref = rl_triton.compute_gae(x, x, torch.zeros_like(x))
+    assert torch.isnan(adv).all() and torch.isnan((ref - ref.mean()) / (ref.std() + 1e-8)).all()
+    torch.testing.assert_close(ret, ref + x)
