@@ -269,41 +269,57 @@ __device__ __forceinline__ void block_stats(double sum, double sq, double* __res
 }
 
 // Second launch of the normalisation: every workgroup combines the per-workgroup partials
-// of the first launch in one fixed order (thread i sums partials i, i+NT, ...; then an LDS
-// tree), so all agree on the statistics, then rewrites its share of x as
+// of the first launch in one fixed order (thread i sums partials i, i+NT, ...; a fixed lane
+// butterfly; the waves in index order), so all agree on the statistics, then rewrites its
+// share of x as
 // (x - mean) / (std + eps), std unbiased (n - 1), as torch computes x.std().
 template <int NT, bool VEC>
 __global__ __launch_bounds__(NT) void normalize_kernel(float* __restrict__ x,
                                                        const double* __restrict__ partials,
                                                        int nparts, int64_t n, float eps) {
-  __shared__ double s_a[NT], s_b[NT];
+  constexpr int NW = NT / kWave;
+  __shared__ double s_a[NW], s_b[NW];
   const int tid = threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * NT;
+  const int64_t first = (int64_t)blockIdx.x * NT + tid;
+  const int64_t units = VEC ? n / 4 : n;
+  // this thread's first element is loaded before the statistics, so the two round trips
+  // overlap
+  float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (first < units) {
+    if constexpr (VEC) v0 = reinterpret_cast<const float4*>(x)[first];
+    else v0.x = x[first];
+  }
   double a = 0.0, b = 0.0;
   for (int i = tid; i < nparts; i += NT) {
     a += partials[2 * i];
     b += partials[2 * i + 1];
   }
-  s_a[tid] = a;
-  s_b[tid] = b;
-  __syncthreads();
-  for (int h = NT / 2; h > 0; h >>= 1) {
-    if (tid < h) {
-      s_a[tid] += s_a[tid + h];
-      s_b[tid] += s_b[tid + h];
-    }
-    __syncthreads();
+#pragma unroll
+  for (int off = kWave / 2; off >= 1; off >>= 1) {
+    a += __shfl_xor(a, off, kWave);
+    b += __shfl_xor(b, off, kWave);
   }
-  const double mean = s_a[0] / (double)n;
-  double var = (s_b[0] - s_a[0] * mean) / (double)(n - 1);
+  if (__lane_id() == 0) {
+    s_a[tid / kWave] = a;
+    s_b[tid / kWave] = b;
+  }
+  __syncthreads();
+  double sum = 0.0, sq = 0.0;
+  for (int w = 0; w < NW; ++w) {
+    sum += s_a[w];
+    sq += s_b[w];
+  }
+  const double mean = sum / (double)n;
+  double var = (sq - sum * mean) / (double)(n - 1);
   var = var > 0.0 ? var : 0.0;
   if (n < 2) var = __builtin_nan("");  // torch: the unbiased std of one element is nan
   const float m = (float)mean;
   const float d = (float)sqrt(var) + eps;
-  const int64_t stride = (int64_t)gridDim.x * NT;
   if constexpr (VEC) {
     float4* x4 = reinterpret_cast<float4*>(x);
-    for (int64_t i = (int64_t)blockIdx.x * NT + tid; i < n / 4; i += stride) {
-      float4 v = x4[i];
+    for (int64_t i = first; i < units; i += stride) {
+      float4 v = i == first ? v0 : x4[i];
       v.x = (v.x - m) / d;
       v.y = (v.y - m) / d;
       v.z = (v.z - m) / d;
@@ -311,7 +327,7 @@ __global__ __launch_bounds__(NT) void normalize_kernel(float* __restrict__ x,
       x4[i] = v;
     }
   } else {
-    for (int64_t i = (int64_t)blockIdx.x * NT + tid; i < n; i += stride) x[i] = (x[i] - m) / d;
+    for (int64_t i = first; i < units; i += stride) x[i] = ((i == first ? v0.x : x[i]) - m) / d;
   }
 }
 
