@@ -140,18 +140,23 @@ def time_ops(torch, rl, sets, iters, batch=100):
     return res
 
 
-def time_configs(torch, names, min_launches=200, batch=50):
+def time_configs(torch, names, min_launches=200, batch=50, dtype=None):
     """Average kernel duration of every BASELINE configuration's public-API call (one
     kernel launch per call), from HIP events around batches of back-to-back launches queued
-    behind a GPU spin, over rotating input sets of more than 3 x 256 MB."""
+    behind a GPU spin, over rotating input sets of more than 3 x 256 MB.  dtype=bfloat16:
+    the same calls with bfloat16 I/O (float32 arithmetic)."""
     import baseline_configs as bc
+    dtype = dtype or torch.float32
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
     res = {}
     for name in names:
-        op, n_env, n_t, bpe = bc.CONFIGS[name]
-        n_sets = min(64, max(2, -(-3 * MALL_BYTES // bc.set_bytes(name)) + 1))
+        op, n_env, n_t, _ = bc.CONFIGS[name]
+        bpe = bc.bytes_per_elem(name, dtype)
+        set_bytes = bc.set_bytes(name) * bpe // bc.CONFIGS[name][3]
+        n_sets = min(64, max(2, -(-3 * MALL_BYTES // set_bytes) + 1))
         sets = [bc.make(name, seed=100 + i, device=dev) for i in range(n_sets)]
+        sets = [(bc.as_dtype(inp, dtype), params) for inp, params in sets]
         for i in range(min(n_sets, 8)):
             bc.call(name, *sets[i])
         torch.cuda.synchronize()
@@ -173,8 +178,9 @@ def time_configs(torch, names, min_launches=200, batch=50):
                      "gelem_s": round(n_env * n_t / (us * 1e-6) / 1e9, 2), "gb_s": round(gbs, 1),
                      "pct_peak": round(100 * gbs / PEAK_GBS, 2), "bytes_per_elem": bpe,
                      "target_pct": (100 * bc.TARGETS[name]) if name in bc.TARGETS else None,
-                     "traffic": measured_traffic(name)}
-        log(f"[bench] {name}: {us:.2f} us/launch, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of 8 TB/s)")
+                     "traffic": measured_traffic(name) if dtype is torch.float32 else None}
+        tag = "" if dtype is torch.float32 else " bf16"
+        log(f"[bench] {name}{tag}: {us:.2f} us/launch, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of 8 TB/s)")
     torch.cuda.empty_cache()
     return res
 
@@ -382,6 +388,7 @@ def main(argv=None):
     elif a.configs != "none":
         cfg_names = a.configs.split(",")
     configs = time_configs(torch, cfg_names) if cfg_names else None
+    configs_bf16 = time_configs(torch, cfg_names, dtype=torch.bfloat16) if cfg_names else None
     extensions = time_extensions(torch) if a.configs != "none" else None
 
     # CPU leg: the float64 oracle checks set 0's outputs, then the reference's sequential
@@ -406,7 +413,8 @@ def main(argv=None):
                                f"{n_sets} HBM-resident sets",
                    "num_envs": E, "seq_len": T, "gamma": 0.99, "lambda": 0.95,
                    "rho_bar": 1.0, "c_bar": 1.0, "timing": "value: eager public-API calls, HIP events around the timed region"},
-        "roofline": roofline, "ops": ops, "configs": configs, "extensions": extensions,
+        "roofline": roofline, "ops": ops, "configs": configs, "configs_bf16_io": configs_bf16,
+        "extensions": extensions,
         "graph_replay": {"ms_per_step": round(graph_ms, 6),
                          "gelem_s": round(2 * E * T / (graph_ms * 1e-3) / 1e9, 3)},
         "parity_max_abs_err": errs, "cpu_baseline": cpu,

@@ -30,6 +30,13 @@
  *     per tile.
  *   - Return value: RLK_OK or a negative RLK_ERR_* code; rlk_status_string() names it.
  *     Empty inputs (num_envs == 0 or seq_len == 0) return RLK_OK without a launch.
+ *   - bfloat16 I/O: every estimator has an `_bf16` twin whose float arrays (inputs,
+ *     bootstrap, seed and outputs alike) are bfloat16, passed as rlk_bf16 (the raw 16
+ *     bits).  The arithmetic stays float32: a bfloat16 result is the float32 entry
+ *     point's result on the same (widened) inputs, rounded to nearest even as torch's
+ *     float -> bfloat16 conversion rounds it (NaN -> 0x7fc0).  The reference accepts
+ *     float32 only (its ROADMAP.md:82-99 lists this as planned); the twins have no
+ *     counterpart there.
  */
 #ifndef RL_TRITON_AMD_H
 #define RL_TRITON_AMD_H
@@ -52,6 +59,9 @@ extern "C" {
 
 #define RLK_BACKWARD 0
 #define RLK_FORWARD 1
+
+/* A bfloat16 value as its raw bits (the upper half of an IEEE float32). */
+typedef uint16_t rlk_bf16;
 
 /* Library version, major*10000 + minor*100 + patch. */
 int rlk_version(void);
@@ -154,6 +164,65 @@ int rlk_prefix_sum(const float *inputs, const float *dones, const float *seed_va
 int rlk_affine_scan(const float *u, const float *v, const float *carry, float *out,
                     int64_t num_envs, int64_t seq_len, int direction, void *workspace,
                     size_t workspace_bytes, void *stream);
+
+/* bfloat16 twins of the entry points above: the same arguments, with rlk_bf16 for every
+ * float array.  See "bfloat16 I/O" at the top of this file. */
+int rlk_gae_bf16(const rlk_bf16 *rewards, const rlk_bf16 *values, const rlk_bf16 *terminateds,
+                 const rlk_bf16 *truncateds, const rlk_bf16 *bootstrap, int boot_mode,
+                 rlk_bf16 *advantages, int64_t num_envs, int64_t seq_len, float gamma,
+                 float lambda_, void *workspace, size_t workspace_bytes, void *stream);
+
+/* The bfloat16 results of rlk_gae_normalized.  The statistics are those of the float32
+ * advantages; the second launch normalises the stored (bfloat16) advantages, so each
+ * normalised value is rounded twice. */
+int rlk_gae_normalized_bf16(const rlk_bf16 *rewards, const rlk_bf16 *values,
+                            const rlk_bf16 *terminateds, const rlk_bf16 *truncateds,
+                            const rlk_bf16 *bootstrap, int boot_mode, rlk_bf16 *advantages,
+                            rlk_bf16 *returns, int64_t num_envs, int64_t seq_len, float gamma,
+                            float lambda_, float eps, void *workspace, size_t workspace_bytes,
+                            void *partials, size_t partials_bytes, void *stream);
+
+int rlk_vtrace_bf16(const rlk_bf16 *log_pi_target, const rlk_bf16 *log_pi_behavior,
+                    const rlk_bf16 *values, const rlk_bf16 *rewards, const rlk_bf16 *terminateds,
+                    const rlk_bf16 *truncateds, const rlk_bf16 *bootstrap, int boot_mode,
+                    rlk_bf16 *targets, rlk_bf16 *advantages, int64_t num_envs, int64_t seq_len,
+                    float gamma, float rho_bar, float c_bar, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
+/* actions stay int64. */
+int rlk_retrace_bf16(const rlk_bf16 *action_probs_target, const rlk_bf16 *action_probs_behavior,
+                     const rlk_bf16 *q_values, const rlk_bf16 *next_q_values_all,
+                     const int64_t *actions, const rlk_bf16 *rewards,
+                     const rlk_bf16 *terminateds, const rlk_bf16 *truncateds, rlk_bf16 *targets,
+                     rlk_bf16 *advantages, int64_t num_envs, int64_t seq_len,
+                     int64_t num_actions, float gamma, float lambda_, float c_bar, float rho_bar,
+                     void *workspace, size_t workspace_bytes, void *stream);
+
+int rlk_lambda_returns_bf16(const rlk_bf16 *rewards, const rlk_bf16 *next_values,
+                            const rlk_bf16 *terminateds, const rlk_bf16 *truncateds,
+                            const rlk_bf16 *bootstrap, int boot_mode, rlk_bf16 *returns,
+                            int64_t num_envs, int64_t seq_len, float gamma, float lambda_,
+                            void *workspace, size_t workspace_bytes, void *stream);
+
+int rlk_discounted_returns_bf16(const rlk_bf16 *rewards, const rlk_bf16 *terminateds,
+                                const rlk_bf16 *truncateds, const rlk_bf16 *bootstrap,
+                                int boot_mode, rlk_bf16 *returns, int64_t num_envs,
+                                int64_t seq_len, float gamma, void *workspace,
+                                size_t workspace_bytes, void *stream);
+
+int rlk_eligibility_traces_bf16(const rlk_bf16 *gradients, const rlk_bf16 *dones,
+                                const rlk_bf16 *seed_values, rlk_bf16 *traces, int64_t num_envs,
+                                int64_t seq_len, float gamma, float lambda_, void *workspace,
+                                size_t workspace_bytes, void *stream);
+
+int rlk_prefix_sum_bf16(const rlk_bf16 *inputs, const rlk_bf16 *dones,
+                        const rlk_bf16 *seed_values, rlk_bf16 *prefix_sums, int64_t num_envs,
+                        int64_t seq_len, int ends_at, void *workspace, size_t workspace_bytes,
+                        void *stream);
+
+int rlk_affine_scan_bf16(const rlk_bf16 *u, const rlk_bf16 *v, const rlk_bf16 *carry,
+                         rlk_bf16 *out, int64_t num_envs, int64_t seq_len, int direction,
+                         void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -140,11 +140,242 @@ int launch(const Op& op, int64_t E, int64_t T, bool vec, void* workspace, size_t
 // are rejected by launch().
 bool is_empty(int64_t E, int64_t T) { return (E == 0 && T >= 0) || (T == 0 && E >= 0); }
 
-bool valid_boot(const float* boot, int mode) {
+bool valid_boot(const void* boot, int mode) {
   if (mode == RLK_BOOT_NONE) return true;
   if (mode == RLK_BOOT_ROW || mode == RLK_BOOT_FULL) return boot != nullptr;
   return false;
 }
+
+// Vector segments need every [E, T] array aligned to four elements (absent ones pass).
+template <class E>
+bool quad_aligned(const E* p) {
+  return p == nullptr || (reinterpret_cast<uintptr_t>(p) % (4 * sizeof(E))) == 0;
+}
+template <class E, class... R>
+bool quad_aligned(const E* p, const R*... rest) {
+  return quad_aligned(p) && quad_aligned(rest...);
+}
+
+// ---------------------------------------------------------------------------------------
+// Entry points, one template per estimator over the storage type E (float or bf16); the
+// extern "C" functions below instantiate them.
+// ---------------------------------------------------------------------------------------
+template <class E>
+int gae_impl(const E* rewards, const E* values, const E* terminateds, const E* truncateds,
+             const E* bootstrap, int boot_mode, E* advantages, int64_t num_envs, int64_t seq_len,
+             float gamma, float lambda_, void* workspace, size_t workspace_bytes, void* stream) {
+  if (is_empty(num_envs, seq_len)) return RLK_OK;
+  if (!rewards || !values || !terminateds || !advantages || !valid_boot(bootstrap, boot_mode))
+    return RLK_ERR_INVALID_ARGUMENT;
+  const E* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
+  const bool vec = seq_len % 4 == 0 &&
+                   quad_aligned(rewards, values, terminateds, truncateds, advantages) &&
+                   (boot_mode != RLK_BOOT_FULL || quad_aligned(bootstrap));
+  if (truncateds) {
+    GaeOp<true, E> op{rewards, values, terminateds, truncateds, boot, advantages, boot_mode, gamma,
+                      gamma * lambda_};
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  }
+  GaeOp<false, E> op{rewards, values, terminateds, nullptr, boot, advantages, boot_mode, gamma,
+                     gamma * lambda_};
+  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+}
+
+size_t gae_normalized_partials(int64_t num_envs, int64_t seq_len) {
+  if (num_envs <= 0 || seq_len <= 0) return 0;
+  // every instantiation has GaeStatsOp<true>'s geometry (the same kLong* constants)
+  return (size_t)launch_grid<GaeStatsOp<true>>(num_envs, seq_len) * 2 * sizeof(double);
+}
+
+template <class E>
+int gae_normalized_impl(const E* rewards, const E* values, const E* terminateds,
+                        const E* truncateds, const E* bootstrap, int boot_mode, E* advantages,
+                        E* returns, int64_t num_envs, int64_t seq_len, float gamma, float lambda_,
+                        float eps, void* workspace, size_t workspace_bytes, void* partials,
+                        size_t partials_bytes, void* stream) {
+  if (is_empty(num_envs, seq_len)) return RLK_OK;
+  if (!rewards || !values || !terminateds || !advantages || !returns ||
+      !valid_boot(bootstrap, boot_mode))
+    return RLK_ERR_INVALID_ARGUMENT;
+  if (num_envs < 0 || seq_len < 0 || seq_len > (int64_t{1} << 30)) return RLK_ERR_INVALID_ARGUMENT;
+  double* parts = reinterpret_cast<double*>(partials);
+  const int64_t nparts = launch_grid<GaeStatsOp<true, E>>(num_envs, seq_len);
+  if (parts == nullptr || (reinterpret_cast<uintptr_t>(parts) & 7u) != 0 ||
+      partials_bytes < (size_t)nparts * 2 * sizeof(double) || nparts > 0x7fffffffLL)
+    return RLK_ERR_WORKSPACE;
+  const E* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
+  const bool vec = seq_len % 4 == 0 &&
+                   quad_aligned(rewards, values, terminateds, truncateds, advantages, returns) &&
+                   (boot_mode != RLK_BOOT_FULL || quad_aligned(bootstrap));
+  int st;
+  if (truncateds) {
+    GaeStatsOp<true, E> op{{rewards, values, terminateds, truncateds, boot, advantages, boot_mode,
+                            gamma, gamma * lambda_},
+                           returns, parts};
+    st = launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  } else {
+    GaeStatsOp<false, E> op{{rewards, values, terminateds, nullptr, boot, advantages, boot_mode,
+                             gamma, gamma * lambda_},
+                            returns, parts};
+    st = launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  }
+  if (st != RLK_OK) return st;
+  // second launch: the statistics, then (A - mean) / (std + eps) in place
+  constexpr int kNormNT = 256;
+  int64_t n = num_envs * seq_len;
+  int np = (int)nparts;
+  const bool nvec = n % 4 == 0 && quad_aligned(advantages);
+  const int64_t units = nvec ? n / 4 : n;
+  int64_t grid = (units + kNormNT - 1) / kNormNT;
+  if (grid > 2048) grid = 2048;
+  void* args[] = {&advantages, &parts, &np, &n, &eps};
+  const void* kernel = nvec ? reinterpret_cast<const void*>(&normalize_kernel<kNormNT, true, E>)
+                            : reinterpret_cast<const void*>(&normalize_kernel<kNormNT, false, E>);
+  const hipError_t e = hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(kNormNT), args, 0,
+                                       reinterpret_cast<hipStream_t>(stream));
+  return e == hipSuccess ? RLK_OK : RLK_ERR_LAUNCH;
+}
+
+template <class E>
+int vtrace_impl(const E* log_pi_target, const E* log_pi_behavior, const E* values,
+                const E* rewards, const E* terminateds, const E* truncateds, const E* bootstrap,
+                int boot_mode, E* targets, E* advantages, int64_t num_envs, int64_t seq_len,
+                float gamma, float rho_bar, float c_bar, void* workspace, size_t workspace_bytes,
+                void* stream) {
+  if (is_empty(num_envs, seq_len)) return RLK_OK;
+  if (!log_pi_target || !log_pi_behavior || !values || !rewards || !terminateds || !targets ||
+      !advantages || !valid_boot(bootstrap, boot_mode))
+    return RLK_ERR_INVALID_ARGUMENT;
+  const E* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
+  const bool vec = seq_len % 4 == 0 &&
+                   quad_aligned(log_pi_target, log_pi_behavior, values, rewards, terminateds,
+                                truncateds, targets, advantages) &&
+                   (boot_mode != RLK_BOOT_FULL || quad_aligned(bootstrap));
+  if (truncateds) {
+    VtraceOp<true, E> op{log_pi_target, log_pi_behavior, values, rewards, terminateds, truncateds,
+                         boot, targets, advantages, boot_mode, gamma, rho_bar, c_bar};
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  }
+  VtraceOp<false, E> op{log_pi_target, log_pi_behavior, values, rewards, terminateds, nullptr,
+                        boot, targets, advantages, boot_mode, gamma, rho_bar, c_bar};
+  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+}
+
+template <class E>
+int retrace_impl(const E* action_probs_target, const E* action_probs_behavior, const E* q_values,
+                 const E* next_q_values_all, const int64_t* actions, const E* rewards,
+                 const E* terminateds, const E* truncateds, E* targets, E* advantages,
+                 int64_t num_envs, int64_t seq_len, int64_t num_actions, float gamma,
+                 float lambda_, float c_bar, float rho_bar, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  if (is_empty(num_envs, seq_len)) return RLK_OK;
+  if (!action_probs_target || !action_probs_behavior || !q_values || !next_q_values_all ||
+      !actions || !rewards || !terminateds || !targets || !advantages || num_actions <= 0 ||
+      num_actions > (1 << 20))
+    return RLK_ERR_INVALID_ARGUMENT;
+  const bool vec = seq_len % 4 == 0 &&
+                   quad_aligned(action_probs_target, action_probs_behavior, q_values,
+                                next_q_values_all, rewards, terminateds, truncateds, targets,
+                                advantages) &&
+                   aligned16(actions);
+  const int A = (int)num_actions;
+#define RLK_RETRACE(NA)                                                                          \
+  {                                                                                              \
+    if (truncateds) {                                                                            \
+      RetraceOp<NA, true, E> op{action_probs_target, action_probs_behavior, q_values,            \
+                                next_q_values_all, actions, rewards, terminateds, truncateds,    \
+                                targets, advantages, A, gamma, lambda_, c_bar, rho_bar};         \
+      return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);             \
+    }                                                                                            \
+    RetraceOp<NA, false, E> op{action_probs_target, action_probs_behavior, q_values,             \
+                               next_q_values_all, actions, rewards, terminateds, nullptr,        \
+                               targets, advantages, A, gamma, lambda_, c_bar, rho_bar};          \
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);               \
+  }
+  switch (A) {
+    case 1: RLK_RETRACE(1)
+    case 2: RLK_RETRACE(2)
+    case 4: RLK_RETRACE(4)
+    default: RLK_RETRACE(0)
+  }
+#undef RLK_RETRACE
+}
+
+template <class E>
+int lambda_returns_impl(const E* rewards, const E* next_values, const E* terminateds,
+                        const E* truncateds, const E* bootstrap, int boot_mode, E* returns,
+                        int64_t num_envs, int64_t seq_len, float gamma, float lambda_,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  if (is_empty(num_envs, seq_len)) return RLK_OK;
+  if (!rewards || !next_values || !terminateds || !returns || !valid_boot(bootstrap, boot_mode))
+    return RLK_ERR_INVALID_ARGUMENT;
+  const E* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
+  const bool vec = seq_len % 4 == 0 &&
+                   quad_aligned(rewards, next_values, terminateds, truncateds, returns) &&
+                   (boot_mode != RLK_BOOT_FULL || quad_aligned(bootstrap));
+  if (truncateds) {
+    ReturnsOp<true, true, E> op{rewards, next_values, terminateds, truncateds, boot, returns,
+                                boot_mode, gamma, gamma * (1.f - lambda_), gamma * lambda_};
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  }
+  ReturnsOp<true, false, E> op{rewards, next_values, terminateds, nullptr, boot, returns,
+                               boot_mode, gamma, gamma * (1.f - lambda_), gamma * lambda_};
+  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+}
+
+template <class E>
+int discounted_returns_impl(const E* rewards, const E* terminateds, const E* truncateds,
+                            const E* bootstrap, int boot_mode, E* returns, int64_t num_envs,
+                            int64_t seq_len, float gamma, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  if (is_empty(num_envs, seq_len)) return RLK_OK;
+  if (!rewards || !terminateds || !returns || !valid_boot(bootstrap, boot_mode))
+    return RLK_ERR_INVALID_ARGUMENT;
+  const E* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
+  const bool vec = seq_len % 4 == 0 && quad_aligned(rewards, terminateds, truncateds, returns) &&
+                   (boot_mode != RLK_BOOT_FULL || quad_aligned(bootstrap));
+  if (truncateds) {
+    ReturnsOp<false, true, E> op{rewards, nullptr, terminateds, truncateds, boot, returns,
+                                 boot_mode, gamma, 0.f, gamma};
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  }
+  ReturnsOp<false, false, E> op{rewards, nullptr, terminateds, nullptr, boot, returns, boot_mode,
+                                gamma, 0.f, gamma};
+  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+}
+
+// eligibility traces (decay = gamma * lambda, gated on done[t-1]) and the episodic prefix
+// sum (decay 1, ends_at or starts_at) share one op
+template <class E>
+int done_gated_impl(const E* x, const E* dones, const E* seed, E* out, int64_t num_envs,
+                    int64_t seq_len, float decay, int ends_at, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  if (is_empty(num_envs, seq_len)) return RLK_OK;
+  if (!x || !dones || !out) return RLK_ERR_INVALID_ARGUMENT;
+  DoneGatedForwardOp<E> op{x, dones, seed, out, decay, ends_at};
+  const bool vec = seq_len % 4 == 0 && quad_aligned(x, dones, out);
+  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+}
+
+template <class E>
+int affine_scan_impl(const E* u, const E* v, const E* carry, E* out, int64_t num_envs,
+                     int64_t seq_len, int direction, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+  if (is_empty(num_envs, seq_len)) return RLK_OK;
+  if (!u || !v || !out || (direction != RLK_BACKWARD && direction != RLK_FORWARD))
+    return RLK_ERR_INVALID_ARGUMENT;
+  const bool vec = seq_len % 4 == 0 && quad_aligned(u, v, out);
+  if (direction == RLK_FORWARD) {
+    AffineScanOp<true, E> op{u, v, carry, out};
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  }
+  AffineScanOp<false, E> op{u, v, carry, out};
+  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+}
+
+// rlk_bf16 (raw bits) <-> the kernels' bf16 storage type
+const bf16* B(const rlk_bf16* p) { return reinterpret_cast<const bf16*>(p); }
+bf16* B(rlk_bf16* p) { return reinterpret_cast<bf16*>(p); }
 
 }  // namespace
 }  // namespace rlk
@@ -173,26 +404,21 @@ int rlk_gae(const float* rewards, const float* values, const float* terminateds,
             const float* truncateds, const float* bootstrap, int boot_mode, float* advantages,
             int64_t num_envs, int64_t seq_len, float gamma, float lambda_, void* workspace,
             size_t workspace_bytes, void* stream) {
-  if (is_empty(num_envs, seq_len)) return RLK_OK;
-  if (!rewards || !values || !terminateds || !advantages || !valid_boot(bootstrap, boot_mode))
-    return RLK_ERR_INVALID_ARGUMENT;
-  const float* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
-  const bool vec = seq_len % 4 == 0 && aligned16(rewards) && aligned16(values) &&
-                   aligned16(terminateds) && aligned16(truncateds) && aligned16(advantages) &&
-                   (boot_mode != RLK_BOOT_FULL || aligned16(bootstrap));
-  if (truncateds) {
-    GaeOp<true> op{rewards, values, terminateds, truncateds, boot, advantages, boot_mode, gamma,
-                   gamma * lambda_};
-    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
-  }
-  GaeOp<false> op{rewards, values, terminateds, nullptr, boot, advantages, boot_mode, gamma,
-                  gamma * lambda_};
-  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  return gae_impl(rewards, values, terminateds, truncateds, bootstrap, boot_mode, advantages,
+                  num_envs, seq_len, gamma, lambda_, workspace, workspace_bytes, stream);
+}
+
+int rlk_gae_bf16(const rlk_bf16* rewards, const rlk_bf16* values, const rlk_bf16* terminateds,
+                 const rlk_bf16* truncateds, const rlk_bf16* bootstrap, int boot_mode,
+                 rlk_bf16* advantages, int64_t num_envs, int64_t seq_len, float gamma,
+                 float lambda_, void* workspace, size_t workspace_bytes, void* stream) {
+  return gae_impl(B(rewards), B(values), B(terminateds), B(truncateds), B(bootstrap), boot_mode,
+                  B(advantages), num_envs, seq_len, gamma, lambda_, workspace, workspace_bytes,
+                  stream);
 }
 
 size_t rlk_gae_normalized_partials_bytes(int64_t num_envs, int64_t seq_len) {
-  if (num_envs <= 0 || seq_len <= 0) return 0;
-  return (size_t)launch_grid<GaeStatsOp<true>>(num_envs, seq_len) * 2 * sizeof(double);
+  return gae_normalized_partials(num_envs, seq_len);
 }
 
 int rlk_gae_normalized(const float* rewards, const float* values, const float* terminateds,
@@ -201,47 +427,21 @@ int rlk_gae_normalized(const float* rewards, const float* values, const float* t
                        float gamma, float lambda_, float eps, void* workspace,
                        size_t workspace_bytes, void* partials, size_t partials_bytes,
                        void* stream) {
-  if (is_empty(num_envs, seq_len)) return RLK_OK;
-  if (!rewards || !values || !terminateds || !advantages || !returns ||
-      !valid_boot(bootstrap, boot_mode))
-    return RLK_ERR_INVALID_ARGUMENT;
-  if (num_envs < 0 || seq_len < 0 || seq_len > (int64_t{1} << 30)) return RLK_ERR_INVALID_ARGUMENT;
-  double* parts = reinterpret_cast<double*>(partials);
-  const int64_t nparts = launch_grid<GaeStatsOp<true>>(num_envs, seq_len);
-  if (parts == nullptr || (reinterpret_cast<uintptr_t>(parts) & 7u) != 0 ||
-      partials_bytes < (size_t)nparts * 2 * sizeof(double) || nparts > 0x7fffffffLL)
-    return RLK_ERR_WORKSPACE;
-  const float* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
-  const bool vec = seq_len % 4 == 0 && aligned16(rewards) && aligned16(values) &&
-                   aligned16(terminateds) && aligned16(truncateds) && aligned16(advantages) &&
-                   aligned16(returns) && (boot_mode != RLK_BOOT_FULL || aligned16(bootstrap));
-  int st;
-  if (truncateds) {
-    GaeStatsOp<true> op{{rewards, values, terminateds, truncateds, boot, advantages, boot_mode,
-                         gamma, gamma * lambda_},
-                        returns, parts};
-    st = launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
-  } else {
-    GaeStatsOp<false> op{{rewards, values, terminateds, nullptr, boot, advantages, boot_mode,
-                          gamma, gamma * lambda_},
-                         returns, parts};
-    st = launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
-  }
-  if (st != RLK_OK) return st;
-  // second launch: the statistics, then (A - mean) / (std + eps) in place
-  constexpr int kNormNT = 256;
-  int64_t n = num_envs * seq_len;
-  int np = (int)nparts;
-  const int64_t units = n % 4 == 0 && aligned16(advantages) ? n / 4 : n;
-  int64_t grid = (units + kNormNT - 1) / kNormNT;
-  if (grid > 2048) grid = 2048;
-  void* args[] = {&advantages, &parts, &np, &n, &eps};
-  const void* kernel = (n % 4 == 0 && aligned16(advantages))
-                           ? reinterpret_cast<const void*>(&normalize_kernel<kNormNT, true>)
-                           : reinterpret_cast<const void*>(&normalize_kernel<kNormNT, false>);
-  const hipError_t e = hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(kNormNT), args, 0,
-                                       reinterpret_cast<hipStream_t>(stream));
-  return e == hipSuccess ? RLK_OK : RLK_ERR_LAUNCH;
+  return gae_normalized_impl(rewards, values, terminateds, truncateds, bootstrap, boot_mode,
+                             advantages, returns, num_envs, seq_len, gamma, lambda_, eps,
+                             workspace, workspace_bytes, partials, partials_bytes, stream);
+}
+
+int rlk_gae_normalized_bf16(const rlk_bf16* rewards, const rlk_bf16* values,
+                            const rlk_bf16* terminateds, const rlk_bf16* truncateds,
+                            const rlk_bf16* bootstrap, int boot_mode, rlk_bf16* advantages,
+                            rlk_bf16* returns, int64_t num_envs, int64_t seq_len, float gamma,
+                            float lambda_, float eps, void* workspace, size_t workspace_bytes,
+                            void* partials, size_t partials_bytes, void* stream) {
+  return gae_normalized_impl(B(rewards), B(values), B(terminateds), B(truncateds), B(bootstrap),
+                             boot_mode, B(advantages), B(returns), num_envs, seq_len, gamma,
+                             lambda_, eps, workspace, workspace_bytes, partials, partials_bytes,
+                             stream);
 }
 
 int rlk_vtrace(const float* log_pi_target, const float* log_pi_behavior, const float* values,
@@ -249,23 +449,20 @@ int rlk_vtrace(const float* log_pi_target, const float* log_pi_behavior, const f
                const float* bootstrap, int boot_mode, float* targets, float* advantages,
                int64_t num_envs, int64_t seq_len, float gamma, float rho_bar, float c_bar,
                void* workspace, size_t workspace_bytes, void* stream) {
-  if (is_empty(num_envs, seq_len)) return RLK_OK;
-  if (!log_pi_target || !log_pi_behavior || !values || !rewards || !terminateds || !targets ||
-      !advantages || !valid_boot(bootstrap, boot_mode))
-    return RLK_ERR_INVALID_ARGUMENT;
-  const float* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
-  const bool vec = seq_len % 4 == 0 && aligned16(log_pi_target) && aligned16(log_pi_behavior) &&
-                   aligned16(values) && aligned16(rewards) && aligned16(terminateds) &&
-                   aligned16(truncateds) && aligned16(targets) && aligned16(advantages) &&
-                   (boot_mode != RLK_BOOT_FULL || aligned16(bootstrap));
-  if (truncateds) {
-    VtraceOp<true> op{log_pi_target, log_pi_behavior, values, rewards, terminateds, truncateds,
-                      boot, targets, advantages, boot_mode, gamma, rho_bar, c_bar};
-    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
-  }
-  VtraceOp<false> op{log_pi_target, log_pi_behavior, values, rewards, terminateds, nullptr,
-                     boot, targets, advantages, boot_mode, gamma, rho_bar, c_bar};
-  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  return vtrace_impl(log_pi_target, log_pi_behavior, values, rewards, terminateds, truncateds,
+                     bootstrap, boot_mode, targets, advantages, num_envs, seq_len, gamma, rho_bar,
+                     c_bar, workspace, workspace_bytes, stream);
+}
+
+int rlk_vtrace_bf16(const rlk_bf16* log_pi_target, const rlk_bf16* log_pi_behavior,
+                    const rlk_bf16* values, const rlk_bf16* rewards, const rlk_bf16* terminateds,
+                    const rlk_bf16* truncateds, const rlk_bf16* bootstrap, int boot_mode,
+                    rlk_bf16* targets, rlk_bf16* advantages, int64_t num_envs, int64_t seq_len,
+                    float gamma, float rho_bar, float c_bar, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  return vtrace_impl(B(log_pi_target), B(log_pi_behavior), B(values), B(rewards), B(terminateds),
+                     B(truncateds), B(bootstrap), boot_mode, B(targets), B(advantages), num_envs,
+                     seq_len, gamma, rho_bar, c_bar, workspace, workspace_bytes, stream);
 }
 
 int rlk_retrace(const float* action_probs_target, const float* action_probs_behavior,
@@ -274,114 +471,104 @@ int rlk_retrace(const float* action_probs_target, const float* action_probs_beha
                 float* targets, float* advantages, int64_t num_envs, int64_t seq_len,
                 int64_t num_actions, float gamma, float lambda_, float c_bar, float rho_bar,
                 void* workspace, size_t workspace_bytes, void* stream) {
-  if (is_empty(num_envs, seq_len)) return RLK_OK;
-  if (!action_probs_target || !action_probs_behavior || !q_values || !next_q_values_all ||
-      !actions || !rewards || !terminateds || !targets || !advantages || num_actions <= 0 ||
-      num_actions > (1 << 20))
-    return RLK_ERR_INVALID_ARGUMENT;
-  const bool vec = seq_len % 4 == 0 && aligned16(action_probs_target) &&
-                   aligned16(action_probs_behavior) && aligned16(q_values) &&
-                   aligned16(next_q_values_all) && aligned16(actions) && aligned16(rewards) &&
-                   aligned16(terminateds) && aligned16(truncateds) && aligned16(targets) &&
-                   aligned16(advantages);
-  const int A = (int)num_actions;
-#define RLK_RETRACE(NA)                                                                          \
-  {                                                                                              \
-    if (truncateds) {                                                                            \
-      RetraceOp<NA, true> op{action_probs_target, action_probs_behavior, q_values,               \
-                             next_q_values_all, actions, rewards, terminateds, truncateds,       \
-                             targets, advantages, A, gamma, lambda_, c_bar, rho_bar};            \
-      return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);             \
-    }                                                                                            \
-    RetraceOp<NA, false> op{action_probs_target, action_probs_behavior, q_values,                \
-                            next_q_values_all, actions, rewards, terminateds, nullptr, targets,  \
-                            advantages, A, gamma, lambda_, c_bar, rho_bar};                      \
-    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);               \
-  }
-  switch (A) {
-    case 1: RLK_RETRACE(1)
-    case 2: RLK_RETRACE(2)
-    case 4: RLK_RETRACE(4)
-    default: RLK_RETRACE(0)
-  }
-#undef RLK_RETRACE
+  return retrace_impl(action_probs_target, action_probs_behavior, q_values, next_q_values_all,
+                      actions, rewards, terminateds, truncateds, targets, advantages, num_envs,
+                      seq_len, num_actions, gamma, lambda_, c_bar, rho_bar, workspace,
+                      workspace_bytes, stream);
+}
+
+int rlk_retrace_bf16(const rlk_bf16* action_probs_target, const rlk_bf16* action_probs_behavior,
+                     const rlk_bf16* q_values, const rlk_bf16* next_q_values_all,
+                     const int64_t* actions, const rlk_bf16* rewards,
+                     const rlk_bf16* terminateds, const rlk_bf16* truncateds, rlk_bf16* targets,
+                     rlk_bf16* advantages, int64_t num_envs, int64_t seq_len,
+                     int64_t num_actions, float gamma, float lambda_, float c_bar, float rho_bar,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  return retrace_impl(B(action_probs_target), B(action_probs_behavior), B(q_values),
+                      B(next_q_values_all), actions, B(rewards), B(terminateds), B(truncateds),
+                      B(targets), B(advantages), num_envs, seq_len, num_actions, gamma, lambda_,
+                      c_bar, rho_bar, workspace, workspace_bytes, stream);
 }
 
 int rlk_lambda_returns(const float* rewards, const float* next_values, const float* terminateds,
                        const float* truncateds, const float* bootstrap, int boot_mode,
                        float* returns, int64_t num_envs, int64_t seq_len, float gamma,
                        float lambda_, void* workspace, size_t workspace_bytes, void* stream) {
-  if (is_empty(num_envs, seq_len)) return RLK_OK;
-  if (!rewards || !next_values || !terminateds || !returns || !valid_boot(bootstrap, boot_mode))
-    return RLK_ERR_INVALID_ARGUMENT;
-  const float* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
-  const bool vec = seq_len % 4 == 0 && aligned16(rewards) && aligned16(next_values) &&
-                   aligned16(terminateds) && aligned16(truncateds) && aligned16(returns) &&
-                   (boot_mode != RLK_BOOT_FULL || aligned16(bootstrap));
-  if (truncateds) {
-    ReturnsOp<true, true> op{rewards, next_values, terminateds, truncateds, boot, returns,
-                             boot_mode, gamma, gamma * (1.f - lambda_), gamma * lambda_};
-    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
-  }
-  ReturnsOp<true, false> op{rewards, next_values, terminateds, nullptr, boot, returns, boot_mode,
-                            gamma, gamma * (1.f - lambda_), gamma * lambda_};
-  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  return lambda_returns_impl(rewards, next_values, terminateds, truncateds, bootstrap, boot_mode,
+                             returns, num_envs, seq_len, gamma, lambda_, workspace,
+                             workspace_bytes, stream);
+}
+
+int rlk_lambda_returns_bf16(const rlk_bf16* rewards, const rlk_bf16* next_values,
+                            const rlk_bf16* terminateds, const rlk_bf16* truncateds,
+                            const rlk_bf16* bootstrap, int boot_mode, rlk_bf16* returns,
+                            int64_t num_envs, int64_t seq_len, float gamma, float lambda_,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  return lambda_returns_impl(B(rewards), B(next_values), B(terminateds), B(truncateds),
+                             B(bootstrap), boot_mode, B(returns), num_envs, seq_len, gamma,
+                             lambda_, workspace, workspace_bytes, stream);
 }
 
 int rlk_discounted_returns(const float* rewards, const float* terminateds,
                            const float* truncateds, const float* bootstrap, int boot_mode,
                            float* returns, int64_t num_envs, int64_t seq_len, float gamma,
                            void* workspace, size_t workspace_bytes, void* stream) {
-  if (is_empty(num_envs, seq_len)) return RLK_OK;
-  if (!rewards || !terminateds || !returns || !valid_boot(bootstrap, boot_mode))
-    return RLK_ERR_INVALID_ARGUMENT;
-  const float* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
-  const bool vec = seq_len % 4 == 0 && aligned16(rewards) && aligned16(terminateds) &&
-                   aligned16(truncateds) && aligned16(returns) &&
-                   (boot_mode != RLK_BOOT_FULL || aligned16(bootstrap));
-  if (truncateds) {
-    ReturnsOp<false, true> op{rewards, nullptr, terminateds, truncateds, boot, returns, boot_mode,
-                              gamma, 0.f, gamma};
-    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
-  }
-  ReturnsOp<false, false> op{rewards, nullptr, terminateds, nullptr, boot, returns, boot_mode,
-                             gamma, 0.f, gamma};
-  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  return discounted_returns_impl(rewards, terminateds, truncateds, bootstrap, boot_mode, returns,
+                                 num_envs, seq_len, gamma, workspace, workspace_bytes, stream);
+}
+
+int rlk_discounted_returns_bf16(const rlk_bf16* rewards, const rlk_bf16* terminateds,
+                                const rlk_bf16* truncateds, const rlk_bf16* bootstrap,
+                                int boot_mode, rlk_bf16* returns, int64_t num_envs,
+                                int64_t seq_len, float gamma, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  return discounted_returns_impl(B(rewards), B(terminateds), B(truncateds), B(bootstrap),
+                                 boot_mode, B(returns), num_envs, seq_len, gamma, workspace,
+                                 workspace_bytes, stream);
 }
 
 int rlk_eligibility_traces(const float* gradients, const float* dones, const float* seed_values,
                            float* traces, int64_t num_envs, int64_t seq_len, float gamma,
                            float lambda_, void* workspace, size_t workspace_bytes, void* stream) {
-  if (is_empty(num_envs, seq_len)) return RLK_OK;
-  if (!gradients || !dones || !traces) return RLK_ERR_INVALID_ARGUMENT;
-  DoneGatedForwardOp op{gradients, dones, seed_values, traces, gamma * lambda_, 1};
-  const bool vec = seq_len % 4 == 0 && aligned16(gradients) && aligned16(dones) && aligned16(traces);
-  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  return done_gated_impl(gradients, dones, seed_values, traces, num_envs, seq_len,
+                         gamma * lambda_, 1, workspace, workspace_bytes, stream);
+}
+
+int rlk_eligibility_traces_bf16(const rlk_bf16* gradients, const rlk_bf16* dones,
+                                const rlk_bf16* seed_values, rlk_bf16* traces, int64_t num_envs,
+                                int64_t seq_len, float gamma, float lambda_, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  return done_gated_impl(B(gradients), B(dones), B(seed_values), B(traces), num_envs, seq_len,
+                         gamma * lambda_, 1, workspace, workspace_bytes, stream);
 }
 
 int rlk_prefix_sum(const float* inputs, const float* dones, const float* seed_values,
                    float* prefix_sums, int64_t num_envs, int64_t seq_len, int ends_at,
                    void* workspace, size_t workspace_bytes, void* stream) {
-  if (is_empty(num_envs, seq_len)) return RLK_OK;
-  if (!inputs || !dones || !prefix_sums) return RLK_ERR_INVALID_ARGUMENT;
-  DoneGatedForwardOp op{inputs, dones, seed_values, prefix_sums, 1.f, ends_at ? 1 : 0};
-  const bool vec = seq_len % 4 == 0 && aligned16(inputs) && aligned16(dones) && aligned16(prefix_sums);
-  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  return done_gated_impl(inputs, dones, seed_values, prefix_sums, num_envs, seq_len, 1.f,
+                         ends_at ? 1 : 0, workspace, workspace_bytes, stream);
+}
+
+int rlk_prefix_sum_bf16(const rlk_bf16* inputs, const rlk_bf16* dones,
+                        const rlk_bf16* seed_values, rlk_bf16* prefix_sums, int64_t num_envs,
+                        int64_t seq_len, int ends_at, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  return done_gated_impl(B(inputs), B(dones), B(seed_values), B(prefix_sums), num_envs, seq_len,
+                         1.f, ends_at ? 1 : 0, workspace, workspace_bytes, stream);
 }
 
 int rlk_affine_scan(const float* u, const float* v, const float* carry, float* out,
                     int64_t num_envs, int64_t seq_len, int direction, void* workspace,
                     size_t workspace_bytes, void* stream) {
-  if (is_empty(num_envs, seq_len)) return RLK_OK;
-  if (!u || !v || !out || (direction != RLK_BACKWARD && direction != RLK_FORWARD))
-    return RLK_ERR_INVALID_ARGUMENT;
-  const bool vec = seq_len % 4 == 0 && aligned16(u) && aligned16(v) && aligned16(out);
-  if (direction == RLK_FORWARD) {
-    AffineScanOp<true> op{u, v, carry, out};
-    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
-  }
-  AffineScanOp<false> op{u, v, carry, out};
-  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  return affine_scan_impl(u, v, carry, out, num_envs, seq_len, direction, workspace,
+                          workspace_bytes, stream);
+}
+
+int rlk_affine_scan_bf16(const rlk_bf16* u, const rlk_bf16* v, const rlk_bf16* carry,
+                         rlk_bf16* out, int64_t num_envs, int64_t seq_len, int direction,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  return affine_scan_impl(B(u), B(v), B(carry), B(out), num_envs, seq_len, direction, workspace,
+                          workspace_bytes, stream);
 }
 
 }  // extern "C"

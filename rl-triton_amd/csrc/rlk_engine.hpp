@@ -52,8 +52,48 @@ __device__ __forceinline__ Affine compose(Affine outer, Affine inner) {
 struct NoHalo {};
 
 // ---------------------------------------------------------------------------------------
-// Segment loads / stores.  VEC: T % 4 == 0 and every base pointer 16-byte aligned, so a
-// segment start t0 (a multiple of 4) is 16-byte aligned and each quad is all-in or all-out.
+// Storage types.  Every array of a call is float32 or every one is bfloat16 (the upper half
+// of an IEEE float32, here `bf16`); the arithmetic is float32 either way.  A bfloat16 load
+// widens exactly; a store rounds to nearest even and turns any NaN into 0x7fc0, which is
+// torch's float -> bfloat16 conversion, so a bfloat16 result is the float32 result as
+// torch would round it.
+// ---------------------------------------------------------------------------------------
+struct bf16 {
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return __uint_as_float((uint32_t)x.bits << 16); }
+
+template <class E>
+__device__ __forceinline__ E from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ bf16 from_f32<bf16>(float x) {
+  const uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return bf16{0x7fc0};
+  return bf16{(uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16)};
+}
+
+// Four consecutive elements (16 bytes of float32, 8 of bfloat16) as float32.
+__device__ __forceinline__ float4 load_quad(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 load_quad(const bf16* p) {
+  const uint2 w = *reinterpret_cast<const uint2*>(p);
+  return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                     __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
+}
+__device__ __forceinline__ void store_quad(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+__device__ __forceinline__ void store_quad(bf16* p, float4 v) {
+  const uint32_t a = from_f32<bf16>(v.x).bits, b = from_f32<bf16>(v.y).bits;
+  const uint32_t c = from_f32<bf16>(v.z).bits, d = from_f32<bf16>(v.w).bits;
+  *reinterpret_cast<uint2*>(p) = make_uint2(a | (b << 16), c | (d << 16));
+}
+
+// ---------------------------------------------------------------------------------------
+// Segment loads / stores.  VEC: T % 4 == 0 and every base pointer aligned to four elements
+// (16 bytes for float32, 8 for bfloat16), so a segment start t0 (a multiple of 4) is
+// aligned and each quad is all-in or all-out.
 //
 // Loads are unconditional: a step beyond T reads the row's last quad (or step).  Padding
 // steps are masked to the identity map in coef() and are not stored, so their register
@@ -61,14 +101,14 @@ struct NoHalo {};
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ int clamp_step(int t, int T) { return t < 0 ? 0 : (t < T ? t : T - 1); }
 
-template <int S, bool VEC>
-__device__ __forceinline__ void load_seg(const float* __restrict__ p, int t0, int T, float (&v)[S]) {
+template <int S, bool VEC, class E>
+__device__ __forceinline__ void load_seg(const E* __restrict__ p, int t0, int T, float (&v)[S]) {
   if constexpr (VEC) {
     static_assert(S % 4 == 0, "vector segments hold whole quads");
 #pragma unroll
     for (int q = 0; q < S / 4; ++q) {
       const int t = t0 + 4 * q;
-      const float4 f = *reinterpret_cast<const float4*>(p + (t < T ? t : T - 4));
+      const float4 f = load_quad(p + (t < T ? t : T - 4));
       v[4 * q + 0] = f.x;
       v[4 * q + 1] = f.y;
       v[4 * q + 2] = f.z;
@@ -76,41 +116,44 @@ __device__ __forceinline__ void load_seg(const float* __restrict__ p, int t0, in
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < S; ++i) v[i] = p[t0 + i < T ? t0 + i : T - 1];
+    for (int i = 0; i < S; ++i) v[i] = to_f32(p[t0 + i < T ? t0 + i : T - 1]);
   }
 }
 
 // Steps beyond T are not stored.
-template <int S, bool VEC>
-__device__ __forceinline__ void store_seg(float* __restrict__ p, int t0, int T, const float (&v)[S]) {
+template <int S, bool VEC, class E>
+__device__ __forceinline__ void store_seg(E* __restrict__ p, int t0, int T, const float (&v)[S]) {
   if constexpr (VEC) {
 #pragma unroll
     for (int q = 0; q < S / 4; ++q) {
       const int t = t0 + 4 * q;
-      if (t < T)
-        *reinterpret_cast<float4*>(p + t) = make_float4(v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+      if (t < T) store_quad(p + t, make_float4(v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]));
     }
   } else {
 #pragma unroll
     for (int i = 0; i < S; ++i)
-      if (t0 + i < T) p[t0 + i] = v[i];
+      if (t0 + i < T) p[t0 + i] = from_f32<E>(v[i]);
   }
 }
 
 // A 0.0f that is never written: the source of an unconditional load whose operand is absent.
 // Global (not __constant__) memory, so that selecting between it and a global operand keeps
-// a global load (a flat load would also count against the LDS counter).
+// a global load (a flat load would also count against the LDS counter).  All-zero bits are
+// also a bfloat16 zero.
 __device__ float g_zero[4] = {0.f, 0.f, 0.f, 0.f};
+template <class E>
+__device__ __forceinline__ const E* zero_src() { return reinterpret_cast<const E*>(g_zero); }
 
 // Bootstrap argument shared by the backward estimators: none, one value per row, or
 // one value per step (the reference's last_value / bootstrap_values pair).
 enum BootMode : int { kBootNone = 0, kBootRow = 1, kBootFull = 2 };
 
 // Address of boot(T-1) for `row` (g_zero when there is no bootstrap).
-__device__ __forceinline__ const float* boot_last(const float* boot, int mode, int64_t row, int T) {
+template <class E>
+__device__ __forceinline__ const E* boot_last(const E* boot, int mode, int64_t row, int T) {
   return mode == kBootFull ? boot + row * (int64_t)T + (T - 1)
        : mode == kBootRow  ? boot + row
-                           : g_zero;
+                           : zero_src<E>();
 }
 
 // The bootstrap in two halves, load (raw, unconditional) and prepare:
@@ -119,16 +162,16 @@ __device__ __forceinline__ const float* boot_last(const float* boot, int mode, i
 //   PER_STEP = true:  a per-step array is read in full; with a per-row value (or none) the
 //                     segment loads read `any_row` (any readable [T] row) and are discarded.
 // boot_prepare turns the raw registers into bt[i] = boot(t0 + i).
-template <int S, bool VEC, bool PER_STEP>
-__device__ __forceinline__ void boot_load(const float* __restrict__ boot, int mode, int64_t row,
+template <int S, bool VEC, bool PER_STEP, class E>
+__device__ __forceinline__ void boot_load(const E* __restrict__ boot, int mode, int64_t row,
                                           int t0, int T, float (&seg)[S], float& last,
-                                          const float* any_row) {
+                                          const E* any_row) {
   if constexpr (PER_STEP) {
     load_seg<S, VEC>(mode == kBootFull ? boot + row * (int64_t)T : any_row, t0, T, seg);
     // a per-step array already holds boot(T-1) in the segment that contains T-1
-    last = mode == kBootFull ? 0.f : *boot_last(boot, mode, row, T);
+    last = mode == kBootFull ? 0.f : to_f32(*boot_last(boot, mode, row, T));
   } else {
-    last = *boot_last(boot, mode, row, T);
+    last = to_f32(*boot_last(boot, mode, row, T));
   }
 }
 template <int S, bool PER_STEP>
@@ -144,8 +187,8 @@ __device__ __forceinline__ void boot_prepare(int mode, int t0, int T, float (&bt
 // nullptr for 0.
 template <class Op>
 __device__ __forceinline__ float row_carry(const Op& op, int64_t row, int T) {
-  const float* src = op.row_carry_src(row, T);
-  return src ? *src : 0.f;
+  const auto* src = op.row_carry_src(row, T);
+  return src ? to_f32(*src) : 0.f;
 }
 
 // A halo value of two floats (Retrace: c[t+1] and q[t+1]).
@@ -273,8 +316,8 @@ __device__ __forceinline__ void block_stats(double sum, double sq, double* __res
 // butterfly; the waves in index order), so all agree on the statistics, then rewrites its
 // share of x as
 // (x - mean) / (std + eps), std unbiased (n - 1), as torch computes x.std().
-template <int NT, bool VEC>
-__global__ __launch_bounds__(NT) void normalize_kernel(float* __restrict__ x,
+template <int NT, bool VEC, class E>
+__global__ __launch_bounds__(NT) void normalize_kernel(E* __restrict__ x,
                                                        const double* __restrict__ partials,
                                                        int nparts, int64_t n, float eps) {
   constexpr int NW = NT / kWave;
@@ -287,8 +330,8 @@ __global__ __launch_bounds__(NT) void normalize_kernel(float* __restrict__ x,
   // overlap
   float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f);
   if (first < units) {
-    if constexpr (VEC) v0 = reinterpret_cast<const float4*>(x)[first];
-    else v0.x = x[first];
+    if constexpr (VEC) v0 = load_quad(x + 4 * first);
+    else v0.x = to_f32(x[first]);
   }
   double a = 0.0, b = 0.0;
   for (int i = tid; i < nparts; i += NT) {
@@ -317,17 +360,17 @@ __global__ __launch_bounds__(NT) void normalize_kernel(float* __restrict__ x,
   const float m = (float)mean;
   const float d = (float)sqrt(var) + eps;
   if constexpr (VEC) {
-    float4* x4 = reinterpret_cast<float4*>(x);
     for (int64_t i = first; i < units; i += stride) {
-      float4 v = i == first ? v0 : x4[i];
+      float4 v = i == first ? v0 : load_quad(x + 4 * i);
       v.x = (v.x - m) / d;
       v.y = (v.y - m) / d;
       v.z = (v.z - m) / d;
       v.w = (v.w - m) / d;
-      x4[i] = v;
+      store_quad(x + 4 * i, v);
     }
   } else {
-    for (int64_t i = first; i < units; i += stride) x[i] = ((i == first ? v0.x : x[i]) - m) / d;
+    for (int64_t i = first; i < units; i += stride)
+      x[i] = from_f32<E>(((i == first ? v0.x : to_f32(x[i])) - m) / d);
   }
 }
 

@@ -26,7 +26,7 @@ __device__ __forceinline__ void fill_regs(float (&v)[S], float x) {
 //   add = r + gamma*v_next*(1-term) - v,   mul = gamma*lambda*(1 - done)
 //   done = min(term + trunc, 1) with truncations, term without;   x[T] = 0
 // ------------------------------------------------------------------------------------------
-template <bool TRUNC>
+template <bool TRUNC, class E = float>
 struct GaeOp {
   static constexpr bool kForward = false;
   static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
@@ -34,12 +34,12 @@ struct GaeOp {
   // in registers (no spills at 1024 threads, whose cap is 128 VGPRs)
   static constexpr int kLongThreads = 1024, kLongMaxSegments = 4;
   using Halo = float;  // values[t+1]
-  const float* r;
-  const float* v;
-  const float* term;
-  const float* trunc;  // read iff TRUNC
-  const float* boot;   // nullable, per boot_mode
-  float* out;
+  const E* r;
+  const E* v;
+  const E* term;
+  const E* trunc;  // read iff TRUNC
+  const E* boot;   // nullable, per boot_mode
+  E* out;
   int boot_mode;
   float gamma, gl;  // gl = gamma*lambda
 
@@ -65,7 +65,7 @@ struct GaeOp {
   }
   template <int S>
   __device__ float export_first(const Regs<S>& R) const { return R.v[0]; }
-  __device__ float halo_load(int64_t row, int t, int T) const { return v[row * (int64_t)T + t]; }
+  __device__ float halo_load(int64_t row, int t, int T) const { return to_f32(v[row * (int64_t)T + t]); }
 
   template <int S>
   __device__ void coef(const Regs<S>& R, float vh, int64_t, int t0, int T, float (&mul)[S],
@@ -82,7 +82,7 @@ struct GaeOp {
       mul[i] = in ? gl * (1.f - done) : 1.f;
     }
   }
-  __device__ const float* row_carry_src(int64_t, int) const { return nullptr; }
+  __device__ const E* row_carry_src(int64_t, int) const { return nullptr; }
 
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>&, float, const float (&xs)[S], float, int64_t row, int t0,
@@ -100,13 +100,13 @@ struct GaeOp {
 // block_stats in rlk_engine.hpp).  normalize_kernel then turns A into
 // (A - mean) / (std + eps) in place.
 // ------------------------------------------------------------------------------------------
-template <bool TRUNC>
-struct GaeStatsOp : GaeOp<TRUNC> {
+template <bool TRUNC, class E = float>
+struct GaeStatsOp : GaeOp<TRUNC, E> {
   static constexpr bool kBlockStats = true;
-  float* returns;
+  E* returns;
   double* partials;
   template <int S>
-  using Regs = typename GaeOp<TRUNC>::template Regs<S>;
+  using Regs = typename GaeOp<TRUNC, E>::template Regs<S>;
 
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>& R, float, const float (&xs)[S], float, int64_t row, int t0,
@@ -131,21 +131,21 @@ struct GaeStatsOp : GaeOp<TRUNC> {
 // The reference passes targets[t+1] through global memory (store, barrier, reload,
 // vtrace_fused.py:149-152); here it is the neighbouring register or lane.
 // ------------------------------------------------------------------------------------------
-template <bool TRUNC>
+template <bool TRUNC, class E = float>
 struct VtraceOp {
   static constexpr bool kForward = false;
   static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
   static constexpr int kLongThreads = 1024, kLongMaxSegments = 2;
   using Halo = float;  // values[t+1]
-  const float* lpt;
-  const float* lpb;
-  const float* v;
-  const float* r;
-  const float* term;
-  const float* trunc;  // read iff TRUNC
-  const float* boot;   // nullable, per boot_mode
-  float* targets;
-  float* adv;
+  const E* lpt;
+  const E* lpb;
+  const E* v;
+  const E* r;
+  const E* term;
+  const E* trunc;  // read iff TRUNC
+  const E* boot;   // nullable, per boot_mode
+  E* targets;
+  E* adv;
   int boot_mode;
   float gamma, rho_bar, c_bar;
 
@@ -179,7 +179,7 @@ struct VtraceOp {
   }
   template <int S>
   __device__ float export_first(const Regs<S>& R) const { return R.v[0]; }
-  __device__ float halo_load(int64_t row, int t, int T) const { return v[row * (int64_t)T + t]; }
+  __device__ float halo_load(int64_t row, int t, int T) const { return to_f32(v[row * (int64_t)T + t]); }
 
   // continuation value at step t from the raw next-step value (values or targets)
   __device__ __forceinline__ float next_value(float raw, float tr, float bt, int t, int T) const {
@@ -201,7 +201,7 @@ struct VtraceOp {
       mul[i] = in ? gamma * R.c[i] * (1.f - done) : 1.f;
     }
   }
-  __device__ const float* row_carry_src(int64_t, int) const { return nullptr; }
+  __device__ const E* row_carry_src(int64_t, int) const { return nullptr; }
 
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>& R, float vh, const float (&xs)[S], float x_next, int64_t row,
@@ -229,22 +229,22 @@ struct VtraceOp {
 //   Q_ret = x + q;  advantages = rho*(r + gamma*Q_ret[t+1]*(1-term) - q),  Q_ret[T] = 0
 // NA > 0: compile-time action count (vector loads of the [S, A] block); NA == 0: runtime A.
 // ------------------------------------------------------------------------------------------
-template <int NA, bool TRUNC>
+template <int NA, bool TRUNC, class E = float>
 struct RetraceOp {
   static constexpr bool kForward = false;
   static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
   static constexpr int kLongThreads = 512, kLongMaxSegments = 2;  // 256 VGPRs: the A-wide rows
   using Halo = Halo2;  // {c[t+1], q[t+1]}
-  const float* pi;     // [E, T, A]
-  const float* mu;     // [E, T]
-  const float* q;
-  const float* nq;     // [E, T, A]
+  const E* pi;     // [E, T, A]
+  const E* mu;     // [E, T]
+  const E* q;
+  const E* nq;     // [E, T, A]
   const int64_t* act;  // [E, T]
-  const float* r;
-  const float* term;
-  const float* trunc;  // read iff TRUNC
-  float* targets;
-  float* adv;
+  const E* r;
+  const E* term;
+  const E* trunc;  // read iff TRUNC
+  E* targets;
+  E* adv;
   int A;
   float gamma, lambda, c_bar, rho_bar;
 
@@ -254,13 +254,14 @@ struct RetraceOp {
   };
 
   // (rho, c, E_pi[Q']) at one step from its action row
-  __device__ __forceinline__ void step_terms(const float* p, const float* n, int64_t a_t, float m,
+  template <class P>
+  __device__ __forceinline__ void step_terms(const P* p, const P* n, int64_t a_t, float m,
                                              float& rho, float& c, float& enq) const {
     float e = 0.f, pa = 0.f;
     const int na = NA > 0 ? NA : A;
     for (int a = 0; a < na; ++a) {
-      const float pv = p[a];
-      e = fmaf(pv, n[a], e);
+      const float pv = to_f32(p[a]);
+      e = fmaf(pv, to_f32(n[a]), e);
       pa = (a == a_t) ? pv : pa;
     }
     const float ratio = pa / m;
@@ -289,13 +290,13 @@ struct RetraceOp {
       // row's first quad instead.  (Larger blocks take the per-step path below: two tiles
       // of them would not fit the register file.)
       float pb[S * NA], nb[S * NA];
-      const float* pp = pi + (o + t0) * NA;
-      const float* np = nq + (o + t0) * NA;
+      const E* pp = pi + (o + t0) * NA;
+      const E* np = nq + (o + t0) * NA;
 #pragma unroll
       for (int qd = 0; qd < S * NA / 4; ++qd) {
         const bool in = t0 + (4 * qd) / NA < T;
-        const float4 a4 = *reinterpret_cast<const float4*>(in ? pp + 4 * qd : pi + o * NA);
-        const float4 b4 = *reinterpret_cast<const float4*>(in ? np + 4 * qd : nq + o * NA);
+        const float4 a4 = load_quad(in ? pp + 4 * qd : pi + o * NA);
+        const float4 b4 = load_quad(in ? np + 4 * qd : nq + o * NA);
         pb[4 * qd] = a4.x, pb[4 * qd + 1] = a4.y, pb[4 * qd + 2] = a4.z, pb[4 * qd + 3] = a4.w;
         nb[4 * qd] = b4.x, nb[4 * qd + 1] = b4.y, nb[4 * qd + 2] = b4.z, nb[4 * qd + 3] = b4.w;
       }
@@ -318,8 +319,8 @@ struct RetraceOp {
     const int64_t i = row * (int64_t)T + t;
     const int na = NA > 0 ? NA : A;
     float rho, c, enq;
-    step_terms(pi + i * na, nq + i * na, act[i], mu[i], rho, c, enq);
-    return Halo2{c, q[i]};
+    step_terms(pi + i * na, nq + i * na, act[i], to_f32(mu[i]), rho, c, enq);
+    return Halo2{c, to_f32(q[i])};
   }
 
   template <int S>
@@ -336,7 +337,7 @@ struct RetraceOp {
       mul[i] = in ? gamma * c_next * (1.f - done) : 1.f;
     }
   }
-  __device__ const float* row_carry_src(int64_t, int) const { return nullptr; }
+  __device__ const E* row_carry_src(int64_t, int) const { return nullptr; }
 
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>& R, Halo2 h, const float (&xs)[S], float x_next, int64_t row,
@@ -363,18 +364,18 @@ struct RetraceOp {
 // Discounted returns: kernels/discounted_returns_fused.py:50-82 -- the same with
 //   add = r + gamma*trunc*boot(t),  mul = gamma*nd  (NV = false: no next values).
 // ------------------------------------------------------------------------------------------
-template <bool NV, bool TRUNC>
+template <bool NV, bool TRUNC, class E = float>
 struct ReturnsOp {
   static constexpr bool kForward = false;
   static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
   static constexpr int kLongThreads = 1024, kLongMaxSegments = (NV || TRUNC) ? 4 : 8;
   using Halo = NoHalo;
-  const float* r;
-  const float* nv;     // read iff NV
-  const float* term;
-  const float* trunc;  // read iff TRUNC
-  const float* boot;   // nullable, per boot_mode
-  float* out;
+  const E* r;
+  const E* nv;     // read iff NV
+  const E* term;
+  const E* trunc;  // read iff TRUNC
+  const E* boot;   // nullable, per boot_mode
+  E* out;
   int boot_mode;
   float gamma, g1l, gl;  // gamma, gamma*(1-lambda), gamma*lambda (discounted: gl = gamma)
 
@@ -418,7 +419,7 @@ struct ReturnsOp {
       mul[i] = in ? gl * nd : 1.f;
     }
   }
-  __device__ const float* row_carry_src(int64_t row, int T) const {
+  __device__ const E* row_carry_src(int64_t row, int T) const {
     return boot_mode == kBootNone ? nullptr : boot_last(boot, boot_mode, row, T);
   }
 
@@ -437,15 +438,16 @@ struct ReturnsOp {
 //       ends_at:   mul = 1 - done[t-1];  starts_at: mul = 1 - done[t];  add = x, x[-1] = seed
 // (decay = gamma*lambda for traces, 1 for the prefix sum)
 // ------------------------------------------------------------------------------------------
+template <class E = float>
 struct DoneGatedForwardOp {
   static constexpr bool kForward = true;
   static constexpr bool kBlockStats = false;
   static constexpr int kLongThreads = 1024, kLongMaxSegments = 8;
   using Halo = float;  // done[t-1]
-  const float* x;
-  const float* dones;
-  const float* seed;  // nullable
-  float* out;
+  const E* x;
+  const E* dones;
+  const E* seed;  // nullable
+  E* out;
   float decay;
   int ends_at;
 
@@ -464,7 +466,7 @@ struct DoneGatedForwardOp {
   __device__ void prepare(Regs<S>&, int64_t, int, int) const {}
   template <int S>
   __device__ float export_last(const Regs<S>& R) const { return R.d[S - 1]; }
-  __device__ float halo_load(int64_t row, int t, int T) const { return dones[row * (int64_t)T + t]; }
+  __device__ float halo_load(int64_t row, int t, int T) const { return to_f32(dones[row * (int64_t)T + t]); }
 
   template <int S>
   __device__ void coef(const Regs<S>& R, float dh, int64_t, int t0, int T, float (&mul)[S],
@@ -480,7 +482,7 @@ struct DoneGatedForwardOp {
       add[i] = in ? R.x[i] : 0.f;
     }
   }
-  __device__ const float* row_carry_src(int64_t row, int) const { return seed ? seed + row : nullptr; }
+  __device__ const E* row_carry_src(int64_t row, int) const { return seed ? seed + row : nullptr; }
 
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>&, float, const float (&xs)[S], float, int64_t row, int t0,
@@ -493,16 +495,16 @@ struct DoneGatedForwardOp {
 // Generic affine scans (ops/_scan.py:69-213, kernels/scan.py:39-138):
 //   backward A[t] = u[t] + v[t]*A[t+1], A[T] = carry;  forward e[t] = u[t] + v[t]*e[t-1], e[-1] = carry
 // ------------------------------------------------------------------------------------------
-template <bool FWD>
+template <bool FWD, class E = float>
 struct AffineScanOp {
   static constexpr bool kForward = FWD;
   static constexpr bool kBlockStats = false;
   static constexpr int kLongThreads = 1024, kLongMaxSegments = 8;
   using Halo = NoHalo;
-  const float* u;
-  const float* v;
-  const float* carry;  // nullable, [E]
-  float* out;
+  const E* u;
+  const E* v;
+  const E* carry;  // nullable, [E]
+  E* out;
 
   template <int S>
   struct Regs {
@@ -526,7 +528,7 @@ struct AffineScanOp {
       add[i] = in ? R.u[i] : 0.f;
     }
   }
-  __device__ const float* row_carry_src(int64_t row, int) const { return carry ? carry + row : nullptr; }
+  __device__ const E* row_carry_src(int64_t row, int) const { return carry ? carry + row : nullptr; }
   template <int S, bool VEC>
   __device__ void emit(const Regs<S>&, NoHalo, const float (&xs)[S], float, int64_t row, int t0,
                        int T) const {

@@ -22,6 +22,7 @@
 
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #include "rl_triton_amd.h"
 
@@ -41,13 +42,19 @@ PyObject* decline() { Py_RETURN_NONE; }
 struct Call {
   c10::DeviceIndex dev = -1;
   int64_t E = 0, T = 0;
+  at::ScalarType io = at::kFloat;  // the storage type of every float tensor of the call
   bool ok = true;
 
-  // The leading [E, T] float32 tensor: fixes device and shape for the rest.
+  bool bf16() const { return io == at::kBFloat16; }
+
+  // The leading [E, T] float32 or bfloat16 tensor: fixes device, shape and storage type
+  // for the rest.
   const at::Tensor* lead(PyObject* o) {
     if (!ok || !THPVariable_Check(o)) return fail();
     const at::Tensor& t = THPVariable_Unpack(o);
-    if (!t.is_cuda() || t.dim() != 2 || t.scalar_type() != at::kFloat || !t.is_contiguous())
+    io = t.scalar_type();
+    if (!t.is_cuda() || t.dim() != 2 || (io != at::kFloat && io != at::kBFloat16) ||
+        !t.is_contiguous())
       return fail();
     dev = t.get_device();
     E = t.size(0);
@@ -55,8 +62,11 @@ struct Call {
     if (dev != c10::hip::current_device() || T > kNoWorkspaceMaxT) return fail();
     return &t;
   }
-  // A tensor of shape [E, T] (or [E] / [E, T, A]) on the same device.
-  const at::Tensor* need(PyObject* o, int kind = 2, int64_t A = 0, at::ScalarType st = at::kFloat) {
+  // A tensor of shape [E, T] (or [E] / [E, T, A]) on the same device, of the call's storage
+  // type unless `st` names another.
+  const at::Tensor* need(PyObject* o, int kind = 2, int64_t A = 0,
+                         at::ScalarType st = at::ScalarType::Undefined) {
+    if (st == at::ScalarType::Undefined) st = io;
     if (!ok || !THPVariable_Check(o)) return fail();
     const at::Tensor& t = THPVariable_Unpack(o);
     if (!t.is_cuda() || t.get_device() != dev || t.scalar_type() != st || !t.is_contiguous())
@@ -92,8 +102,29 @@ struct Call {
   at::Tensor output(const at::Tensor& like) const { return at::empty({E, T}, like.options()); }
 };
 
-const float* fp(const at::Tensor* t) { return t ? t->data_ptr<float>() : nullptr; }
-float* fp_out(at::Tensor& t) { return t.data_ptr<float>(); }
+// Typed data pointers (T = float or rlk_bf16) of an input (nullable) and of an output.
+template <class T>
+const T* in_ptr(const at::Tensor* t) {
+  return t ? static_cast<const T*>(t->data_ptr()) : nullptr;
+}
+template <class T>
+T* out_ptr(at::Tensor& t) {
+  return static_cast<T*>(t.data_ptr());
+}
+
+// The entry point for storage type T: `f32` for float, its `_bf16` twin for rlk_bf16.
+template <class T, class F32, class BF16>
+constexpr auto pick(F32 f32, BF16 bf16) {
+  if constexpr (std::is_same_v<T, float>) return f32;
+  else return bf16;
+}
+
+// Runs `body` with a value of the call's storage type; body(x) picks the entry point and
+// pointer types from decltype(x).
+template <class Body>
+int dispatch(const Call& c, Body body) {
+  return c.bf16() ? body(rlk_bf16{}) : body(0.f);
+}
 
 PyObject* finish(int status, const char* what, PyObject* result) {
   if (status != RLK_OK) {
@@ -136,8 +167,11 @@ PyObject* op_gae(PyObject* const* a, Py_ssize_t n) {
   if (!c.ok) return decline();
   const int mode = has_lv ? RLK_BOOT_ROW : has_bv ? RLK_BOOT_FULL : RLK_BOOT_NONE;
   at::Tensor out = c.output(*r);
-  const int st = rlk_gae(fp(r), fp(v), fp(te), fp(tr), fp(boot), mode, fp_out(out), c.E, c.T,
-                         gamma, lam, nullptr, 0, c.stream());
+  const int st = dispatch(c, [&](auto z) {
+    using T = decltype(z);
+    return pick<T>(rlk_gae, rlk_gae_bf16)(in_ptr<T>(r), in_ptr<T>(v), in_ptr<T>(te), in_ptr<T>(tr),
+      in_ptr<T>(boot), mode, out_ptr<T>(out), c.E, c.T, gamma, lam, nullptr, 0, c.stream());
+  });
   return finish(st, "rlk_gae", THPVariable_Wrap(std::move(out)));
 }
 
@@ -161,9 +195,12 @@ PyObject* op_gae_normalized(PyObject* const* a, Py_ssize_t n) {
   at::Tensor adv = c.output(*r), ret = c.output(*r);
   const size_t pb = rlk_gae_normalized_partials_bytes(c.E, c.T);
   at::Tensor parts = at::empty({(int64_t)(pb > 0 ? pb : 8)}, r->options().dtype(at::kByte));
-  const int st = rlk_gae_normalized(fp(r), fp(v), fp(te), fp(tr), fp(boot), mode, fp_out(adv),
-                                    fp_out(ret), c.E, c.T, gamma, lam, eps, nullptr, 0,
-                                    parts.data_ptr(), pb, c.stream());
+  const int st = dispatch(c, [&](auto z) {
+    using T = decltype(z);
+    return pick<T>(rlk_gae_normalized, rlk_gae_normalized_bf16)(in_ptr<T>(r), in_ptr<T>(v),
+      in_ptr<T>(te), in_ptr<T>(tr), in_ptr<T>(boot), mode, out_ptr<T>(adv), out_ptr<T>(ret), c.E,
+      c.T, gamma, lam, eps, nullptr, 0, parts.data_ptr(), pb, c.stream());
+  });
   return finish(st, "rlk_gae_normalized", pair(adv, ret));
 }
 
@@ -186,9 +223,12 @@ PyObject* op_vtrace(PyObject* const* a, Py_ssize_t n) {
   if (!c.ok) return decline();
   const int mode = has_lv ? RLK_BOOT_ROW : has_bv ? RLK_BOOT_FULL : RLK_BOOT_NONE;
   at::Tensor tg = c.output(*r), adv = c.output(*r);
-  const int st = rlk_vtrace(fp(lpt), fp(lpb), fp(v), fp(r), fp(te), fp(tr), fp(boot), mode,
-                            fp_out(tg), fp_out(adv), c.E, c.T, gamma, rho_bar, c_bar, nullptr, 0,
-                            c.stream());
+  const int st = dispatch(c, [&](auto z) {
+    using T = decltype(z);
+    return pick<T>(rlk_vtrace, rlk_vtrace_bf16)(in_ptr<T>(lpt), in_ptr<T>(lpb), in_ptr<T>(v),
+      in_ptr<T>(r), in_ptr<T>(te), in_ptr<T>(tr), in_ptr<T>(boot), mode, out_ptr<T>(tg),
+      out_ptr<T>(adv), c.E, c.T, gamma, rho_bar, c_bar, nullptr, 0, c.stream());
+  });
   return finish(st, "rlk_vtrace", pair(tg, adv));
 }
 
@@ -216,9 +256,13 @@ PyObject* op_retrace(PyObject* const* a, Py_ssize_t n) {
               rho_bar = c.scalar(a[11]);
   if (!c.ok) return decline();
   at::Tensor tg = c.output(*r), adv = c.output(*r);
-  const int st = rlk_retrace(fp(pi), fp(mu), fp(q), fp(nq), act->data_ptr<int64_t>(), fp(r),
-                             fp(te), fp(tr), fp_out(tg), fp_out(adv), c.E, c.T, A, gamma, lam,
-                             c_bar, rho_bar, nullptr, 0, c.stream());
+  const int st = dispatch(c, [&](auto z) {
+    using T = decltype(z);
+    return pick<T>(rlk_retrace, rlk_retrace_bf16)(in_ptr<T>(pi), in_ptr<T>(mu), in_ptr<T>(q),
+      in_ptr<T>(nq), act->data_ptr<int64_t>(), in_ptr<T>(r), in_ptr<T>(te), in_ptr<T>(tr),
+      out_ptr<T>(tg), out_ptr<T>(adv), c.E, c.T, A, gamma, lam, c_bar, rho_bar, nullptr, 0,
+      c.stream());
+  });
   return finish(st, "rlk_retrace", pair(tg, adv));
 }
 
@@ -235,9 +279,12 @@ PyObject* op_lambda_returns(PyObject* const* a, Py_ssize_t n) {
   const at::Tensor* boot = c.opt(a[6]);
   if (!c.ok) return decline();
   at::Tensor out = c.output(*r);
-  const int st = rlk_lambda_returns(fp(r), fp(nv), fp(te), fp(tr), fp(boot),
-                                    boot ? RLK_BOOT_FULL : RLK_BOOT_NONE, fp_out(out), c.E, c.T,
-                                    gamma, lam, nullptr, 0, c.stream());
+  const int st = dispatch(c, [&](auto z) {
+    using T = decltype(z);
+    return pick<T>(rlk_lambda_returns, rlk_lambda_returns_bf16)(in_ptr<T>(r), in_ptr<T>(nv),
+      in_ptr<T>(te), in_ptr<T>(tr), in_ptr<T>(boot), boot ? RLK_BOOT_FULL : RLK_BOOT_NONE,
+      out_ptr<T>(out), c.E, c.T, gamma, lam, nullptr, 0, c.stream());
+  });
   return finish(st, "rlk_lambda_returns", THPVariable_Wrap(std::move(out)));
 }
 
@@ -253,9 +300,12 @@ PyObject* op_discounted_returns(PyObject* const* a, Py_ssize_t n) {
   const at::Tensor* boot = c.opt(a[4]);
   if (!c.ok) return decline();
   at::Tensor out = c.output(*r);
-  const int st = rlk_discounted_returns(fp(r), fp(te), fp(tr), fp(boot),
-                                        boot ? RLK_BOOT_FULL : RLK_BOOT_NONE, fp_out(out), c.E,
-                                        c.T, gamma, nullptr, 0, c.stream());
+  const int st = dispatch(c, [&](auto z) {
+    using T = decltype(z);
+    return pick<T>(rlk_discounted_returns, rlk_discounted_returns_bf16)(in_ptr<T>(r), in_ptr<T>(te),
+      in_ptr<T>(tr), in_ptr<T>(boot), boot ? RLK_BOOT_FULL : RLK_BOOT_NONE, out_ptr<T>(out), c.E,
+      c.T, gamma, nullptr, 0, c.stream());
+  });
   return finish(st, "rlk_discounted_returns", THPVariable_Wrap(std::move(out)));
 }
 
@@ -270,8 +320,11 @@ PyObject* op_eligibility_traces(PyObject* const* a, Py_ssize_t n) {
   const at::Tensor* seed = c.opt(a[4], 1);
   if (!c.ok) return decline();
   at::Tensor out = c.output(*g);
-  const int st = rlk_eligibility_traces(fp(g), fp(d), fp(seed), fp_out(out), c.E, c.T, gamma,
-                                        lam, nullptr, 0, c.stream());
+  const int st = dispatch(c, [&](auto z) {
+    using T = decltype(z);
+    return pick<T>(rlk_eligibility_traces, rlk_eligibility_traces_bf16)(in_ptr<T>(g), in_ptr<T>(d),
+      in_ptr<T>(seed), out_ptr<T>(out), c.E, c.T, gamma, lam, nullptr, 0, c.stream());
+  });
   return finish(st, "rlk_eligibility_traces", THPVariable_Wrap(std::move(out)));
 }
 
@@ -285,8 +338,11 @@ PyObject* op_prefix_sum(PyObject* const* a, Py_ssize_t n) {
   const at::Tensor* seed = c.opt(a[2], 1);
   if (!c.ok || !PyBool_Check(a[3])) return decline();
   at::Tensor out = c.output(*x);
-  const int st = rlk_prefix_sum(fp(x), fp(d), fp(seed), fp_out(out), c.E, c.T,
-                                a[3] == Py_True ? 1 : 0, nullptr, 0, c.stream());
+  const int st = dispatch(c, [&](auto z) {
+    using T = decltype(z);
+    return pick<T>(rlk_prefix_sum, rlk_prefix_sum_bf16)(in_ptr<T>(x), in_ptr<T>(d), in_ptr<T>(seed),
+      out_ptr<T>(out), c.E, c.T, a[3] == Py_True ? 1 : 0, nullptr, 0, c.stream());
+  });
   return finish(st, "rlk_prefix_sum", THPVariable_Wrap(std::move(out)));
 }
 
@@ -301,8 +357,11 @@ PyObject* op_affine_scan(PyObject* const* a, Py_ssize_t n) {
   const long dir = PyLong_CheckExact(a[3]) ? PyLong_AsLong(a[3]) : -1;
   if (!c.ok || (dir != RLK_BACKWARD && dir != RLK_FORWARD)) return decline();
   at::Tensor out = c.output(*u);
-  const int st = rlk_affine_scan(fp(u), fp(v), fp(carry), fp_out(out), c.E, c.T, (int)dir,
-                                 nullptr, 0, c.stream());
+  const int st = dispatch(c, [&](auto z) {
+    using T = decltype(z);
+    return pick<T>(rlk_affine_scan, rlk_affine_scan_bf16)(in_ptr<T>(u), in_ptr<T>(v),
+      in_ptr<T>(carry), out_ptr<T>(out), c.E, c.T, (int)dir, nullptr, 0, c.stream());
+  });
   return finish(st, "rlk_affine_scan", THPVariable_Wrap(std::move(out)));
 }
 

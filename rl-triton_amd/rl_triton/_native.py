@@ -48,6 +48,12 @@ SIGNATURES = {
     "rlk_status_string": [_INT],
     "rlk_version": [],
 }
+# the bfloat16 twins take the same arguments (rlk_bf16 arrays in place of float ones)
+for _name in ("rlk_gae", "rlk_gae_normalized", "rlk_vtrace", "rlk_retrace", "rlk_lambda_returns",
+              "rlk_discounted_returns", "rlk_eligibility_traces", "rlk_prefix_sum",
+              "rlk_affine_scan"):
+    SIGNATURES[_name + "_bf16"] = SIGNATURES[_name]
+del _name
 _RESTYPES = {"rlk_workspace_bytes": _SZ, "rlk_gae_normalized_partials_bytes": _SZ,
              "rlk_status_string": ctypes.c_char_p}
 
@@ -102,6 +108,7 @@ def load():
 # a short per-call path: a few C-level tensor queries per argument.
 # ---------------------------------------------------------------------------------------
 _F32 = torch.float32
+_BF16 = torch.bfloat16
 _I64 = torch.int64
 _raw_stream = torch._C._cuda_getCurrentRawStream
 _cur_device = torch._C._cuda_getDevice
@@ -118,8 +125,18 @@ def _ptr(t, name, shape, dev, dtype=_F32) -> int:
     return t.data_ptr()
 
 
-def _opt(t, name, shape, dev):
-    return None if t is None else _ptr(t, name, shape, dev)
+def _opt(t, name, shape, dev, dtype=_F32):
+    return None if t is None else _ptr(t, name, shape, dev, dtype)
+
+
+def _entry(lib, name, dtype):
+    """The C entry point for arrays of `dtype`: `name` for float32, its `_bf16` twin for
+    bfloat16 (every float array of a call has the leading tensor's dtype)."""
+    if dtype is _F32:
+        return getattr(lib, name)
+    if dtype is _BF16:
+        return getattr(lib, name + "_bf16")
+    raise ValueError(f"{name}: expected float32 or bfloat16 tensors, got {dtype}")
 
 
 def _device_of(t) -> int:
@@ -203,12 +220,12 @@ def _launch(fn, what, dev, n_env, n_t, *args):
         _check(status, what)
 
 
-def _boot_args(boot, n_env, n_t, dev):
+def _boot_args(boot, n_env, n_t, dev, dtype=_F32):
     if boot is None:
         return None, BOOT_NONE
     if boot.dim() == 1:
-        return _ptr(boot, "bootstrap", torch.Size((n_env,)), dev), BOOT_ROW
-    return _ptr(boot, "bootstrap", torch.Size((n_env, n_t)), dev), BOOT_FULL
+        return _ptr(boot, "bootstrap", torch.Size((n_env,)), dev, dtype), BOOT_ROW
+    return _ptr(boot, "bootstrap", torch.Size((n_env, n_t)), dev, dtype), BOOT_FULL
 
 
 # ---------------------------------------------------------------------------------------
@@ -217,13 +234,14 @@ def _boot_args(boot, n_env, n_t, dev):
 def gae(rewards, values, terminateds, truncateds, bootstrap, out, gamma, lambda_):
     dev = _device_of(rewards)
     shape = rewards.shape
+    dt = rewards.dtype
     n_env, n_t = shape
     lib = _lib or load()
-    bp, mode = _boot_args(bootstrap, n_env, n_t, dev)
-    _launch(lib.rlk_gae, "rlk_gae", dev, n_env, n_t,
-            _ptr(rewards, "rewards", shape, dev), _ptr(values, "values", shape, dev),
-            _ptr(terminateds, "terminateds", shape, dev), _opt(truncateds, "truncateds", shape, dev),
-            bp, mode, _ptr(out, "out", shape, dev), n_env, n_t, gamma, lambda_)
+    bp, mode = _boot_args(bootstrap, n_env, n_t, dev, dt)
+    _launch(_entry(lib, "rlk_gae", dt), "rlk_gae", dev, n_env, n_t,
+            _ptr(rewards, "rewards", shape, dev, dt), _ptr(values, "values", shape, dev, dt),
+            _ptr(terminateds, "terminateds", shape, dev, dt), _opt(truncateds, "truncateds", shape, dev, dt),
+            bp, mode, _ptr(out, "out", shape, dev, dt), n_env, n_t, gamma, lambda_)
     return out
 
 
@@ -231,12 +249,13 @@ def gae_normalized(rewards, values, terminateds, truncateds, bootstrap, advantag
                    lambda_, eps):
     dev = _device_of(rewards)
     shape = rewards.shape
+    dt = rewards.dtype
     n_env, n_t = shape
     lib = _lib or load()
-    bp, mode = _boot_args(bootstrap, n_env, n_t, dev)
-    args = (_ptr(rewards, "rewards", shape, dev), _ptr(values, "values", shape, dev),
-            _ptr(terminateds, "terminateds", shape, dev), _opt(truncateds, "truncateds", shape, dev),
-            bp, mode, _ptr(advantages, "advantages", shape, dev), _ptr(returns, "returns", shape, dev),
+    bp, mode = _boot_args(bootstrap, n_env, n_t, dev, dt)
+    args = (_ptr(rewards, "rewards", shape, dev, dt), _ptr(values, "values", shape, dev, dt),
+            _ptr(terminateds, "terminateds", shape, dev, dt), _opt(truncateds, "truncateds", shape, dev, dt),
+            bp, mode, _ptr(advantages, "advantages", shape, dev, dt), _ptr(returns, "returns", shape, dev, dt),
             n_env, n_t, gamma, lambda_, eps)
     if dev != _cur_device():
         with torch.cuda.device(dev):
@@ -245,7 +264,7 @@ def gae_normalized(rewards, values, terminateds, truncateds, bootstrap, advantag
     stream = _raw_stream(dev)
     ws, wsb = _workspace(dev, stream, n_env, n_t)
     pp, ppb = _partials_buffer(dev, stream, n_env, n_t) if n_env * n_t > 0 else (None, 0)
-    status = lib.rlk_gae_normalized(*args, ws, wsb, pp, ppb, stream)
+    status = _entry(lib, "rlk_gae_normalized", dt)(*args, ws, wsb, pp, ppb, stream)
     if status != 0:
         _check(status, "rlk_gae_normalized")
     return advantages, returns
@@ -255,15 +274,16 @@ def vtrace(log_pi_target, log_pi_behavior, values, rewards, terminateds, truncat
            targets, advantages, gamma, rho_bar, c_bar):
     dev = _device_of(rewards)
     shape = rewards.shape
+    dt = rewards.dtype
     n_env, n_t = shape
     lib = _lib or load()
-    bp, mode = _boot_args(bootstrap, n_env, n_t, dev)
-    _launch(lib.rlk_vtrace, "rlk_vtrace", dev, n_env, n_t,
-            _ptr(log_pi_target, "log_pi_target", shape, dev),
-            _ptr(log_pi_behavior, "log_pi_behavior", shape, dev),
-            _ptr(values, "values", shape, dev), _ptr(rewards, "rewards", shape, dev),
-            _ptr(terminateds, "terminateds", shape, dev), _opt(truncateds, "truncateds", shape, dev),
-            bp, mode, _ptr(targets, "targets", shape, dev), _ptr(advantages, "advantages", shape, dev),
+    bp, mode = _boot_args(bootstrap, n_env, n_t, dev, dt)
+    _launch(_entry(lib, "rlk_vtrace", dt), "rlk_vtrace", dev, n_env, n_t,
+            _ptr(log_pi_target, "log_pi_target", shape, dev, dt),
+            _ptr(log_pi_behavior, "log_pi_behavior", shape, dev, dt),
+            _ptr(values, "values", shape, dev, dt), _ptr(rewards, "rewards", shape, dev, dt),
+            _ptr(terminateds, "terminateds", shape, dev, dt), _opt(truncateds, "truncateds", shape, dev, dt),
+            bp, mode, _ptr(targets, "targets", shape, dev, dt), _ptr(advantages, "advantages", shape, dev, dt),
             n_env, n_t, gamma, rho_bar, c_bar)
     return targets, advantages
 
@@ -272,6 +292,7 @@ def retrace(action_probs_target, action_probs_behavior, q_values, next_q_values_
             rewards, terminateds, truncateds, targets, advantages, gamma, lambda_, c_bar, rho_bar):
     dev = _device_of(rewards)
     shape = rewards.shape
+    dt = rewards.dtype
     n_env, n_t = shape
     if action_probs_target.dim() != 3:
         raise ValueError("action_probs_target must be [num_envs, seq_len, num_actions]")
@@ -280,15 +301,15 @@ def retrace(action_probs_target, action_probs_behavior, q_values, next_q_values_
     if n_act == 0 and n_env * n_t > 0:
         raise ValueError("num_actions must be positive")
     lib = _lib or load()
-    _launch(lib.rlk_retrace, "rlk_retrace", dev, n_env, n_t,
-            _ptr(action_probs_target, "action_probs_target", shape3, dev),
-            _ptr(action_probs_behavior, "action_probs_behavior", shape, dev),
-            _ptr(q_values, "q_values", shape, dev),
-            _ptr(next_q_values_all, "next_q_values_all", shape3, dev),
+    _launch(_entry(lib, "rlk_retrace", dt), "rlk_retrace", dev, n_env, n_t,
+            _ptr(action_probs_target, "action_probs_target", shape3, dev, dt),
+            _ptr(action_probs_behavior, "action_probs_behavior", shape, dev, dt),
+            _ptr(q_values, "q_values", shape, dev, dt),
+            _ptr(next_q_values_all, "next_q_values_all", shape3, dev, dt),
             _ptr(actions, "actions", shape, dev, _I64),
-            _ptr(rewards, "rewards", shape, dev), _ptr(terminateds, "terminateds", shape, dev),
-            _opt(truncateds, "truncateds", shape, dev),
-            _ptr(targets, "targets", shape, dev), _ptr(advantages, "advantages", shape, dev),
+            _ptr(rewards, "rewards", shape, dev, dt), _ptr(terminateds, "terminateds", shape, dev, dt),
+            _opt(truncateds, "truncateds", shape, dev, dt),
+            _ptr(targets, "targets", shape, dev, dt), _ptr(advantages, "advantages", shape, dev, dt),
             n_env, n_t, max(n_act, 1), gamma, lambda_, c_bar, rho_bar)
     return targets, advantages
 
@@ -296,37 +317,40 @@ def retrace(action_probs_target, action_probs_behavior, q_values, next_q_values_
 def lambda_returns(rewards, next_values, terminateds, truncateds, bootstrap, out, gamma, lambda_):
     dev = _device_of(rewards)
     shape = rewards.shape
+    dt = rewards.dtype
     n_env, n_t = shape
     lib = _lib or load()
-    bp, mode = _boot_args(bootstrap, n_env, n_t, dev)
-    _launch(lib.rlk_lambda_returns, "rlk_lambda_returns", dev, n_env, n_t,
-            _ptr(rewards, "rewards", shape, dev), _ptr(next_values, "next_values", shape, dev),
-            _ptr(terminateds, "terminateds", shape, dev), _opt(truncateds, "truncateds", shape, dev),
-            bp, mode, _ptr(out, "out", shape, dev), n_env, n_t, gamma, lambda_)
+    bp, mode = _boot_args(bootstrap, n_env, n_t, dev, dt)
+    _launch(_entry(lib, "rlk_lambda_returns", dt), "rlk_lambda_returns", dev, n_env, n_t,
+            _ptr(rewards, "rewards", shape, dev, dt), _ptr(next_values, "next_values", shape, dev, dt),
+            _ptr(terminateds, "terminateds", shape, dev, dt), _opt(truncateds, "truncateds", shape, dev, dt),
+            bp, mode, _ptr(out, "out", shape, dev, dt), n_env, n_t, gamma, lambda_)
     return out
 
 
 def discounted_returns(rewards, terminateds, truncateds, bootstrap, out, gamma):
     dev = _device_of(rewards)
     shape = rewards.shape
+    dt = rewards.dtype
     n_env, n_t = shape
     lib = _lib or load()
-    bp, mode = _boot_args(bootstrap, n_env, n_t, dev)
-    _launch(lib.rlk_discounted_returns, "rlk_discounted_returns", dev, n_env, n_t,
-            _ptr(rewards, "rewards", shape, dev), _ptr(terminateds, "terminateds", shape, dev),
-            _opt(truncateds, "truncateds", shape, dev), bp, mode,
-            _ptr(out, "out", shape, dev), n_env, n_t, gamma)
+    bp, mode = _boot_args(bootstrap, n_env, n_t, dev, dt)
+    _launch(_entry(lib, "rlk_discounted_returns", dt), "rlk_discounted_returns", dev, n_env, n_t,
+            _ptr(rewards, "rewards", shape, dev, dt), _ptr(terminateds, "terminateds", shape, dev, dt),
+            _opt(truncateds, "truncateds", shape, dev, dt), bp, mode,
+            _ptr(out, "out", shape, dev, dt), n_env, n_t, gamma)
     return out
 
 
 def eligibility_traces(gradients, dones, seed, out, gamma, lambda_):
     dev = _device_of(gradients)
     shape = gradients.shape
+    dt = gradients.dtype
     n_env, n_t = shape
     lib = _lib or load()
-    _launch(lib.rlk_eligibility_traces, "rlk_eligibility_traces", dev, n_env, n_t,
-            _ptr(gradients, "gradients", shape, dev), _ptr(dones, "dones", shape, dev),
-            _opt(seed, "seed_values", torch.Size((n_env,)), dev), _ptr(out, "out", shape, dev),
+    _launch(_entry(lib, "rlk_eligibility_traces", dt), "rlk_eligibility_traces", dev, n_env, n_t,
+            _ptr(gradients, "gradients", shape, dev, dt), _ptr(dones, "dones", shape, dev, dt),
+            _opt(seed, "seed_values", torch.Size((n_env,)), dev, dt), _ptr(out, "out", shape, dev, dt),
             n_env, n_t, gamma, lambda_)
     return out
 
@@ -334,11 +358,12 @@ def eligibility_traces(gradients, dones, seed, out, gamma, lambda_):
 def prefix_sum(inputs, dones, seed, out, ends_at):
     dev = _device_of(inputs)
     shape = inputs.shape
+    dt = inputs.dtype
     n_env, n_t = shape
     lib = _lib or load()
-    _launch(lib.rlk_prefix_sum, "rlk_prefix_sum", dev, n_env, n_t,
-            _ptr(inputs, "inputs", shape, dev), _ptr(dones, "dones", shape, dev),
-            _opt(seed, "seed_values", torch.Size((n_env,)), dev), _ptr(out, "out", shape, dev),
+    _launch(_entry(lib, "rlk_prefix_sum", dt), "rlk_prefix_sum", dev, n_env, n_t,
+            _ptr(inputs, "inputs", shape, dev, dt), _ptr(dones, "dones", shape, dev, dt),
+            _opt(seed, "seed_values", torch.Size((n_env,)), dev, dt), _ptr(out, "out", shape, dev, dt),
             n_env, n_t, int(bool(ends_at)))
     return out
 
@@ -346,10 +371,11 @@ def prefix_sum(inputs, dones, seed, out, ends_at):
 def affine_scan(u, v, carry, out, direction):
     dev = _device_of(u)
     shape = u.shape
+    dt = u.dtype
     n_env, n_t = shape
     lib = _lib or load()
-    _launch(lib.rlk_affine_scan, "rlk_affine_scan", dev, n_env, n_t,
-            _ptr(u, "u", shape, dev), _ptr(v, "v", shape, dev),
-            _opt(carry, "bootstrap" if direction == BACKWARD else "seed", torch.Size((n_env,)), dev),
-            _ptr(out, "out", shape, dev), n_env, n_t, direction)
+    _launch(_entry(lib, "rlk_affine_scan", dt), "rlk_affine_scan", dev, n_env, n_t,
+            _ptr(u, "u", shape, dev, dt), _ptr(v, "v", shape, dev, dt),
+            _opt(carry, "bootstrap" if direction == BACKWARD else "seed", torch.Size((n_env,)), dev, dt),
+            _ptr(out, "out", shape, dev, dt), n_env, n_t, direction)
     return out

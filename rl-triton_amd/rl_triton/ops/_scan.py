@@ -30,6 +30,14 @@ def _CORRECTNESS_WARNINGS() -> bool:
     return os.environ.get("RL_TRITON_CORRECTNESS_WARNINGS", "0") == "1"
 
 
+def _float_io(t, lead) -> bool:
+    """The dtype rule of every op: float32 as in the reference, or else bfloat16 for every
+    float tensor of the call (the dtype of `lead`, the call's first [num_envs, seq_len]
+    tensor).  bfloat16 calls compute in float32 and return bfloat16, rounded as torch's
+    float -> bfloat16 conversion rounds."""
+    return t.dtype == lead.dtype and lead.dtype in (torch.float32, torch.bfloat16)
+
+
 def _perf_warn(msg: str) -> None:
     if _PERF_WARNINGS:
         warnings.warn(msg, stacklevel=3)
@@ -81,8 +89,8 @@ def _run_scan(
     if _CORRECTNESS_WARNINGS():
         assert u.shape == v.shape,      "u and v must have the same shape"
         assert u.is_cuda and v.is_cuda, "u and v must be on CUDA"
-        assert u.dtype == torch.float32, f"u: expected float32, got {u.dtype}"
-        assert v.dtype == torch.float32, f"v: expected float32, got {v.dtype}"
+        assert _float_io(u, u), f"u: expected float32 (or bfloat16 throughout), got {u.dtype}"
+        assert _float_io(v, u), f"v: expected float32 (or bfloat16 throughout), got {v.dtype}"
         if bootstrap is not None:
             assert bootstrap.shape == (u.shape[0],), \
                 f"bootstrap must have shape [{u.shape[0]}], got {bootstrap.shape}"
@@ -130,8 +138,8 @@ def _run_scan_forward(
     if _CORRECTNESS_WARNINGS():
         assert u.shape == v.shape,      "u and v must have the same shape"
         assert u.is_cuda and v.is_cuda, "u and v must be on CUDA"
-        assert u.dtype == torch.float32, f"u: expected float32, got {u.dtype}"
-        assert v.dtype == torch.float32, f"v: expected float32, got {v.dtype}"
+        assert _float_io(u, u), f"u: expected float32 (or bfloat16 throughout), got {u.dtype}"
+        assert _float_io(v, u), f"v: expected float32 (or bfloat16 throughout), got {v.dtype}"
         if seed is not None:
             assert seed.shape == (u.shape[0],), \
                 f"seed must have shape [{u.shape[0]}], got {seed.shape}"

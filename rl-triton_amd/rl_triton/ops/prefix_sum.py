@@ -1,7 +1,7 @@
 import torch
 
 from rl_triton import _native
-from rl_triton.ops._scan import _FLAT_MAX_SEQ_LEN, _CORRECTNESS_WARNINGS  # noqa: F401
+from rl_triton.ops._scan import _FLAT_MAX_SEQ_LEN, _CORRECTNESS_WARNINGS, _float_io  # noqa: F401
 
 
 def compute_episodic_prefix_sum(
@@ -39,8 +39,8 @@ def compute_episodic_prefix_sum(
 
     if _CORRECTNESS_WARNINGS():
         assert inputs.is_cuda and dones.is_cuda, "inputs and dones must be on CUDA"
-        assert inputs.dtype == torch.float32, f"inputs: expected float32, got {inputs.dtype}"
-        assert dones.dtype == torch.float32,  f"dones: expected float32, got {dones.dtype}"
+        assert _float_io(inputs, inputs), f"inputs: expected float32 (or bfloat16 throughout), got {inputs.dtype}"
+        assert _float_io(dones, inputs),  f"dones: expected float32 (or bfloat16 throughout), got {dones.dtype}"
         assert inputs.shape == dones.shape,   "inputs and dones must have the same shape"
         if seed_values is not None:
             assert seed_values.shape == (num_envs,), \

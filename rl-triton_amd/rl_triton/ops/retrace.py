@@ -1,7 +1,7 @@
 import torch
 
 from rl_triton import _native
-from rl_triton.ops._scan import _CORRECTNESS_WARNINGS
+from rl_triton.ops._scan import _CORRECTNESS_WARNINGS, _float_io
 from rl_triton.ops.retrace_fused import _retrace_launch, compute_retrace_fused
 
 # The reference routes seq_len > 2048 away from its fused Triton kernel because of
@@ -59,16 +59,16 @@ def compute_retrace(
         ("truncateds",            truncateds),
     ]:
         assert t.is_cuda,                 f"{name} must be on CUDA"
-        assert t.dtype == torch.float32,  f"{name}: expected float32, got {t.dtype}"
+        assert _float_io(t, rewards),  f"{name}: expected float32 (or bfloat16 throughout), got {t.dtype}"
         assert t.shape == rewards.shape,  f"{name} shape {t.shape} != rewards shape {rewards.shape}"
 
     assert action_probs_target.is_cuda,                "action_probs_target must be on CUDA"
-    assert action_probs_target.dtype == torch.float32, "action_probs_target: expected float32"
+    assert _float_io(action_probs_target, rewards), "action_probs_target: expected float32 (or bfloat16 throughout)"
     assert action_probs_target.shape[:2] == rewards.shape, (
         f"action_probs_target shape {action_probs_target.shape} incompatible with rewards {rewards.shape}"
     )
     assert next_q_values_all.is_cuda,                "next_q_values_all must be on CUDA"
-    assert next_q_values_all.dtype == torch.float32, "next_q_values_all: expected float32"
+    assert _float_io(next_q_values_all, rewards), "next_q_values_all: expected float32 (or bfloat16 throughout)"
     assert next_q_values_all.shape == action_probs_target.shape, (
         f"next_q_values_all {next_q_values_all.shape} != action_probs_target {action_probs_target.shape}"
     )

@@ -1,7 +1,7 @@
 import torch
 
 from rl_triton import _native
-from rl_triton.ops._scan import _FLAT_MAX_SEQ_LEN, _CORRECTNESS_WARNINGS  # noqa: F401
+from rl_triton.ops._scan import _FLAT_MAX_SEQ_LEN, _CORRECTNESS_WARNINGS, _float_io  # noqa: F401
 
 
 def compute_lambda_returns(
@@ -41,16 +41,16 @@ def compute_lambda_returns(
     # Cheap structural checks -- always-on (ops/returns.py:81-95).
     for name, t in [("rewards", rewards), ("next_values", next_values), ("terminateds", terminateds)]:
         assert t.is_cuda,                f"{name} must be on CUDA"
-        assert t.dtype == torch.float32, f"{name}: expected float32, got {t.dtype}"
+        assert _float_io(t, rewards), f"{name}: expected float32 (or bfloat16 throughout), got {t.dtype}"
         assert t.shape == rewards.shape, f"{name} shape {t.shape} != rewards shape {rewards.shape}"
     if has_truncations:
         assert truncateds.is_cuda,                "truncateds must be on CUDA"
-        assert truncateds.dtype == torch.float32, "truncateds: expected float32"
+        assert _float_io(truncateds, rewards), "truncateds: expected float32 (or bfloat16 throughout)"
         assert truncateds.shape == rewards.shape, \
             f"truncateds shape {truncateds.shape} != rewards shape {rewards.shape}"
     if bootstrap_values is not None:
         assert bootstrap_values.is_cuda,                "bootstrap_values must be on CUDA"
-        assert bootstrap_values.dtype == torch.float32, "bootstrap_values: expected float32"
+        assert _float_io(bootstrap_values, rewards), "bootstrap_values: expected float32 (or bfloat16 throughout)"
         assert bootstrap_values.shape == rewards.shape, \
             f"bootstrap_values shape {bootstrap_values.shape} != rewards shape {rewards.shape}"
 
@@ -105,16 +105,16 @@ def compute_discounted_returns(
     # Cheap structural checks -- always-on (ops/returns.py:194-208).
     for name, t in [("rewards", rewards), ("terminateds", terminateds)]:
         assert t.is_cuda,                f"{name} must be on CUDA"
-        assert t.dtype == torch.float32, f"{name}: expected float32, got {t.dtype}"
+        assert _float_io(t, rewards), f"{name}: expected float32 (or bfloat16 throughout), got {t.dtype}"
         assert t.shape == rewards.shape, f"{name} shape {t.shape} != rewards shape {rewards.shape}"
     if has_truncations:
         assert truncateds.is_cuda,                "truncateds must be on CUDA"
-        assert truncateds.dtype == torch.float32, "truncateds: expected float32"
+        assert _float_io(truncateds, rewards), "truncateds: expected float32 (or bfloat16 throughout)"
         assert truncateds.shape == rewards.shape, \
             f"truncateds shape {truncateds.shape} != rewards shape {rewards.shape}"
     if bootstrap_values is not None:
         assert bootstrap_values.is_cuda,                "bootstrap_values must be on CUDA"
-        assert bootstrap_values.dtype == torch.float32, "bootstrap_values: expected float32"
+        assert _float_io(bootstrap_values, rewards), "bootstrap_values: expected float32 (or bfloat16 throughout)"
         assert bootstrap_values.shape == rewards.shape, \
             f"bootstrap_values shape {bootstrap_values.shape} != rewards shape {rewards.shape}"
 
@@ -168,8 +168,8 @@ def compute_eligibility_traces(
 
     # Cheap structural checks -- always-on (ops/returns.py:309-317).
     assert gradients.is_cuda and dones.is_cuda, "gradients and dones must be on CUDA"
-    assert gradients.dtype == torch.float32, f"gradients: expected float32, got {gradients.dtype}"
-    assert dones.dtype == torch.float32,     f"dones: expected float32, got {dones.dtype}"
+    assert _float_io(gradients, gradients), f"gradients: expected float32 (or bfloat16 throughout), got {gradients.dtype}"
+    assert _float_io(dones, gradients),     f"dones: expected float32 (or bfloat16 throughout), got {dones.dtype}"
     assert gradients.shape == dones.shape,   "gradients and dones must have the same shape"
     if seed_values is not None:
         assert seed_values.shape == (num_envs,), \

@@ -1,7 +1,7 @@
 import torch
 
 from rl_triton import _native
-from rl_triton.ops._scan import _FLAT_MAX_SEQ_LEN, _CORRECTNESS_WARNINGS
+from rl_triton.ops._scan import _FLAT_MAX_SEQ_LEN, _CORRECTNESS_WARNINGS, _float_io
 
 
 def compute_vtrace_fused(
@@ -58,11 +58,11 @@ def compute_vtrace_fused(
         ("terminateds",     terminateds),
     ]:
         assert t.is_cuda,                f"{name} must be on CUDA"
-        assert t.dtype == torch.float32, f"{name}: expected float32, got {t.dtype}"
+        assert _float_io(t, rewards), f"{name}: expected float32 (or bfloat16 throughout), got {t.dtype}"
         assert t.shape == rewards.shape, f"{name} shape {t.shape} != rewards shape {rewards.shape}"
     if has_truncations:
         assert truncateds.is_cuda,                "truncateds must be on CUDA"
-        assert truncateds.dtype == torch.float32, "truncateds: expected float32"
+        assert _float_io(truncateds, rewards), "truncateds: expected float32 (or bfloat16 throughout)"
         assert truncateds.shape == rewards.shape, \
             f"truncateds shape {truncateds.shape} != rewards shape {rewards.shape}"
     if last_value is not None:
@@ -73,10 +73,10 @@ def compute_vtrace_fused(
         assert last_value.shape == (num_envs,), \
             f"last_value must have shape [{num_envs}], got {last_value.shape}"
         assert last_value.is_cuda,                "last_value must be on CUDA"
-        assert last_value.dtype == torch.float32, "last_value: expected float32"
+        assert _float_io(last_value, rewards), "last_value: expected float32 (or bfloat16 throughout)"
     if bootstrap_values is not None:
         assert bootstrap_values.is_cuda,                "bootstrap_values must be on CUDA"
-        assert bootstrap_values.dtype == torch.float32, "bootstrap_values: expected float32"
+        assert _float_io(bootstrap_values, rewards), "bootstrap_values: expected float32 (or bfloat16 throughout)"
         assert bootstrap_values.shape == rewards.shape, \
             f"bootstrap_values shape {bootstrap_values.shape} != rewards shape {rewards.shape}"
 

@@ -83,7 +83,8 @@ def run_oracle(op, inp, params):
     raise KeyError(op)
 
 
-def to_device(inp, device):
+def to_device(inp, device, dtype=torch.float32):
+    """Float inputs as `dtype` (float32 or bfloat16, rounded to nearest even), int64 actions."""
     out = {}
     for k, v in inp.items():
         if v is None:
@@ -91,14 +92,14 @@ def to_device(inp, device):
         elif k == "actions":
             out[k] = torch.as_tensor(np.asarray(v, dtype=np.int64)).to(device)
         else:
-            out[k] = torch.as_tensor(np.asarray(v, dtype=np.float32)).to(device)
+            out[k] = torch.as_tensor(np.asarray(v, dtype=np.float32)).to(dtype).to(device)
     return out
 
 
-def run_api(op, inp, params, device):
+def run_api(op, inp, params, device, dtype=torch.float32):
     import rl_triton
     from rl_triton.ops._scan import _run_scan, _run_scan_forward
-    d = to_device(inp, device)
+    d = to_device(inp, device, dtype)
     g = lambda k: d.get(k)  # noqa: E731
     if op == "gae":
         return (rl_triton.compute_gae(g("rewards"), g("values"), g("terminateds"), g("truncateds"),

@@ -101,6 +101,20 @@ def make(name: str, seed: int = 0, device="cpu"):
     raise KeyError(name)
 
 
+def as_dtype(inp: dict, dtype) -> dict:
+    """The float inputs of a configuration as `dtype` (int64 actions unchanged)."""
+    return {k: (v.to(dtype) if v is not None and v.is_floating_point() else v)
+            for k, v in inp.items()}
+
+
+def bytes_per_elem(name: str, dtype=torch.float32) -> int:
+    """Algorithmic bytes per element with float arrays of `dtype` (Retrace's int64 actions
+    are 8 bytes either way)."""
+    bpe = CONFIGS[name][3]
+    ints = 8 if CONFIGS[name][0] == "retrace" else 0
+    return ints + (bpe - ints) * torch.finfo(dtype).bits // 32
+
+
 def call(name: str, inp: dict, params: dict):
     """One public-API call of configuration `name` on device tensors; returns a tuple."""
     import rl_triton

@@ -1,0 +1,152 @@
+"""bfloat16 I/O (the reference's ROADMAP.md:82-99 item; the reference itself accepts float32
+only, so there is no reference output to match).
+
+What pins it:
+  * bit identity: every op on bfloat16 tensors returns exactly the float32 op's result on
+    the same (widened) inputs, rounded by torch's float -> bfloat16 conversion.  The float32
+    path is pinned against the oracle by test_gpu_parity.py, so this carries that parity
+    over.  Both launch paths (the C++ fast path and the Python path), short rows, padding
+    waves, scalar (seq_len % 4 != 0) and vector loads, and the look-back path are covered.
+  * precision drift: against the float64 oracle on the unrounded float32 inputs, the
+    bfloat16-I/O error stays within the bound of input and output rounding propagated
+    through the recurrence, 2^-8 * (max|expected| + L_eff * max|input|), with L_eff the
+    effective horizon (1/(1 - decay); the longest done-free run for the prefix sum).
+  * compute_gae_normalized: returns bit-identical as above; normalised advantages within
+    one bfloat16 rounding of normalising the rounded advantages (the second launch reads
+    the stored bfloat16 advantages, so those values are rounded twice).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from _common import OUTPUTS, make_inputs, run_api, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+OPS = ["gae", "vtrace", "retrace", "lambda_returns", "discounted_returns", "eligibility_traces",
+       "prefix_sum", "backward_scan", "forward_scan"]
+SHAPES = [(1, 1), (1, 7), (33, 257), (4096, 128), (16, 2048), (3, 1100), (2, 5001), (3, 5000),
+          (2, 40000)]
+
+
+def _inputs(op, shape, seed):
+    boot = ("full" if op in ("gae", "vtrace", "lambda_returns", "discounted_returns") else "row")
+    kw = {"p_done": 1e-3} if op in ("prefix_sum", "eligibility_traces") else {}
+    return make_inputs(op, *shape, seed=seed, p_trunc=0.02 if op != "retrace" else 0.0,
+                       boot=boot, **kw)
+
+
+def _bf16_values(inp):
+    """The inputs rounded to bfloat16 and widened back (exact), as float32 arrays."""
+    out = {}
+    for k, v in inp.items():
+        if v is None or k == "actions":
+            out[k] = v
+        else:
+            out[k] = torch.as_tensor(v).to(BF16).float().numpy()
+    return out
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16)
+
+
+@pytest.mark.parametrize("path", ["python", "fast"])
+@pytest.mark.parametrize("op", OPS)
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+def test_bf16_is_float32_result_rounded(op, shape, path, device, monkeypatch):
+    if path == "fast":
+        if shape[1] > 2048:
+            pytest.skip("the fast path declines rows that need the look-back workspace")
+        monkeypatch.delenv("RL_TRITON_CORRECTNESS_WARNINGS")
+    inp, params = _inputs(op, shape, seed=31)
+    inp = _bf16_values(inp)
+    got = run_api(op, inp, params, device, dtype=BF16)
+    ref = run_api(op, inp, params, device, dtype=torch.float32)
+    for name, g, r in zip(OUTPUTS[op], got, ref):
+        assert g.dtype == BF16, f"{op}:{name} returned {g.dtype}"
+        want = r.to(BF16)
+        same = _bits(g) == _bits(want)
+        if not bool(same.all()):
+            i = int((~same).flatten().nonzero()[0])
+            raise AssertionError(f"{op}{shape}:{name}: {int((~same).sum())} elements differ; "
+                                 f"first at flat index {i}: got {g.flatten()[i].item()!r}, "
+                                 f"float32 result {r.flatten()[i].item()!r}")
+
+
+def _longest_run(d):
+    best = 0
+    for row in np.asarray(d) > 0:
+        idx = np.flatnonzero(np.concatenate(([True], row, [True])))
+        best = max(best, int(np.max(np.diff(idx))))
+    return best
+
+
+def drift_bound(op, inp, exp):
+    """2^-8 * (max|expected| + L_eff * max|input|): each input's bfloat16 rounding (relative
+    2^-9) reaches an output through weights whose sum is at most L_eff, and the output's own
+    rounding adds 2^-9 relative."""
+    if op == "prefix_sum":
+        l_eff = _longest_run(inp["dones"])
+    elif op == "discounted_returns":
+        l_eff = 1.0 / (1.0 - 0.99)
+    elif op in ("backward_scan", "forward_scan"):
+        l_eff = 1.0 / (1.0 - 0.99)
+    else:
+        l_eff = 1.0 / (1.0 - 0.99 * 0.95)
+    vin = max(float(np.max(np.abs(v))) for k, v in inp.items()
+              if v is not None and k != "actions" and np.size(v))
+    return 2.0 ** -8 * (float(np.max(np.abs(exp))) + l_eff * vin)
+
+
+@pytest.mark.parametrize("op", OPS)
+@pytest.mark.parametrize("shape", [(64, 128), (16, 2048), (2, 131072)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_bf16_drift_against_float64(op, shape, device):
+    inp, params = _inputs(op, shape, seed=7)
+    got = run_api(op, inp, params, device, dtype=BF16)
+    exp = run_oracle(op, inp, params)
+    for name, g, e in zip(OUTPUTS[op], got, exp):
+        err = float(np.max(np.abs(g.float().cpu().numpy().astype(np.float64) - e)))
+        bound = drift_bound(op, inp, e)
+        assert err <= bound, f"{op}{shape}:{name}: max abs err {err:.3e} > bound {bound:.3e}"
+
+
+@pytest.mark.parametrize("shape", [(2, 3), (33, 257), (4096, 128), (3, 5000)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_bf16_gae_normalized(shape, device):
+    inp, params = make_inputs("gae_normalized", *shape, seed=9, p_trunc=0.02, boot="full")
+    inp = _bf16_values(inp)
+    params = dict(params, eps=1e-8)
+    adv, ret = run_api("gae_normalized", inp, params, device, dtype=BF16)
+    a32, r32 = run_api("gae_normalized", inp, params, device, dtype=torch.float32)
+    raw = run_api("gae", inp, {k: v for k, v in params.items() if k != "eps"}, device)[0]
+    assert adv.dtype == BF16 and ret.dtype == BF16
+    assert torch.equal(_bits(ret), _bits(r32.to(BF16)))
+    # normalise the rounded advantages with the float32 path's statistics
+    a = raw.double()
+    mean, std = float(a.mean()), float(a.std())
+    want = ((raw.to(BF16).double() - mean) / (std + 1e-8))
+    err = (adv.double() - want).abs()
+    assert bool((err <= want.abs() * 2.0 ** -8 + 1e-6).all()), f"max err {float(err.max()):.3e}"
+    # and the float32 path's normalised advantages to within bfloat16 precision
+    torch.testing.assert_close(adv.float(), a32, rtol=2.0 ** -7, atol=2.0 ** -7 * max(1.0, math.sqrt(2)))
+
+
+def test_bf16_mixed_dtypes_are_rejected(device, monkeypatch):
+    """All float tensors of a call share one dtype; a mix raises before any launch, on both
+    launch paths (the fast path declines and the Python path raises)."""
+    import rl_triton
+    x = torch.zeros(4, 8, device=device)
+    b = x.to(BF16)
+    for flag in ("1", None):
+        if flag is None:
+            monkeypatch.delenv("RL_TRITON_CORRECTNESS_WARNINGS")
+        with pytest.raises(AssertionError, match="expected float32"):
+            rl_triton.compute_gae(b, x, x)
+        with pytest.raises(AssertionError, match="expected float32"):
+            rl_triton.compute_discounted_returns(x, b)
+        with pytest.raises(AssertionError, match="expected float32"):
+            rl_triton.compute_gae(x.double(), x.double(), x.double())
