@@ -185,15 +185,40 @@ def time_configs(torch, names, min_launches=200, batch=50, dtype=None):
     return res
 
 
+def _device_us(torch, fn, sets, min_launches=200, batch=50):
+    """Average device time of fn(*set) from HIP events around batches of back-to-back calls
+    queued behind a GPU spin, rotating over `sets`."""
+    stream = torch.cuda.current_stream()
+    for i in range(min(len(sets), 8)):
+        fn(*sets[i])
+    torch.cuda.synchronize()
+    total_ms, n = 0.0, 0
+    while n < min_launches:
+        torch.cuda._sleep(20_000_000)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for i in range(batch):
+            fn(*sets[(n + i) % len(sets)])
+        b.record(stream)
+        torch.cuda.synchronize()
+        total_ms += a.elapsed_time(b)
+        n += batch
+    return 1e3 * total_ms / n
+
+
 def time_extensions(torch, min_launches=200, batch=50):
-    """compute_gae_normalized (GAE + returns + batch-normalised advantages, the reference's
-    ROADMAP.md:75-81 item) at the C2 shape, against the composition it replaces:
-    compute_gae, then returns = A + values, then (A - A.mean()) / (A.std() + 1e-8) in torch.
-    Device time per call from HIP events around batches queued behind a GPU spin."""
+    """The paths beyond the reference's API (its ROADMAP.md items), on rotating HBM-resident
+    sets of more than 3 x 256 MB:
+      * compute_gae_normalized (GAE + returns + batch-normalised advantages) at the C2 shape,
+        against the composition it replaces: compute_gae, then returns = A + values, then
+        (A - A.mean()) / (A.std() + 1e-8) in torch;
+      * compute_gae(..., mask=...) (skipped steps) at the C2 shape and distribution with a
+        multi-turn mask (alternating kept/skipped spans, mean length 12), and at
+        [16, 131072] (C5 shape, done ~ Bern(1e-4), last_value)."""
     import baseline_configs as bc
     import rl_triton
     dev = torch.device("cuda:0")
-    stream = torch.cuda.current_stream()
+    out = {}
     name = "C2_gae_4096x128"
     _, n_env, n_t, _ = bc.CONFIGS[name]
     n_sets = min(64, -(-3 * MALL_BYTES // (n_env * n_t * 4 * 7)) + 1)
@@ -210,34 +235,62 @@ def time_extensions(torch, min_launches=200, batch=50):
         ret = a + inp["values"]
         return (a - a.mean()) / (a.std() + 1e-8), ret
 
-    res = {}
-    for label, fn in (("fused", fused), ("torch_composition", composed)):
-        for i in range(min(n_sets, 8)):
-            fn(*sets[i])
-        torch.cuda.synchronize()
-        total_ms, n = 0.0, 0
-        while n < min_launches:
-            torch.cuda._sleep(20_000_000)
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            for i in range(batch):
-                fn(*sets[(n + i) % n_sets])
-            b.record(stream)
-            torch.cuda.synchronize()
-            total_ms += a.elapsed_time(b)
-            n += batch
-        res[label] = round(1e3 * total_ms / n, 3)
-    del sets
-    torch.cuda.empty_cache()
+    us_f = _device_us(torch, fused, sets, min_launches, batch)
+    us_c = _device_us(torch, composed, sets, min_launches, batch)
     elems = n_env * n_t
-    out = {"shape": [n_env, n_t], "device_us": res["fused"],
-           "torch_composition_us": res["torch_composition"],
-           "speedup": round(res["torch_composition"] / res["fused"], 2),
-           "bytes_per_elem": 28,  # 5 inputs read, advantages and returns written, once each
-           "gb_s": round(elems * 28 / (res["fused"] * 1e-6) / 1e9, 1)}
-    log(f"[bench] gae_normalized [{n_env},{n_t}]: {res['fused']:.2f} us/call fused vs "
-        f"{res['torch_composition']:.2f} us composed in torch")
-    return {"gae_normalized_4096x128": out}
+    out["gae_normalized_4096x128"] = {
+        "shape": [n_env, n_t], "device_us": round(us_f, 3), "torch_composition_us": round(us_c, 3),
+        "speedup": round(us_c / us_f, 2),
+        "bytes_per_elem": 28,  # 5 inputs read, advantages and returns written, once each
+        "gb_s": round(elems * 28 / (us_f * 1e-6) / 1e9, 1)}
+    log(f"[bench] gae_normalized [{n_env},{n_t}]: {us_f:.2f} us/call fused vs "
+        f"{us_c:.2f} us composed in torch")
+
+    # masked GAE: the C2 sets with a multi-turn mask; then few long rows
+    from baseline_configs import span_mask
+    g = torch.Generator().manual_seed(300)
+    masks = [span_mask(n_env, n_t, g).to(dev) for _ in range(4)]
+    msets = [(dict(inp, mask=masks[i % len(masks)]), params) for i, (inp, params) in enumerate(sets)]
+
+    def masked(inp, params):
+        return rl_triton.compute_gae(inp["rewards"], inp["values"], inp["terminateds"],
+                                     inp["truncateds"], bootstrap_values=inp["bootstrap_values"],
+                                     mask=inp["mask"], **params)
+
+    us_m = _device_us(torch, masked, msets, min_launches, batch)
+    us_p = _device_us(torch, lambda inp, params: bc.call(name, inp, params), sets, min_launches, batch)
+    out["gae_masked_4096x128"] = {
+        "shape": [n_env, n_t], "device_us": round(us_m, 3), "unmasked_device_us": round(us_p, 3),
+        "bytes_per_elem": 28,  # the C2 inputs and the mask read, advantages written
+        "gb_s": round(elems * 28 / (us_m * 1e-6) / 1e9, 1),
+        "pct_peak": round(100 * elems * 28 / (us_m * 1e-6) / 1e9 / PEAK_GBS, 2)}
+    log(f"[bench] gae_masked [{n_env},{n_t}]: {us_m:.2f} us/call (unmasked {us_p:.2f} us), "
+        f"{elems * 28 / (us_m * 1e-6) / 1e9:.0f} GB/s")
+    del sets, msets, masks
+
+    E, T = 16, 131072
+    lsets = []
+    for i in range(8):  # 8 x 42 MB (+ outputs) > 3 x 256 MB with the outputs
+        gi = torch.Generator(device=dev).manual_seed(400 + i)
+        lsets.append(({"rewards": torch.randn(E, T, generator=gi, device=dev),
+                       "values": torch.randn(E, T, generator=gi, device=dev),
+                       "terminateds": (torch.rand(E, T, generator=gi, device=dev) < 1e-4).float(),
+                       "last_value": torch.randn(E, generator=gi, device=dev),
+                       "mask": span_mask(E, T, g).to(dev)}, {"gamma": 0.99, "lambda_": 0.95}))
+
+    def masked_long(inp, params):
+        return rl_triton.compute_gae(inp["rewards"], inp["values"], inp["terminateds"],
+                                     last_value=inp["last_value"], mask=inp["mask"], **params)
+
+    us_l = _device_us(torch, masked_long, lsets, min_launches, batch)
+    gbs = E * T * 20 / (us_l * 1e-6) / 1e9
+    out["gae_masked_16x131072"] = {"shape": [E, T], "device_us": round(us_l, 3),
+                                   "bytes_per_elem": 20, "gb_s": round(gbs, 1),
+                                   "pct_peak": round(100 * gbs / PEAK_GBS, 2)}
+    log(f"[bench] gae_masked [{E},{T}]: {us_l:.2f} us/call, {gbs:.0f} GB/s")
+    del lsets
+    torch.cuda.empty_cache()
+    return out
 
 
 def time_graph_steps(torch, rl, sets, steps):

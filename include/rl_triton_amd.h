@@ -26,8 +26,8 @@
  *     stream (concurrent use races).  Calls that need no workspace ignore the argument
  *     (NULL is fine).  Layout (uint64 words): [0..7] header, word [3] the error flag --
  *     nonzero if a look-back wait gave up or the counters were not at rest (results of
- *     that call are invalid); [8..2055] 64 ticket-counter slots; then two status words
- *     per tile.
+ *     that call are invalid); [8..2055] 64 ticket-counter slots; then up to five status
+ *     words per tile.
  *   - Return value: RLK_OK or a negative RLK_ERR_* code; rlk_status_string() names it.
  *     Empty inputs (num_envs == 0 or seq_len == 0) return RLK_OK without a launch.
  *   - bfloat16 I/O: every estimator has an `_bf16` twin whose float arrays (inputs,
@@ -80,6 +80,19 @@ int rlk_gae(const float *rewards, const float *values, const float *terminateds,
             const float *truncateds, const float *bootstrap, int boot_mode, float *advantages,
             int64_t num_envs, int64_t seq_len, float gamma, float lambda_, void *workspace,
             size_t workspace_bytes, void *stream);
+
+/* GAE with skipped steps ("verl-style" masking, listed in the reference's
+ * ROADMAP.md:131-140; no counterpart in the reference).  mask [num_envs, seq_len]: a step
+ * with mask == 0 is skipped -- its advantage is the next kept step's (0 if none) and the
+ * next value passes across it, so a kept step's TD target uses the value of the nearest
+ * kept step after it (bootstrap(T-1) after the last one).  Kept steps follow rlk_gae's
+ * rules (terminations, truncations with bootstrap_values); with every step kept the result
+ * is rlk_gae's.  The other arguments are rlk_gae's. */
+int rlk_gae_masked(const float *rewards, const float *values, const float *terminateds,
+                   const float *truncateds, const float *bootstrap, int boot_mode,
+                   const float *mask, float *advantages, int64_t num_envs, int64_t seq_len,
+                   float gamma, float lambda_, void *workspace, size_t workspace_bytes,
+                   void *stream);
 
 /* GAE with returns and batch-normalised advantages (no counterpart in the reference: the
  * "fused GAE + advantage normalisation" item of its ROADMAP.md:75-81).  Writes
@@ -171,6 +184,12 @@ int rlk_gae_bf16(const rlk_bf16 *rewards, const rlk_bf16 *values, const rlk_bf16
                  const rlk_bf16 *truncateds, const rlk_bf16 *bootstrap, int boot_mode,
                  rlk_bf16 *advantages, int64_t num_envs, int64_t seq_len, float gamma,
                  float lambda_, void *workspace, size_t workspace_bytes, void *stream);
+
+int rlk_gae_masked_bf16(const rlk_bf16 *rewards, const rlk_bf16 *values,
+                        const rlk_bf16 *terminateds, const rlk_bf16 *truncateds,
+                        const rlk_bf16 *bootstrap, int boot_mode, const rlk_bf16 *mask,
+                        rlk_bf16 *advantages, int64_t num_envs, int64_t seq_len, float gamma,
+                        float lambda_, void *workspace, size_t workspace_bytes, void *stream);
 
 /* The bfloat16 results of rlk_gae_normalized.  The statistics are those of the float32
  * advantages; the second launch normalises the stored (bfloat16) advantages, so each

@@ -32,6 +32,7 @@ _SIGS = {
     "orc_backward_scan": [_I64, _I64, _P, _P, _P, _P],
     "orc_forward_scan": [_I64, _I64, _P, _P, _P, _P],
     "orc_gae": [_I64, _I64, _P, _P, _P, _P, _P, _INT, _D, _D, _P],
+    "orc_gae_masked": [_I64, _I64, _P, _P, _P, _P, _P, _INT, _P, _D, _D, _P],
     "orc_vtrace": [_I64, _I64, _P, _P, _P, _P, _P, _P, _P, _INT, _D, _D, _D, _P, _P],
     "orc_retrace": [_I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _D, _D, _D, _D, _P, _P],
     "orc_lambda_returns": [_I64, _I64, _P, _P, _P, _P, _P, _INT, _D, _D, _P],
@@ -113,6 +114,18 @@ def gae(rewards, values, terminateds, truncateds=None, gamma=0.99, lambda_=0.95,
     out = np.empty((E, T), np.float64)
     _load().orc_gae(E, T, _ptr(r), _ptr(v), _ptr(te), _ptr(tr), _ptr(b), mode,
                     gamma, lambda_, _ptr(out))
+    return out
+
+
+def gae_masked(rewards, values, terminateds, mask, truncateds=None, gamma=0.99, lambda_=0.95,
+               bootstrap=None):
+    """GAE in which steps with mask == 0 pass the advantage and the next value through."""
+    r, v, te, mk, tr = map(_f32, (rewards, values, terminateds, mask, truncateds))
+    E, T = r.shape
+    b, mode = _boot(bootstrap, E, T)
+    out = np.empty((E, T), np.float64)
+    _load().orc_gae_masked(E, T, _ptr(r), _ptr(v), _ptr(te), _ptr(tr), _ptr(b), mode, _ptr(mk),
+                           gamma, lambda_, _ptr(out))
     return out
 
 

@@ -101,6 +101,42 @@ int orc_gae(int64_t E, int64_t T, const float *r, const float *val,
     return 0;
 }
 
+/* GAE with skipped steps: the "verl-style" masking of the reference's ROADMAP.md:131-140,
+ * which the reference does not implement.  Restates verl's compute_gae_advantage_return
+ * (verl/trainer/ppo/core_algos.py, the multi-turn form, verl is not a dependency of the
+ * reference), whose loop keeps `nextvalues` and `lastgaelam` across steps with
+ * response_mask == 0:
+ *     delta       = r + gamma * nextvalues - values
+ *     lastgaelam' = delta + gamma * lam * lastgaelam
+ *     nextvalues  = mask ? values : nextvalues;   lastgaelam = mask ? lastgaelam' : lastgaelam
+ *     A[t]        = lastgaelam
+ * with this library's boundary rules at kept steps (the GAE above): nextvalues starts at
+ * boot(T-1); a truncated step takes boot(t) as its next value; (1 - term) masks the TD
+ * target and (1 - done) cuts lastgaelam.  A step is kept when mask != 0. */
+int orc_gae_masked(int64_t E, int64_t T, const float *r, const float *val,
+                   const float *term, const float *trunc, const float *boot, int boot_mode,
+                   const float *mask, double gamma, double lambda, double *out)
+{
+    for (int64_t n = 0; n < E; ++n) {
+        double nv = boot_at(boot, boot_mode, n, T - 1, T);
+        double a = 0.0;
+        for (int64_t t = T - 1; t >= 0; --t) {
+            int64_t i = n * T + t;
+            if (mask[i] != 0.0f) {
+                double tr = trunc ? (double)trunc[i] : 0.0;
+                double te = (double)term[i];
+                double v_next = (tr == 1.0) ? boot_at(boot, boot_mode, n, t, T) : nv;
+                double done = dmin(te + tr, 1.0);
+                double delta = (double)r[i] + gamma * (1.0 - te) * v_next - (double)val[i];
+                a = delta + gamma * lambda * (1.0 - done) * a;
+                nv = (double)val[i];
+            }
+            out[i] = a;
+        }
+    }
+    return 0;
+}
+
 /* V-trace.  Follows reference_vtrace, tests/test_vtrace.py:56-101 and
  * _ref_vtrace_sequential, tests/test_vtrace.py:424-480, with the fused
  * kernel's bootstrap rule (kernels/vtrace_fused.py:109-196):

@@ -55,7 +55,7 @@ int long_segments(int64_t E, int64_t T) {
 size_t workspace_bytes(int64_t E, int64_t T) {
   if (E <= 0 || T <= kShortMaxT) return 0;
   const int64_t tiles = E * ((T + kMinTile - 1) / kMinTile);
-  return (size_t)(kStatusOffset + 2 * tiles) * sizeof(uint64_t);
+  return (size_t)(kStatusOffset + kStatusWords * tiles) * sizeof(uint64_t);
 }
 
 bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -178,6 +178,29 @@ int gae_impl(const E* rewards, const E* values, const E* terminateds, const E* t
   }
   GaeOp<false, E> op{rewards, values, terminateds, nullptr, boot, advantages, boot_mode, gamma,
                      gamma * lambda_};
+  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+}
+
+template <class E>
+int gae_masked_impl(const E* rewards, const E* values, const E* terminateds, const E* truncateds,
+                    const E* bootstrap, int boot_mode, const E* mask, E* advantages,
+                    int64_t num_envs, int64_t seq_len, float gamma, float lambda_,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  if (is_empty(num_envs, seq_len)) return RLK_OK;
+  if (!rewards || !values || !terminateds || !mask || !advantages ||
+      !valid_boot(bootstrap, boot_mode))
+    return RLK_ERR_INVALID_ARGUMENT;
+  const E* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
+  const bool vec = seq_len % 4 == 0 &&
+                   quad_aligned(rewards, values, terminateds, truncateds, mask, advantages) &&
+                   (boot_mode != RLK_BOOT_FULL || quad_aligned(bootstrap));
+  if (truncateds) {
+    MaskedGaeOp<true, E> op{rewards, values, terminateds, truncateds, boot, mask, advantages,
+                            boot_mode, gamma, gamma * lambda_};
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  }
+  MaskedGaeOp<false, E> op{rewards, values, terminateds, nullptr, boot, mask, advantages,
+                           boot_mode, gamma, gamma * lambda_};
   return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
 }
 
@@ -415,6 +438,26 @@ int rlk_gae_bf16(const rlk_bf16* rewards, const rlk_bf16* values, const rlk_bf16
   return gae_impl(B(rewards), B(values), B(terminateds), B(truncateds), B(bootstrap), boot_mode,
                   B(advantages), num_envs, seq_len, gamma, lambda_, workspace, workspace_bytes,
                   stream);
+}
+
+int rlk_gae_masked(const float* rewards, const float* values, const float* terminateds,
+                   const float* truncateds, const float* bootstrap, int boot_mode,
+                   const float* mask, float* advantages, int64_t num_envs, int64_t seq_len,
+                   float gamma, float lambda_, void* workspace, size_t workspace_bytes,
+                   void* stream) {
+  return gae_masked_impl(rewards, values, terminateds, truncateds, bootstrap, boot_mode, mask,
+                         advantages, num_envs, seq_len, gamma, lambda_, workspace,
+                         workspace_bytes, stream);
+}
+
+int rlk_gae_masked_bf16(const rlk_bf16* rewards, const rlk_bf16* values,
+                        const rlk_bf16* terminateds, const rlk_bf16* truncateds,
+                        const rlk_bf16* bootstrap, int boot_mode, const rlk_bf16* mask,
+                        rlk_bf16* advantages, int64_t num_envs, int64_t seq_len, float gamma,
+                        float lambda_, void* workspace, size_t workspace_bytes, void* stream) {
+  return gae_masked_impl(B(rewards), B(values), B(terminateds), B(truncateds), B(bootstrap),
+                         boot_mode, B(mask), B(advantages), num_envs, seq_len, gamma, lambda_,
+                         workspace, workspace_bytes, stream);
 }
 
 size_t rlk_gae_normalized_partials_bytes(int64_t num_envs, int64_t seq_len) {

@@ -39,15 +39,67 @@ namespace rlk {
 
 constexpr int kWave = 64;
 
+// ---------------------------------------------------------------------------------------
+// Scan elements ("maps").  An op's steps are maps of one of two kinds; a kind provides its
+// carried State, identity, apply, compose (outer o inner: inner first) and the number of
+// look-back status words its aggregate and its state take.
+//
+//   Affine      x' = mul*x + add                              (State: x)
+//   SkipAffine  nv' = a*nv + c,  x' = p*nv + q*x + d          (State: {nv, x})
+//
+// SkipAffine carries a second value beside x, a "next value" nv that skipped steps pass
+// through unchanged; the steps of the masked GAE mode are of this kind (a step either
+// replaces nv, a = 0, or keeps it, a = 1, so a stays exactly 0 or 1 under composition).
+// ---------------------------------------------------------------------------------------
 struct Affine {
+  using State = float;
+  static constexpr int kWords = 2;       // status words of an aggregate
+  static constexpr int kStateWords = 1;  // status words of an inclusive value
   float mul;
   float add;
+  __device__ static Affine identity() { return Affine{1.f, 0.f}; }
+  __device__ float apply(float x) const { return fmaf(mul, x, add); }
+  __device__ bool constant() const { return mul == 0.f; }  // apply() ignores its argument
+  __device__ float word(int i) const { return i == 0 ? mul : add; }
+  __device__ static Affine from_words(const float* w) { return Affine{w[0], w[1]}; }
 };
 
 __device__ __forceinline__ Affine compose(Affine outer, Affine inner) {
   // outer(inner(x))
   return Affine{outer.mul * inner.mul, fmaf(outer.mul, inner.add, outer.add)};
 }
+
+struct NvX {
+  float nv;  // the carried next value
+  float x;   // the scanned value
+};
+
+struct SkipAffine {
+  using State = NvX;
+  static constexpr int kWords = 5;
+  static constexpr int kStateWords = 2;
+  float a, c, p, q, d;
+  __device__ static SkipAffine identity() { return SkipAffine{1.f, 0.f, 0.f, 1.f, 0.f}; }
+  __device__ NvX apply(NvX s) const { return NvX{fmaf(a, s.nv, c), fmaf(p, s.nv, fmaf(q, s.x, d))}; }
+  __device__ bool constant() const { return a == 0.f && p == 0.f && q == 0.f; }
+  __device__ float word(int i) const { return i == 0 ? a : i == 1 ? c : i == 2 ? p : i == 3 ? q : d; }
+  __device__ static SkipAffine from_words(const float* w) { return SkipAffine{w[0], w[1], w[2], w[3], w[4]}; }
+};
+
+__device__ __forceinline__ SkipAffine compose(SkipAffine o, SkipAffine i) {
+  return SkipAffine{o.a * i.a, fmaf(o.a, i.c, o.c), fmaf(o.p, i.a, o.q * i.p), o.q * i.q,
+                    fmaf(o.p, i.c, fmaf(o.q, i.d, o.d))};
+}
+
+// States as status words (an inclusive value): x first, so word 0 names the kind.
+__device__ __forceinline__ float state_word(float x, int) { return x; }
+__device__ __forceinline__ float state_word(NvX s, int i) { return i == 0 ? s.x : s.nv; }
+template <class S>
+__device__ __forceinline__ S state_from_words(const float* w);
+template <>
+__device__ __forceinline__ float state_from_words<float>(const float* w) { return w[0]; }
+template <>
+__device__ __forceinline__ NvX state_from_words<NvX>(const float* w) { return NvX{w[1], w[0]}; }
 
 struct NoHalo {};
 
@@ -185,10 +237,15 @@ __device__ __forceinline__ void boot_prepare(int mode, int t0, int T, float (&bt
 
 // The row's carry x[T] (backward) / x[-1] (forward): op.row_carry_src() gives its address,
 // nullptr for 0.
+// Ops whose map is not Affine give their row's carried state by op.row_state(row, T).
 template <class Op>
-__device__ __forceinline__ float row_carry(const Op& op, int64_t row, int T) {
-  const auto* src = op.row_carry_src(row, T);
-  return src ? to_f32(*src) : 0.f;
+__device__ __forceinline__ typename Op::Map::State row_carry(const Op& op, int64_t row, int T) {
+  if constexpr (std::is_same<typename Op::Map, Affine>::value) {
+    const auto* src = op.row_carry_src(row, T);
+    return src ? to_f32(*src) : 0.f;
+  } else {
+    return op.row_state(row, T);
+  }
 }
 
 // A halo value of two floats (Retrace: c[t+1] and q[t+1]).
@@ -197,9 +254,11 @@ struct Halo2 {
 };
 
 // ---------------------------------------------------------------------------------------
-// Decoupled look-back status words.  Per tile two 64-bit words {tag:32 | value:32}:
-//   word0 = AGG: mul   or INC: x at the tile's outgoing edge
-//   word1 = AGG: add
+// Decoupled look-back status words.  Per tile kStatusWords 64-bit words {tag:32 | value:32}:
+//   AGG (the tile's map):           words 0..Map::kWords-1 = the map's coefficients
+//   INC (the state at the tile's outgoing edge): words 0..kStateWords-1 (x first)
+// Every word carries its own tag, so a reader accepts a map or a state only when all of
+// its words carry the same current tag.
 // tag = (epoch << 2) | kind, kind 1 = AGG, 2 = INC.  A word whose epoch differs from the
 // current call's is "not yet published", so the workspace needs clearing only once.
 //
@@ -210,7 +269,8 @@ struct Halo2 {
 //                                 not at rest); others reserved
 //   slots    [8 + 32*s], s < 64   ticket counter slot s (256 bytes each): +0 ticket,
 //                                 +16 drawn-workgroup counter (its own 128-byte line)
-//   status   [8 + 32*64 ...]      two words per tile, tiles of row r at r*tiles_per_row
+//   status   [8 + 32*64 ...]      kStatusWords words per tile, tiles of row r at
+//                                 r*tiles_per_row
 // Device-scope atomics on one address serialise (~12 ns each on MI355X), so tickets come
 // from up to 64 counters: row r draws from slot r % 64, and since a tile only ever waits
 // on tiles of its own row, handing out each slot's tiles in scan order is enough for
@@ -222,6 +282,7 @@ constexpr int kHeaderWords = 8;
 constexpr int kSlots = 64;
 constexpr int kSlotWords = 32;
 constexpr int kStatusOffset = kHeaderWords + kSlots * kSlotWords;
+constexpr int kStatusWords = 5;  // the largest map (SkipAffine); Affine tiles use 2 of them
 constexpr uint32_t kAgg = 1, kInc = 2;
 constexpr uint32_t kEpochMask = 0x3fffffffu;
 constexpr int kSpinLimit = 1 << 20;  // polls before a wait gives up (~1 s), never reached when correct
@@ -241,30 +302,30 @@ __device__ __forceinline__ uint64_t pack(uint32_t tag, float v) {
 // ---------------------------------------------------------------------------------------
 
 // The segment's map: steps composed in scan order.
-template <bool FWD, int S>
-__device__ __forceinline__ Affine fold_segment(const float (&mul)[S], const float (&add)[S]) {
-  Affine m{1.f, 0.f};
+template <bool FWD, int S, class M>
+__device__ __forceinline__ M fold_segment(const M (&steps)[S]) {
+  M m = M::identity();
   if constexpr (FWD) {
 #pragma unroll
-    for (int i = 0; i < S; ++i) m = compose(Affine{mul[i], add[i]}, m);
+    for (int i = 0; i < S; ++i) m = compose(steps[i], m);
   } else {
 #pragma unroll
-    for (int i = S - 1; i >= 0; --i) m = compose(Affine{mul[i], add[i]}, m);
+    for (int i = S - 1; i >= 0; --i) m = compose(steps[i], m);
   }
   return m;
 }
 
-// Every step's value from the value entering the segment.
-template <bool FWD, int S>
-__device__ __forceinline__ void replay(const float (&mul)[S], const float (&add)[S], float x_in,
-                                       float (&xs)[S]) {
-  float x = x_in;
+// Every step's state from the state entering the segment.
+template <bool FWD, int S, class M>
+__device__ __forceinline__ void replay(const M (&steps)[S], typename M::State x_in,
+                                       typename M::State (&xs)[S]) {
+  typename M::State x = x_in;
   if constexpr (FWD) {
 #pragma unroll
-    for (int i = 0; i < S; ++i) xs[i] = x = fmaf(mul[i], x, add[i]);
+    for (int i = 0; i < S; ++i) xs[i] = x = steps[i].apply(x);
   } else {
 #pragma unroll
-    for (int i = S - 1; i >= 0; --i) xs[i] = x = fmaf(mul[i], x, add[i]);
+    for (int i = S - 1; i >= 0; --i) xs[i] = x = steps[i].apply(x);
   }
 }
 
@@ -394,6 +455,19 @@ __device__ __forceinline__ float dpp(float src, float old) {
 __device__ __forceinline__ float lane_prev(float v) { return dpp<kDppWaveShr1, 0xf>(v, v); }
 __device__ __forceinline__ Halo2 lane_prev(Halo2 h) { return Halo2{lane_prev(h.a), lane_prev(h.b)}; }
 __device__ __forceinline__ NoHalo lane_prev(NoHalo h) { return h; }
+__device__ __forceinline__ NvX lane_prev(NvX s) { return NvX{lane_prev(s.nv), lane_prev(s.x)}; }
+
+// A map moved by a DPP control; lanes without a source get the identity.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ Affine dpp_map(Affine m) {
+  return Affine{dpp<CTRL, ROW_MASK>(m.mul, 1.f), dpp<CTRL, ROW_MASK>(m.add, 0.f)};
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ SkipAffine dpp_map(SkipAffine m) {
+  return SkipAffine{dpp<CTRL, ROW_MASK>(m.a, 1.f), dpp<CTRL, ROW_MASK>(m.c, 0.f),
+                    dpp<CTRL, ROW_MASK>(m.p, 0.f), dpp<CTRL, ROW_MASK>(m.q, 1.f),
+                    dpp<CTRL, ROW_MASK>(m.d, 0.f)};
+}
 
 // The data of a segment that the next segment in scan order needs: its last step (forward
 // scans: done[t-1]) or its first step (backward scans: values[t+1], ...).
@@ -403,28 +477,25 @@ __device__ __forceinline__ typename Op::Halo scan_export(const Op& op, const typ
   else return op.template export_first<S>(R);
 }
 
-template <int D>
-__device__ __forceinline__ Affine scan_step_rows(Affine m, int li) {
-  float pm = dpp<kDppRowShr + D, 0xf>(m.mul, 1.f);
-  float pa = dpp<kDppRowShr + D, 0xf>(m.add, 0.f);
-  if (li < D) {  // groups narrower than a DPP row: the source lane is in another group
-    pm = 1.f;
-    pa = 0.f;
-  }
-  return compose(m, Affine{pm, pa});
+template <int D, class M>
+__device__ __forceinline__ M scan_step_rows(M m, int li) {
+  M prev = dpp_map<kDppRowShr + D, 0xf>(m);
+  if (li < D) prev = M::identity();  // groups narrower than a DPP row: the source is in another group
+  return compose(m, prev);
 }
 
-// Inclusive scan of affine maps towards higher lanes, in groups of W lanes (W a power of
-// two <= 64, wave-uniform): lane i ends up with m_i o m_{i-1} o ... o m_0 of its group.
-// Kogge-Stone within rows of 16 lanes, then row_bcast to join rows.
-__device__ __forceinline__ Affine lane_scan(Affine m, int W) {
+// Inclusive scan of maps towards higher lanes, in groups of W lanes (W a power of two <= 64,
+// wave-uniform): lane i ends up with m_i o m_{i-1} o ... o m_0 of its group.  Kogge-Stone
+// within rows of 16 lanes, then row_bcast to join rows.
+template <class M>
+__device__ __forceinline__ M lane_scan(M m, int W) {
   const int li = __lane_id() & (W - 1);
   if (W > 1) m = scan_step_rows<1>(m, li);
   if (W > 2) m = scan_step_rows<2>(m, li);
   if (W > 4) m = scan_step_rows<4>(m, li);
   if (W > 8) m = scan_step_rows<8>(m, li);
-  if (W > 16) m = compose(m, Affine{dpp<kDppRowBcast15, 0xa>(m.mul, 1.f), dpp<kDppRowBcast15, 0xa>(m.add, 0.f)});
-  if (W > 32) m = compose(m, Affine{dpp<kDppRowBcast31, 0xc>(m.mul, 1.f), dpp<kDppRowBcast31, 0xc>(m.add, 0.f)});
+  if (W > 16) m = compose(m, dpp_map<kDppRowBcast15, 0xa>(m));
+  if (W > 32) m = compose(m, dpp_map<kDppRowBcast31, 0xc>(m));
   return m;
 }
 
@@ -446,8 +517,10 @@ __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T,
   constexpr int NW = NT / kWave;
   using Regs = typename Op::template Regs<S>;
   using Halo = typename Op::Halo;
+  using Map = typename Op::Map;
+  using State = typename Map::State;
   constexpr bool HAS_HALO = !std::is_same<Halo, NoHalo>::value;
-  __shared__ float s_mul[NW], s_add[NW];
+  __shared__ Map s_map[NW];
 
   const int tid = threadIdx.x;
   const int lane = __lane_id();
@@ -467,7 +540,7 @@ __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T,
   }
   Regs R;
   op.template load<S, VEC>(row, t0, T, R);
-  float carry = row_carry(op, row, T);
+  State carry = row_carry(op, row, T);
   op.template prepare<S, VEC>(R, row, t0, T);
   Halo h{};
   if constexpr (HAS_HALO) {
@@ -475,25 +548,22 @@ __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T,
     if (lane == 0) h = edge;  // unused when li == 0: the row's first segment in scan order
   }
 
-  float mul[S], add[S];
-  op.template coef<S>(R, h, row, t0, T, mul, add);
-  const Affine m = lane_scan(fold_segment<FWD, S>(mul, add), W);
+  Map steps[S];
+  op.template coef<S>(R, h, row, t0, T, steps);
+  const Map m = lane_scan(fold_segment<FWD, S>(steps), W);
 
   if (L > kWave) {
     // rows spanning several waves: combine the wave aggregates of the row through LDS
-    if (lane == kWave - 1) {
-      s_mul[wave] = m.mul;
-      s_add[wave] = m.add;
-    }
+    if (lane == kWave - 1) s_map[wave] = m;
     __syncthreads();
     const int first = (wave / (L / kWave)) * (L / kWave);
-    for (int v = first; v < wave; ++v) carry = fmaf(s_mul[v], carry, s_add[v]);
+    for (int v = first; v < wave; ++v) carry = s_map[v].apply(carry);
   }
-  // value entering the segment: the previous lane's outgoing value, or the carry
-  float x_in = lane_prev(fmaf(m.mul, carry, m.add));
+  // state entering the segment: the previous lane's outgoing state, or the carry
+  State x_in = lane_prev(m.apply(carry));
   if ((li & (W - 1)) == 0) x_in = carry;
-  float xs[S];
-  replay<FWD, S>(mul, add, x_in, xs);
+  State xs[S];
+  replay<FWD, S>(steps, x_in, xs);
   if (active) op.template emit<S, VEC>(R, h, xs, x_in, row, t0, T);
   if constexpr (Op::kBlockStats) {
     double sum = 0.0, sq = 0.0;
@@ -517,61 +587,79 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 
 // Carry entering tile k of `row` (one wave, all 64 lanes): publish the tile's
 // map and look back.  Predecessors are read 64 at a time (lane i <-> i+1 tiles away).
-// Once the nearest published inclusive value X has only aggregates between it and this
+// Once the nearest published inclusive state X has only aggregates between it and this
 // tile, they are applied to X one at a time, nearest last, so every published X equals the
-// sequential chain X_k = fma(A_k, X_{k+1}, B_k) however far the look-back reached: results
-// are bit-reproducible.  A bounded wait gives up (error flag, carry 0) rather than hang.
+// sequential chain X_k = A_k(X_{k+1}) however far the look-back reached: results are
+// bit-reproducible.  A bounded wait gives up (error flag, carry 0) rather than hang.
 // The first tile of a row (in scan order) takes `row_c`, the row's own carry.
-template <bool FWD>
-__device__ __forceinline__ float tile_carry(Affine tm, float row_c, int64_t row, int k,
-                                            int tiles_per_row, uint32_t epoch, uint64_t* ws,
-                                            int lane) {
-  uint64_t* st = ws + kStatusOffset + 2 * (row * (int64_t)tiles_per_row);
+// Tile k's status words are st[M::kWords * k + i] (kStatusWords bounds M::kWords).
+template <bool FWD, class M>
+__device__ __forceinline__ typename M::State tile_carry(M tm, typename M::State row_c, int64_t row,
+                                                        int k, int tiles_per_row, uint32_t epoch,
+                                                        uint64_t* ws, int lane) {
+  using State = typename M::State;
+  constexpr int NWD = M::kWords, NSW = M::kStateWords;
+  static_assert(NWD <= kStatusWords && NSW <= NWD, "status words per tile");
+  uint64_t* st = ws + kStatusOffset + NWD * (row * (int64_t)tiles_per_row);
   const uint32_t tag_agg = (epoch << 2) | kAgg, tag_inc = (epoch << 2) | kInc;
+  // word 0 last: it names the kind
+  auto publish_inc = [&](State x) {
+#pragma unroll
+    for (int i = NSW - 1; i >= 0; --i) atomic_st(st + NWD * k + i, pack(tag_inc, state_word(x, i)));
+  };
   if (FWD ? (k == 0) : (k == tiles_per_row - 1)) {
     wait_vmem();
-    if (lane == 0) atomic_st(st + 2 * k, pack(tag_inc, fmaf(tm.mul, row_c, tm.add)));
+    if (lane == 0) publish_inc(tm.apply(row_c));
     return row_c;
   }
   if (lane == 0) {
-    if (tm.mul == 0.f) {
-      // the tile's outgoing value does not depend on its carry
-      atomic_st(st + 2 * k, pack(tag_inc, tm.add));
+    if (tm.constant()) {
+      // the tile's outgoing state does not depend on its carry
+      publish_inc(tm.apply(State{}));
     } else {
-      atomic_st(st + 2 * k + 1, pack(tag_agg, tm.add));
-      atomic_st(st + 2 * k, pack(tag_agg, tm.mul));
+#pragma unroll
+      for (int i = NWD - 1; i >= 0; --i) atomic_st(st + NWD * k + i, pack(tag_agg, tm.word(i)));
     }
   }
-  float c = 0.f;
+  State c{};
   for (int spins = 0;; ++spins) {
     const int jj = FWD ? k - 1 - lane : k + 1 + lane;
     const bool inr = FWD ? (jj >= 0) : (jj < tiles_per_row);
     uint32_t kind = 0;
-    float v0 = 1.f, v1 = 0.f;
+    float w[NWD];
+#pragma unroll
+    for (int i = 0; i < NWD; ++i) w[i] = 0.f;
     if (inr) {
-      // Both words in flight at once.  word1 is written once per call, before word0's AGG,
-      // so a current-epoch AGG word0 with a current-epoch word1 is a consistent (mul, add)
-      // pair; a stale word1 just means "not yet".
-      const uint64_t w0 = atomic_ld(st + 2 * jj);
-      const uint64_t w1 = atomic_ld(st + 2 * jj + 1);
-      const uint32_t tag0 = (uint32_t)(w0 >> 32);
-      v0 = __uint_as_float((uint32_t)w0);
+      // All words in flight at once.  Each word is written at most once per call and kind,
+      // so words that all carry the current AGG tag (or INC tag) are one consistent map (or
+      // state); a word with another tag just means "not yet".
+      uint64_t raw[NWD];
+#pragma unroll
+      for (int i = 0; i < NWD; ++i) raw[i] = atomic_ld(st + NWD * jj + i);
+      const uint32_t tag0 = (uint32_t)(raw[0] >> 32);
       if ((tag0 >> 2) == epoch) kind = tag0 & 3u;
-      if (kind == kAgg) {
-        if ((uint32_t)(w1 >> 32) == tag_agg) v1 = __uint_as_float((uint32_t)w1);
-        else kind = 0;
-      }
+      const uint32_t want = kind == kAgg ? tag_agg : tag_inc;
+      const int nw = kind == kAgg ? NWD : NSW;
+#pragma unroll
+      for (int i = 1; i < NWD; ++i)
+        if (i < nw && (uint32_t)(raw[i] >> 32) != want) kind = 0;
+#pragma unroll
+      for (int i = 0; i < NWD; ++i) w[i] = __uint_as_float((uint32_t)raw[i]);
     }
     const uint64_t inc_mask = __ballot(kind == kInc);
     const uint64_t bad_mask = __ballot(kind == 0);
     const int first_inc = inc_mask ? __ffsll((long long)inc_mask) - 1 : kWave;
     const int first_bad = bad_mask ? __ffsll((long long)bad_mask) - 1 : kWave;
     if (first_inc < first_bad) {
-      float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v0), first_inc));
+      float iw[NSW];
+#pragma unroll
+      for (int i = 0; i < NSW; ++i) iw[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[i]), first_inc));
+      State x = state_from_words<State>(iw);
       for (int l = first_inc - 1; l >= 0; --l) {
-        const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v0), l));
-        const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v1), l));
-        x = fmaf(a, x, b);
+        float aw[NWD];
+#pragma unroll
+        for (int i = 0; i < NWD; ++i) aw[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[i]), l));
+        x = M::from_words(aw).apply(x);
       }
       c = x;
       break;
@@ -583,7 +671,7 @@ __device__ __forceinline__ float tile_carry(Affine tm, float row_c, int64_t row,
     __builtin_amdgcn_s_sleep(1);
   }
   wait_vmem();
-  if (lane == 0 && tm.mul != 0.f) atomic_st(st + 2 * k, pack(tag_inc, fmaf(tm.mul, c, tm.add)));
+  if (lane == 0 && !tm.constant()) publish_inc(tm.apply(c));
   return c;
 }
 
@@ -611,6 +699,13 @@ __device__ __forceinline__ float lane_bcast(float v, int l) {
 }
 __device__ __forceinline__ Halo2 lane_bcast(Halo2 h, int l) { return Halo2{lane_bcast(h.a, l), lane_bcast(h.b, l)}; }
 __device__ __forceinline__ NoHalo lane_bcast(NoHalo h, int) { return h; }
+__device__ __forceinline__ Affine lane_bcast(Affine m, int l) {
+  return Affine{lane_bcast(m.mul, l), lane_bcast(m.add, l)};
+}
+__device__ __forceinline__ SkipAffine lane_bcast(SkipAffine m, int l) {
+  return SkipAffine{lane_bcast(m.a, l), lane_bcast(m.c, l), lane_bcast(m.p, l), lane_bcast(m.q, l),
+                    lane_bcast(m.d, l)};
+}
 
 constexpr int kSeg = 4;  // steps per segment of the long-row path
 
@@ -623,9 +718,11 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
   static_assert(NT % kWave == 0, "whole waves");
   using Regs = typename Op::template Regs<kSeg>;
   using Halo = typename Op::Halo;
+  using Map = typename Op::Map;
+  using State = typename Map::State;
   constexpr bool HAS_HALO = !std::is_same<Halo, NoHalo>::value;
-  __shared__ float s_mul[NW], s_add[NW];
-  __shared__ float s_carry;
+  __shared__ Map s_map[NW];
+  __shared__ State s_carry;
   __shared__ uint64_t s_q;
   __shared__ uint32_t s_epoch;
 
@@ -678,7 +775,7 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
         edge = op.halo_load(row, clamp_step(FWD ? wbase - 1 : wbase + WSTEPS, T), T);
     }
     const bool first = FWD ? (k == 0) : (k == tiles_per_row - 1);
-    const float rc = (first && wave == 0) ? row_carry(op, row, T) : 0.f;
+    const State rc = (first && wave == 0) ? row_carry(op, row, T) : State{};
 
 #pragma unroll
     for (int r = 0; r < Q; ++r) op.template prepare<kSeg, VEC>(R[r], row, seg_t0(r), T);
@@ -695,41 +792,38 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
       }
     }
 
-    float mul[Q][kSeg], add[Q][kSeg];
-    Affine m[Q];
-    Affine rowagg[Q];  // map of each segment row (wave-uniform)
+    Map steps[Q][kSeg];
+    Map m[Q];
+    Map rowagg[Q];  // map of each segment row (wave-uniform)
 #pragma unroll
     for (int r = 0; r < Q; ++r) {
-      op.template coef<kSeg>(R[r], h[r], row, seg_t0(r), T, mul[r], add[r]);
-      m[r] = lane_scan(fold_segment<FWD, kSeg>(mul[r], add[r]), kWave);
-      rowagg[r] = Affine{lane_bcast(m[r].mul, kWave - 1), lane_bcast(m[r].add, kWave - 1)};
+      op.template coef<kSeg>(R[r], h[r], row, seg_t0(r), T, steps[r]);
+      m[r] = lane_scan(fold_segment<FWD, kSeg>(steps[r]), kWave);
+      rowagg[r] = lane_bcast(m[r], kWave - 1);
     }
     // the chunk's map: segment rows composed in scan order
-    Affine wm{1.f, 0.f};
+    Map wm = Map::identity();
 #pragma unroll
     for (int r = 0; r < Q; ++r) wm = compose(rowagg[r], wm);
-    if (lane == 0) {
-      s_mul[wave] = wm.mul;
-      s_add[wave] = wm.add;
-    }
+    if (lane == 0) s_map[wave] = wm;
     __syncthreads();
     if (wave == 0) {
-      Affine tm{1.f, 0.f};
-      for (int v = 0; v < NW; ++v) tm = compose(Affine{s_mul[v], s_add[v]}, tm);
-      const float c = tile_carry<FWD>(tm, rc, row, k, tiles_per_row, epoch, ws, lane);
+      Map tm = Map::identity();
+      for (int v = 0; v < NW; ++v) tm = compose(s_map[v], tm);
+      const State c = tile_carry<FWD>(tm, rc, row, k, tiles_per_row, epoch, ws, lane);
       if (lane == 0) s_carry = c;
     }
     __syncthreads();
-    // value entering this wave's chunk, then each segment row, then each lane
-    float carry = s_carry;
-    for (int v = 0; v < wave; ++v) carry = fmaf(s_mul[v], carry, s_add[v]);
+    // state entering this wave's chunk, then each segment row, then each lane
+    State carry = s_carry;
+    for (int v = 0; v < wave; ++v) carry = s_map[v].apply(carry);
 #pragma unroll
     for (int r = 0; r < Q; ++r) {
-      float x_in = lane_prev(fmaf(m[r].mul, carry, m[r].add));
+      State x_in = lane_prev(m[r].apply(carry));
       if (lane == 0) x_in = carry;
-      carry = fmaf(rowagg[r].mul, carry, rowagg[r].add);
-      float xs[kSeg];
-      replay<FWD, kSeg>(mul[r], add[r], x_in, xs);
+      carry = rowagg[r].apply(carry);
+      State xs[kSeg];
+      replay<FWD, kSeg>(steps[r], x_in, xs);
       op.template emit<kSeg, VEC>(R[r], h[r], xs, x_in, row, seg_t0(r), T);
       if constexpr (Op::kBlockStats) accumulate_stats<kSeg>(xs, seg_t0(r), T, true, st_sum, st_sq);
     }

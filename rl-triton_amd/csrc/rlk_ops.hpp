@@ -34,6 +34,7 @@ struct GaeOp {
   // in registers (no spills at 1024 threads, whose cap is 128 VGPRs)
   static constexpr int kLongThreads = 1024, kLongMaxSegments = 4;
   using Halo = float;  // values[t+1]
+  using Map = Affine;  // one carried value
   const E* r;
   const E* v;
   const E* term;
@@ -68,8 +69,7 @@ struct GaeOp {
   __device__ float halo_load(int64_t row, int t, int T) const { return to_f32(v[row * (int64_t)T + t]); }
 
   template <int S>
-  __device__ void coef(const Regs<S>& R, float vh, int64_t, int t0, int T, float (&mul)[S],
-                       float (&add)[S]) const {
+  __device__ void coef(const Regs<S>& R, float vh, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
@@ -78,8 +78,8 @@ struct GaeOp {
       const float done = TRUNC ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
       const float a = fmaf(gamma * vn, 1.f - R.te[i], R.r[i]) - R.v[i];
       const bool in = t < T;  // padding steps are the identity map
-      add[i] = in ? a : 0.f;
-      mul[i] = in ? gl * (1.f - done) : 1.f;
+      m[i].add = in ? a : 0.f;
+      m[i].mul = in ? gl * (1.f - done) : 1.f;
     }
   }
   __device__ const E* row_carry_src(int64_t, int) const { return nullptr; }
@@ -121,6 +121,92 @@ struct GaeStatsOp : GaeOp<TRUNC, E> {
 };
 
 // ------------------------------------------------------------------------------------------
+// GAE with skipped steps: the "verl-style" masking of the reference's ROADMAP.md:131-140
+// (not implemented in the reference).  Steps with mask == 0 leave the advantage and the
+// next value unchanged, so credit and the continuation value pass across them (multi-turn
+// rollouts whose observation tokens are not actions).  With nv = the value of the nearest
+// kept step after t (boot(T-1) if there is none):
+//   kept t:     v_next = boot(t) if trunc[t] == 1, nv otherwise
+//               A[t] = r + gamma*v_next*(1-term) - v + gamma*lambda*(1-done)*A(after t)
+//               nv <- v[t]
+//   skipped t:  A[t] = A(after t) (0 if no kept step follows), nv unchanged
+// With every step kept this is GaeOp.  The state {nv, A} is carried by SkipAffine maps:
+// a kept step is (a, c, p, q, d) = (0, v, gamma*(1-term) [0 if truncated], gamma*lambda*
+// (1-done), r - v [+ gamma*boot*(1-term) if truncated]); a skipped step is the identity.
+// No halo: the next value arrives through the scan itself.
+// ------------------------------------------------------------------------------------------
+template <bool TRUNC, class E = float>
+struct MaskedGaeOp {
+  static constexpr bool kForward = false;
+  static constexpr bool kBlockStats = false;
+  static constexpr int kLongThreads = 512, kLongMaxSegments = 4;  // five-word maps
+  using Halo = NoHalo;
+  using Map = SkipAffine;  // state {next value, advantage}
+  const E* r;
+  const E* v;
+  const E* term;
+  const E* trunc;  // read iff TRUNC
+  const E* boot;   // nullable, per boot_mode
+  const E* mask;
+  E* out;
+  int boot_mode;
+  float gamma, gl;  // gl = gamma*lambda
+
+  template <int S>
+  struct Regs {
+    float r[S], v[S], te[S], tr[S], bt[S], mk[S];
+    float blast;
+  };
+
+  template <int S, bool VEC>
+  __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
+    const int64_t o = row * (int64_t)T;
+    load_seg<S, VEC>(r + o, t0, T, R.r);
+    load_seg<S, VEC>(v + o, t0, T, R.v);
+    load_seg<S, VEC>(term + o, t0, T, R.te);
+    load_seg<S, VEC>(mask + o, t0, T, R.mk);
+    if constexpr (TRUNC) {
+      load_seg<S, VEC>(trunc + o, t0, T, R.tr);
+      boot_load<S, VEC, true>(boot, boot_mode, row, t0, T, R.bt, R.blast, r + o);
+    } else {
+      fill_regs(R.tr, 0.f), fill_regs(R.bt, 0.f);
+      R.blast = 0.f;
+    }
+  }
+  template <int S, bool VEC>
+  __device__ void prepare(Regs<S>& R, int64_t, int t0, int T) const {
+    if constexpr (TRUNC) boot_prepare<S, true>(boot_mode, t0, T, R.bt, R.blast);
+  }
+  // state after the row: next value boot(T-1), advantage 0
+  __device__ NvX row_state(int64_t row, int T) const {
+    return NvX{to_f32(*boot_last(boot, boot_mode, row, T)), 0.f};
+  }
+
+  template <int S>
+  __device__ void coef(const Regs<S>& R, NoHalo, int64_t, int t0, int T, SkipAffine (&m)[S]) const {
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const bool sel = TRUNC && R.tr[i] == 1.f;
+      const float done = TRUNC ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
+      const float g1 = gamma * (1.f - R.te[i]);
+      const float d = sel ? fmaf(gamma * R.bt[i], 1.f - R.te[i], R.r[i]) - R.v[i] : R.r[i] - R.v[i];
+      const bool kept = t0 + i < T && R.mk[i] != 0.f;  // padding steps are skipped too
+      m[i] = kept ? SkipAffine{0.f, R.v[i], sel ? 0.f : g1, gl * (1.f - done), d}
+                  : SkipAffine::identity();
+    }
+  }
+
+  template <int S, bool VEC>
+  __device__ void emit(const Regs<S>&, NoHalo, const NvX (&xs)[S], NvX, int64_t row, int t0,
+                       int T) const {
+    float a[S];
+#pragma unroll
+    for (int i = 0; i < S; ++i) a[i] = xs[i].x;
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, a);
+  }
+};
+
+// ------------------------------------------------------------------------------------------
 // V-trace: kernels/vtrace_fused.py:90-196 (vtrace_fused_kernel).
 //   rho = min(exp(lpt - lpb), rho_bar),  c = min(exp(lpt - lpb), c_bar)
 //   truncations:  v_next = values[t+1]*[t < T-1 and trunc == 0] + boot(t)   (additive)
@@ -137,6 +223,7 @@ struct VtraceOp {
   static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
   static constexpr int kLongThreads = 1024, kLongMaxSegments = 2;
   using Halo = float;  // values[t+1]
+  using Map = Affine;  // one carried value
   const E* lpt;
   const E* lpb;
   const E* v;
@@ -188,8 +275,7 @@ struct VtraceOp {
   }
 
   template <int S>
-  __device__ void coef(const Regs<S>& R, float vh, int64_t, int t0, int T, float (&mul)[S],
-                       float (&add)[S]) const {
+  __device__ void coef(const Regs<S>& R, float vh, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
@@ -197,8 +283,8 @@ struct VtraceOp {
       const float done = TRUNC ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
       const float a = R.rho[i] * (fmaf(gamma * vn, 1.f - R.te[i], R.r[i]) - R.v[i]);
       const bool in = t < T;
-      add[i] = in ? a : 0.f;
-      mul[i] = in ? gamma * R.c[i] * (1.f - done) : 1.f;
+      m[i].add = in ? a : 0.f;
+      m[i].mul = in ? gamma * R.c[i] * (1.f - done) : 1.f;
     }
   }
   __device__ const E* row_carry_src(int64_t, int) const { return nullptr; }
@@ -235,6 +321,7 @@ struct RetraceOp {
   static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
   static constexpr int kLongThreads = 512, kLongMaxSegments = 2;  // 256 VGPRs: the A-wide rows
   using Halo = Halo2;  // {c[t+1], q[t+1]}
+  using Map = Affine;  // one carried value
   const E* pi;     // [E, T, A]
   const E* mu;     // [E, T]
   const E* q;
@@ -324,8 +411,7 @@ struct RetraceOp {
   }
 
   template <int S>
-  __device__ void coef(const Regs<S>& R, Halo2 h, int64_t, int t0, int T, float (&mul)[S],
-                       float (&add)[S]) const {
+  __device__ void coef(const Regs<S>& R, Halo2 h, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
@@ -333,8 +419,8 @@ struct RetraceOp {
       const float done = fminf(R.te[i] + R.tr[i], 1.f);
       const float a = fmaf(gamma * R.enq[i], 1.f - R.te[i], R.r[i]) - R.q[i];
       const bool in = t < T;
-      add[i] = in ? a : 0.f;
-      mul[i] = in ? gamma * c_next * (1.f - done) : 1.f;
+      m[i].add = in ? a : 0.f;
+      m[i].mul = in ? gamma * c_next * (1.f - done) : 1.f;
     }
   }
   __device__ const E* row_carry_src(int64_t, int) const { return nullptr; }
@@ -370,6 +456,7 @@ struct ReturnsOp {
   static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
   static constexpr int kLongThreads = 1024, kLongMaxSegments = (NV || TRUNC) ? 4 : 8;
   using Halo = NoHalo;
+  using Map = Affine;  // one carried value
   const E* r;
   const E* nv;     // read iff NV
   const E* term;
@@ -406,8 +493,7 @@ struct ReturnsOp {
   }
 
   template <int S>
-  __device__ void coef(const Regs<S>& R, NoHalo, int64_t, int t0, int T, float (&mul)[S],
-                       float (&add)[S]) const {
+  __device__ void coef(const Regs<S>& R, NoHalo, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
@@ -415,8 +501,8 @@ struct ReturnsOp {
       float a = NV ? fmaf(g1l * nd, R.nv[i], R.r[i]) : R.r[i];
       if constexpr (TRUNC) a = fmaf(gamma * R.tr[i], R.bt[i], a);
       const bool in = t < T;
-      add[i] = in ? a : 0.f;
-      mul[i] = in ? gl * nd : 1.f;
+      m[i].add = in ? a : 0.f;
+      m[i].mul = in ? gl * nd : 1.f;
     }
   }
   __device__ const E* row_carry_src(int64_t row, int T) const {
@@ -444,6 +530,7 @@ struct DoneGatedForwardOp {
   static constexpr bool kBlockStats = false;
   static constexpr int kLongThreads = 1024, kLongMaxSegments = 8;
   using Halo = float;  // done[t-1]
+  using Map = Affine;  // one carried value
   const E* x;
   const E* dones;
   const E* seed;  // nullable
@@ -469,8 +556,7 @@ struct DoneGatedForwardOp {
   __device__ float halo_load(int64_t row, int t, int T) const { return to_f32(dones[row * (int64_t)T + t]); }
 
   template <int S>
-  __device__ void coef(const Regs<S>& R, float dh, int64_t, int t0, int T, float (&mul)[S],
-                       float (&add)[S]) const {
+  __device__ void coef(const Regs<S>& R, float dh, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
@@ -478,8 +564,8 @@ struct DoneGatedForwardOp {
       if (ends_at) gate = (i > 0) ? R.d[i - 1] : (t == 0 ? 0.f : dh);
       else gate = R.d[i];
       const bool in = t < T;
-      mul[i] = in ? decay * (1.f - gate) : 1.f;
-      add[i] = in ? R.x[i] : 0.f;
+      m[i].mul = in ? decay * (1.f - gate) : 1.f;
+      m[i].add = in ? R.x[i] : 0.f;
     }
   }
   __device__ const E* row_carry_src(int64_t row, int) const { return seed ? seed + row : nullptr; }
@@ -501,6 +587,7 @@ struct AffineScanOp {
   static constexpr bool kBlockStats = false;
   static constexpr int kLongThreads = 1024, kLongMaxSegments = 8;
   using Halo = NoHalo;
+  using Map = Affine;  // one carried value
   const E* u;
   const E* v;
   const E* carry;  // nullable, [E]
@@ -519,13 +606,12 @@ struct AffineScanOp {
   template <int S, bool VEC>
   __device__ void prepare(Regs<S>&, int64_t, int, int) const {}
   template <int S>
-  __device__ void coef(const Regs<S>& R, NoHalo, int64_t, int t0, int T, float (&mul)[S],
-                       float (&add)[S]) const {
+  __device__ void coef(const Regs<S>& R, NoHalo, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const bool in = t0 + i < T;
-      mul[i] = in ? R.v[i] : 1.f;
-      add[i] = in ? R.u[i] : 0.f;
+      m[i].mul = in ? R.v[i] : 1.f;
+      m[i].add = in ? R.u[i] : 0.f;
     }
   }
   __device__ const E* row_carry_src(int64_t row, int) const { return carry ? carry + row : nullptr; }

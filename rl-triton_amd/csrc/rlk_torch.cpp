@@ -150,9 +150,10 @@ bool nargs_is(Py_ssize_t n, Py_ssize_t want, const char* name) {
   return false;
 }
 
-// gae(rewards, values, terminateds, truncateds, gamma, lambda_, bootstrap_values, last_value)
+// gae(rewards, values, terminateds, truncateds, gamma, lambda_, bootstrap_values, last_value,
+//     mask)
 PyObject* op_gae(PyObject* const* a, Py_ssize_t n) {
-  if (!nargs_is(n, 8, "gae")) return nullptr;
+  if (!nargs_is(n, 9, "gae")) return nullptr;
   if (correctness_warnings()) return decline();
   Call c;
   const at::Tensor* r = c.lead(a[0]);
@@ -164,15 +165,20 @@ PyObject* op_gae(PyObject* const* a, Py_ssize_t n) {
   if (has_bv && has_lv) return decline();  // the wrapper raises "not both"
   if (has_lv && tr) return decline();      // ... and "cannot be combined with truncateds"
   const at::Tensor* boot = has_lv ? c.need(a[7], 1) : c.opt(a[6]);
+  const at::Tensor* mask = c.opt(a[8]);
   if (!c.ok) return decline();
   const int mode = has_lv ? RLK_BOOT_ROW : has_bv ? RLK_BOOT_FULL : RLK_BOOT_NONE;
   at::Tensor out = c.output(*r);
   const int st = dispatch(c, [&](auto z) {
     using T = decltype(z);
+    if (mask)
+      return pick<T>(rlk_gae_masked, rlk_gae_masked_bf16)(in_ptr<T>(r), in_ptr<T>(v),
+        in_ptr<T>(te), in_ptr<T>(tr), in_ptr<T>(boot), mode, in_ptr<T>(mask), out_ptr<T>(out),
+        c.E, c.T, gamma, lam, nullptr, 0, c.stream());
     return pick<T>(rlk_gae, rlk_gae_bf16)(in_ptr<T>(r), in_ptr<T>(v), in_ptr<T>(te), in_ptr<T>(tr),
       in_ptr<T>(boot), mode, out_ptr<T>(out), c.E, c.T, gamma, lam, nullptr, 0, c.stream());
   });
-  return finish(st, "rlk_gae", THPVariable_Wrap(std::move(out)));
+  return finish(st, mask ? "rlk_gae_masked" : "rlk_gae", THPVariable_Wrap(std::move(out)));
 }
 
 // gae_normalized(rewards, values, terminateds, truncateds, gamma, lambda_, bootstrap_values,

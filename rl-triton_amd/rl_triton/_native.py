@@ -33,6 +33,7 @@ _SZ = ctypes.c_size_t
 # name -> argtypes (must match include/rl_triton_amd.h)
 SIGNATURES = {
     "rlk_gae": [_P, _P, _P, _P, _P, _INT, _P, _I64, _I64, _F, _F, _P, _SZ, _P],
+    "rlk_gae_masked": [_P, _P, _P, _P, _P, _INT, _P, _P, _I64, _I64, _F, _F, _P, _SZ, _P],
     "rlk_gae_normalized": [_P, _P, _P, _P, _P, _INT, _P, _P, _I64, _I64, _F, _F, _F, _P, _SZ, _P,
                            _SZ, _P],
     "rlk_gae_normalized_partials_bytes": [_I64, _I64],
@@ -49,7 +50,7 @@ SIGNATURES = {
     "rlk_version": [],
 }
 # the bfloat16 twins take the same arguments (rlk_bf16 arrays in place of float ones)
-for _name in ("rlk_gae", "rlk_gae_normalized", "rlk_vtrace", "rlk_retrace", "rlk_lambda_returns",
+for _name in ("rlk_gae", "rlk_gae_masked", "rlk_gae_normalized", "rlk_vtrace", "rlk_retrace", "rlk_lambda_returns",
               "rlk_discounted_returns", "rlk_eligibility_traces", "rlk_prefix_sum",
               "rlk_affine_scan"):
     SIGNATURES[_name + "_bf16"] = SIGNATURES[_name]
@@ -242,6 +243,22 @@ def gae(rewards, values, terminateds, truncateds, bootstrap, out, gamma, lambda_
             _ptr(rewards, "rewards", shape, dev, dt), _ptr(values, "values", shape, dev, dt),
             _ptr(terminateds, "terminateds", shape, dev, dt), _opt(truncateds, "truncateds", shape, dev, dt),
             bp, mode, _ptr(out, "out", shape, dev, dt), n_env, n_t, gamma, lambda_)
+    return out
+
+
+def gae_masked(rewards, values, terminateds, truncateds, bootstrap, mask, out, gamma, lambda_):
+    dev = _device_of(rewards)
+    shape = rewards.shape
+    dt = rewards.dtype
+    n_env, n_t = shape
+    lib = _lib or load()
+    bp, mode = _boot_args(bootstrap, n_env, n_t, dev, dt)
+    _launch(_entry(lib, "rlk_gae_masked", dt), "rlk_gae_masked", dev, n_env, n_t,
+            _ptr(rewards, "rewards", shape, dev, dt), _ptr(values, "values", shape, dev, dt),
+            _ptr(terminateds, "terminateds", shape, dev, dt),
+            _opt(truncateds, "truncateds", shape, dev, dt), bp, mode,
+            _ptr(mask, "mask", shape, dev, dt), _ptr(out, "out", shape, dev, dt), n_env, n_t,
+            gamma, lambda_)
     return out
 
 

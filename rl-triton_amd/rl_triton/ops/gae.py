@@ -4,10 +4,12 @@ from rl_triton import _native
 from rl_triton.ops._scan import _CORRECTNESS_WARNINGS, _float_io
 
 
-def _check_gae_args(rewards, values, terminateds, truncateds, bootstrap_values, last_value):
+def _check_gae_args(rewards, values, terminateds, truncateds, bootstrap_values, last_value,
+                    mask=None):
     """The reference's compute_gae checks (ops/gae.py:106-145), in its order and with its
     messages: always-on structural checks, then the expensive ones under
-    RL_TRITON_CORRECTNESS_WARNINGS=1."""
+    RL_TRITON_CORRECTNESS_WARNINGS=1.  `mask` (an extension) gets the same structural
+    checks as truncateds."""
     num_envs, seq_len = rewards.shape
     has_truncations   = truncateds is not None
 
@@ -21,6 +23,10 @@ def _check_gae_args(rewards, values, terminateds, truncateds, bootstrap_values, 
         assert _float_io(truncateds, rewards), "truncateds: expected float32 (or bfloat16 throughout)"
         assert truncateds.shape == rewards.shape, \
             f"truncateds shape {truncateds.shape} != rewards shape {rewards.shape}"
+    if mask is not None:
+        assert mask.is_cuda,                "mask must be on CUDA"
+        assert _float_io(mask, rewards),    "mask: expected float32 (or bfloat16 throughout)"
+        assert mask.shape == rewards.shape, f"mask shape {mask.shape} != rewards shape {rewards.shape}"
     if last_value is not None:
         assert bootstrap_values is None, \
             "pass either last_value (shape [num_envs], convenience for the " \
@@ -63,6 +69,8 @@ def compute_gae(
     lambda_: float = 0.95,
     bootstrap_values: torch.Tensor | None = None,
     last_value: torch.Tensor | None = None,
+    *,
+    mask: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """
     Generalized Advantage Estimation by a backward affine scan on gfx950.
@@ -85,6 +93,14 @@ def compute_gae(
     One kernel launch for every seq_len (rows longer than one workgroup tile use the
     look-back path); truncation and bootstrap are folded into (δ, β) in-kernel.
 
+    `mask` (keyword-only; an extension listed in the reference's ROADMAP.md:131-140, in
+    the manner of verl's compute_gae_advantage_return with its response_mask): steps with
+    mask == 0 are skipped.  A skipped step passes the recurrence through (β = 1, δ = 0)
+    and returns the advantage of the next kept step (0 if none); the value a kept step
+    bootstraps from is that of the nearest kept step after it, so credit crosses skipped
+    spans (observation tokens of multi-turn rollouts).  Kept steps follow the rules
+    above; with every step kept the result is the unmasked one.
+
     Args:
         rewards:          [num_envs, seq_len], float32, GPU.
         values:           V(s_t), [num_envs, seq_len], float32, GPU.
@@ -94,6 +110,8 @@ def compute_gae(
         lambda_:          GAE λ (default 0.95).
         bootstrap_values: V(s_{t+1}^true) per step, [num_envs, seq_len], or None.
         last_value:       V(s_T) per environment, [num_envs], or None.
+        mask:             1.0 for steps that take part, 0.0 for skipped ones, same shape,
+                          or None (every step takes part).
 
     Returns:
         advantages: A[t], shape [num_envs, seq_len], float32.
@@ -101,12 +119,13 @@ def compute_gae(
     # fast path: a well-formed call goes straight to the C ABI (rl_triton._rlk_torch)
     fast = _native.fast
     if fast is not None:
-        res = fast.gae(rewards, values, terminateds, truncateds, gamma, lambda_, bootstrap_values, last_value)
+        res = fast.gae(rewards, values, terminateds, truncateds, gamma, lambda_, bootstrap_values,
+                       last_value, mask)
         if res is not None:
             return res
 
     has_truncations = truncateds is not None
-    _check_gae_args(rewards, values, terminateds, truncateds, bootstrap_values, last_value)
+    _check_gae_args(rewards, values, terminateds, truncateds, bootstrap_values, last_value, mask)
 
     rewards     = rewards.contiguous()
     values      = values.contiguous()
@@ -121,4 +140,7 @@ def compute_gae(
         bootstrap = None
 
     out = torch.empty_like(rewards)
+    if mask is not None:
+        return _native.gae_masked(rewards, values, terminateds, truncateds, bootstrap,
+                                  mask.contiguous(), out, gamma, lambda_)
     return _native.gae(rewards, values, terminateds, truncateds, bootstrap, out, gamma, lambda_)

@@ -11,6 +11,7 @@ import os
 import numpy as np
 import torch
 
+from baseline_configs import span_mask  # noqa: F401  (re-exported for the tests)
 from oracle import oracle as orc
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "known_answers.json")
@@ -30,7 +31,7 @@ OUTPUTS = {
     "retrace": ("targets", "advantages"), "lambda_returns": ("returns",),
     "discounted_returns": ("returns",), "eligibility_traces": ("traces",),
     "prefix_sum": ("prefix_sums",), "backward_scan": ("out",), "forward_scan": ("out",),
-    "gae_normalized": ("advantages", "returns"),
+    "gae_normalized": ("advantages", "returns"), "gae_masked": ("advantages",),
 }
 
 
@@ -49,6 +50,10 @@ def run_oracle(op, inp, params):
         boot = g("last_value") if g("last_value") is not None else g("bootstrap_values")
         return (orc.gae(g("rewards"), g("values"), g("terminateds"), g("truncateds"),
                         bootstrap=boot, **params),)
+    if op == "gae_masked":
+        boot = g("last_value") if g("last_value") is not None else g("bootstrap_values")
+        return (orc.gae_masked(g("rewards"), g("values"), g("terminateds"), g("mask"),
+                               g("truncateds"), bootstrap=boot, **params),)
     if op == "gae_normalized":
         boot = g("last_value") if g("last_value") is not None else g("bootstrap_values")
         p = dict(params)
@@ -105,6 +110,10 @@ def run_api(op, inp, params, device, dtype=torch.float32):
         return (rl_triton.compute_gae(g("rewards"), g("values"), g("terminateds"), g("truncateds"),
                                       bootstrap_values=g("bootstrap_values"),
                                       last_value=g("last_value"), **params),)
+    if op == "gae_masked":
+        return (rl_triton.compute_gae(g("rewards"), g("values"), g("terminateds"), g("truncateds"),
+                                      bootstrap_values=g("bootstrap_values"),
+                                      last_value=g("last_value"), mask=g("mask"), **params),)
     if op == "gae_normalized":
         return rl_triton.compute_gae_normalized(g("rewards"), g("values"), g("terminateds"),
                                                 g("truncateds"),
@@ -163,7 +172,8 @@ def make_inputs(op, n_env, n_t, seed=0, p_term=0.05, p_trunc=0.0, boot="none", n
     if p_trunc > 0:
         trunc = (ru(*shape) < p_trunc).float() * (1.0 - term)
     inp = {}
-    if op in ("gae", "gae_normalized", "vtrace", "lambda_returns", "discounted_returns"):
+    if op in ("gae", "gae_normalized", "gae_masked", "vtrace", "lambda_returns",
+              "discounted_returns"):
         if boot == "row":
             inp["last_value"] = rn(n_env)
         elif boot == "full":
@@ -172,9 +182,11 @@ def make_inputs(op, n_env, n_t, seed=0, p_term=0.05, p_trunc=0.0, boot="none", n
                 bv = torch.where(trunc.bool(), rn(*shape), bv)
             bv[:, -1] = rn(n_env)
             inp["bootstrap_values"] = bv
-    if op in ("gae", "gae_normalized"):
+    if op in ("gae", "gae_normalized", "gae_masked"):
         inp.update(rewards=rn(*shape), values=rn(*shape), terminateds=term, truncateds=trunc)
         params = {"gamma": 0.99, "lambda_": 0.95}
+        if op == "gae_masked":
+            inp["mask"] = span_mask(n_env, n_t, g)
     elif op == "vtrace":
         inp.update(log_pi_target=-ru(*shape), log_pi_behavior=-ru(*shape), values=rn(*shape),
                    rewards=rn(*shape), terminateds=term, truncateds=trunc)

@@ -115,6 +115,20 @@ def bytes_per_elem(name: str, dtype=torch.float32) -> int:
     return ints + (bpe - ints) * torch.finfo(dtype).bits // 32
 
 
+def span_mask(n_env: int, n_t: int, g: torch.Generator, mean_span: float = 12.0):
+    """A multi-turn mask for compute_gae(..., mask=...): alternating kept (response) and
+    skipped (observation) spans of geometric lengths with mean `mean_span`, each row
+    starting with either; float32 [n_env, n_t] on the CPU, drawn from `g`."""
+    p = 1.0 / mean_span
+    n_spans = int(2 * n_t / mean_span) + 64
+    u = torch.rand(n_env, n_spans, generator=g).clamp_min(1e-12)
+    ends = torch.cumsum(1 + torch.floor(torch.log(u) / math.log(1.0 - p)).long(), dim=1)
+    t = torch.arange(n_t).expand(n_env, n_t).contiguous()
+    span = torch.searchsorted(ends, t, right=True)
+    first_kept = (torch.rand(n_env, 1, generator=g) < 0.5).long()
+    return ((span + first_kept) % 2 == 1).float()
+
+
 def call(name: str, inp: dict, params: dict):
     """One public-API call of configuration `name` on device tensors; returns a tuple."""
     import rl_triton

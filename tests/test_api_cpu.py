@@ -134,7 +134,7 @@ def test_fast_path_declines_cpu_tensors():
         pytest.skip("rl_triton._rlk_torch is not built")
     x = torch.zeros(4, 8)
     f = _native.fast
-    assert f.gae(x, x, x, None, 0.99, 0.95, None, None) is None
+    assert f.gae(x, x, x, None, 0.99, 0.95, None, None, None) is None
     assert f.vtrace(x, x, x, x, x, None, 0.99, 1.0, 1.0, None, None) is None
     assert f.prefix_sum(x, x, None, True) is None
     assert f.affine_scan(x, x, None, 0) is None

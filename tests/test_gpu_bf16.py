@@ -26,14 +26,15 @@ from _common import OUTPUTS, make_inputs, run_api, run_oracle
 pytestmark = pytest.mark.gpu
 
 BF16 = torch.bfloat16
-OPS = ["gae", "vtrace", "retrace", "lambda_returns", "discounted_returns", "eligibility_traces",
-       "prefix_sum", "backward_scan", "forward_scan"]
+OPS = ["gae", "gae_masked", "vtrace", "retrace", "lambda_returns", "discounted_returns",
+       "eligibility_traces", "prefix_sum", "backward_scan", "forward_scan"]
 SHAPES = [(1, 1), (1, 7), (33, 257), (4096, 128), (16, 2048), (3, 1100), (2, 5001), (3, 5000),
           (2, 40000)]
 
 
 def _inputs(op, shape, seed):
-    boot = ("full" if op in ("gae", "vtrace", "lambda_returns", "discounted_returns") else "row")
+    boot = ("full" if op in ("gae", "gae_masked", "vtrace", "lambda_returns", "discounted_returns")
+            else "row")
     kw = {"p_done": 1e-3} if op in ("prefix_sum", "eligibility_traces") else {}
     return make_inputs(op, *shape, seed=seed, p_trunc=0.02 if op != "retrace" else 0.0,
                        boot=boot, **kw)
@@ -91,6 +92,9 @@ def drift_bound(op, inp, exp):
     rounding adds 2^-9 relative."""
     if op == "prefix_sum":
         l_eff = _longest_run(inp["dones"])
+    elif op == "gae_masked":
+        # skipped steps do not decay: the horizon in steps grows by the skipped share
+        l_eff = 1.0 / (1.0 - 0.99 * 0.95) / max(float(np.mean(inp["mask"])), 1e-3)
     elif op == "discounted_returns":
         l_eff = 1.0 / (1.0 - 0.99)
     elif op in ("backward_scan", "forward_scan"):

@@ -272,8 +272,9 @@ def test_max_abs_error_report(device):
 # ---------------------------------------------------------------------------------------
 # the tensor-level fast path (rl_triton._rlk_torch) against the general Python path
 # ---------------------------------------------------------------------------------------
-FAST_OPS = ["gae", "gae_normalized", "vtrace", "retrace", "lambda_returns", "discounted_returns",
-            "eligibility_traces", "prefix_sum", "backward_scan", "forward_scan"]
+FAST_OPS = ["gae", "gae_masked", "gae_normalized", "vtrace", "retrace", "lambda_returns",
+            "discounted_returns", "eligibility_traces", "prefix_sum", "backward_scan",
+            "forward_scan"]
 
 
 @pytest.mark.parametrize("op", FAST_OPS)
@@ -285,7 +286,8 @@ def test_fast_path_matches_python_path(op, shape, device, monkeypatch):
     the results are bit-identical."""
     from rl_triton import _native
     assert _native.fast is not None, "rl_triton._rlk_torch is not built"
-    boot = ("full" if op in ("gae", "gae_normalized", "vtrace", "lambda_returns", "discounted_returns")
+    boot = ("full" if op in ("gae", "gae_masked", "gae_normalized", "vtrace", "lambda_returns",
+                             "discounted_returns")
             else "row")
     inp, params = make_inputs(op, *shape, seed=21, p_trunc=0.02 if op != "retrace" else 0.0,
                               boot=boot)
@@ -321,14 +323,14 @@ def test_fast_path_declines_what_it_cannot_take(device, monkeypatch):
     from rl_triton import _native
     f = _native.fast
     x = torch.zeros(8, 64, device=device)
-    assert f.gae(x, x, x, None, 0.99, 0.95, None, None) is None  # flag set by the fixture
+    assert f.gae(x, x, x, None, 0.99, 0.95, None, None, None) is None  # flag set by the fixture
     monkeypatch.delenv("RL_TRITON_CORRECTNESS_WARNINGS")
-    assert f.gae(x, x, x, None, 0.99, 0.95, None, None) is not None
-    assert f.gae(x.t(), x.t(), x.t(), None, 0.99, 0.95, None, None) is None
+    assert f.gae(x, x, x, None, 0.99, 0.95, None, None, None) is not None
+    assert f.gae(x.t(), x.t(), x.t(), None, 0.99, 0.95, None, None, None) is None
     long = torch.zeros(2, 4096, device=device)
-    assert f.gae(long, long, long, None, 0.99, 0.95, None, None) is None
-    assert f.gae(x, x, x, None, 0.99, 0.95, x, torch.zeros(8, device=device)) is None
-    assert f.gae(x, x, x.double(), None, 0.99, 0.95, None, None) is None
+    assert f.gae(long, long, long, None, 0.99, 0.95, None, None, None) is None
+    assert f.gae(x, x, x, None, 0.99, 0.95, x, torch.zeros(8, device=device), None) is None
+    assert f.gae(x, x, x.double(), None, 0.99, 0.95, None, None, None) is None
 
 
 # ---------------------------------------------------------------------------------------

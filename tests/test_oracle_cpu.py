@@ -227,3 +227,99 @@ def test_checks_catch_planted_mistakes():
     for nm in names:  # and the unplanted copy passes them all
         c = cases[nm]
         assert np.allclose(gae_variant(c["inputs"], c["params"], None), c["expected"]["advantages"])
+
+
+# ---------------------------------------------------------------------------------------
+# masked GAE (steps with mask == 0 pass A and the next value through; the reference's
+# ROADMAP.md:131-140 item, restating verl's compute_gae_advantage_return).  No reference
+# implementation or fixture exists, so it is pinned by what the semantics fix:
+#   * every step kept == compute_gae's oracle, bit for bit;
+#   * dropping the skipped steps and running plain GAE on what is left gives the kept
+#     steps' advantages, and each skipped step carries the next kept step's (0 if none);
+#   * a hand-worked example of verl's loop.
+# ---------------------------------------------------------------------------------------
+def _masked_case(seed, E, T, p_keep, boot, trunc):
+    inp, _ = make_inputs("gae", E, T, seed=seed, p_term=0.05, p_trunc=0.05 if trunc else 0.0,
+                         boot=boot)
+    mask = (_rng(seed + 100).random((E, T)) < p_keep).astype(np.float32)
+    bootstrap = inp.get("last_value") if boot == "row" else inp.get("bootstrap_values")
+    return inp, mask, bootstrap
+
+
+@pytest.mark.parametrize("boot", ["none", "row", "full"])
+@pytest.mark.parametrize("trunc", [False, True])
+def test_masked_gae_all_kept_is_gae(boot, trunc):
+    if boot == "row" and trunc:
+        pytest.skip("last_value cannot be combined with truncateds")
+    inp, _, bootstrap = _masked_case(1, 9, 77, 1.0, boot, trunc)
+    ones = np.ones_like(inp["rewards"])
+    got = orc.gae_masked(inp["rewards"], inp["values"], inp["terminateds"], ones,
+                         inp["truncateds"], 0.99, 0.95, bootstrap=bootstrap)
+    ref = orc.gae(inp["rewards"], inp["values"], inp["terminateds"], inp["truncateds"], 0.99,
+                  0.95, bootstrap=bootstrap)
+    assert np.array_equal(got, ref)
+
+
+def _compressed_reference(inp, mask, bootstrap, boot, gamma, lam):
+    """Plain GAE (the pinned orc.gae) on each row's kept steps only, spread back: a kept
+    step gets its compressed advantage, a skipped one the next kept step's (0 if none)."""
+    r, v, te = (inp[k] for k in ("rewards", "values", "terminateds"))
+    tr = inp["truncateds"]
+    E, T = r.shape
+    out = np.zeros((E, T))
+    for n in range(E):
+        keep = np.flatnonzero(mask[n] != 0)
+        if keep.size == 0:
+            continue
+        sub = lambda a: a[n, keep][None, :]  # noqa: E731
+        b = None
+        if boot == "row":
+            b = bootstrap[n:n + 1]
+        elif boot == "full":
+            # the window boundary value boot(T-1) follows the last kept step, unless that
+            # step is truncated and bootstraps from its own column
+            b = sub(bootstrap).copy()
+            last = keep[-1]
+            if tr is None or tr[n, last] != 1.0:
+                b[0, -1] = bootstrap[n, T - 1]
+        a = orc.gae(sub(r), sub(v), sub(te), None if tr is None else sub(tr), gamma, lam,
+                    bootstrap=b)[0]
+        nxt = 0.0
+        j = keep.size - 1
+        for t in range(T - 1, -1, -1):
+            if j >= 0 and keep[j] == t:
+                nxt = a[j]
+                j -= 1
+            out[n, t] = nxt
+    return out
+
+
+@pytest.mark.parametrize("boot", ["none", "row", "full"])
+@pytest.mark.parametrize("trunc", [False, True])
+@pytest.mark.parametrize("p_keep", [0.0, 0.3, 0.8])
+def test_masked_gae_equals_gae_on_kept_steps(boot, trunc, p_keep):
+    if boot == "row" and trunc:
+        pytest.skip("last_value cannot be combined with truncateds")
+    inp, mask, bootstrap = _masked_case(2, 7, 61, p_keep, boot, trunc)
+    mask[0, :] = 0.0          # a row with nothing kept
+    mask[1, -5:] = 0.0        # a skipped tail: the boundary value crosses it
+    got = orc.gae_masked(inp["rewards"], inp["values"], inp["terminateds"], mask,
+                         inp["truncateds"], 0.97, 0.9, bootstrap=bootstrap)
+    ref = _compressed_reference(inp, mask, bootstrap, boot, 0.97, 0.9)
+    assert_close(got, ref, 1e-12, 1e-12, f"boot={boot} trunc={trunc} p_keep={p_keep}")
+
+
+def test_masked_gae_hand_worked():
+    """verl's loop by hand, gamma = lambda = 0.5, mask [1, 0, 0, 1, 0], no bootstrap:
+    t=4 skipped: A=0, nv=0;  t=3: delta = 2 + 0.5*0 - 0.25 = 1.75, A = 1.75, nv = 0.25;
+    t=2, t=1 skipped: A = 1.75;  t=0: delta = 1 + 0.5*0.25 - 0.5 = 0.625,
+    A = 0.625 + 0.25*1.75 = 1.0625."""
+    r = np.array([[1.0, 7.0, 7.0, 2.0, 7.0]], np.float32)
+    v = np.array([[0.5, 9.0, 9.0, 0.25, 9.0]], np.float32)
+    mask = np.array([[1.0, 0.0, 0.0, 1.0, 0.0]], np.float32)
+    got = orc.gae_masked(r, v, np.zeros_like(r), mask, None, 0.5, 0.5)
+    assert np.array_equal(got, [[1.0625, 1.75, 1.75, 1.75, 0.0]])
+    # a planted mistake -- the skipped steps' own values as the next value (plain GAE on
+    # the unmasked row, then masked) -- misses the hand-worked answer
+    plain = orc.gae(r, v, np.zeros_like(r), None, 0.5, 0.5)
+    assert not np.allclose(plain[0, 0], 1.0625)
