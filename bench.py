@@ -322,6 +322,58 @@ def time_graph_steps(torch, rl, sets, steps):
     return a.elapsed_time(b) / (reps * n)
 
 
+def time_launch_paths(torch, calls=2000):
+    """The launch-bound path (the reference's ROADMAP.md:125-130 graph item): C1 [64, 512]
+    GAE calls issued eagerly back to back (host-inclusive time per call) against the same
+    calls replayed from a captured HIP graph (device time per call)."""
+    import baseline_configs as bc
+    dev = torch.device("cuda:0")
+    name = "C1_gae_64x512"
+    c1 = [bc.make(name, seed=500 + i, device=dev) for i in range(8)]
+
+    def per_call_eager():
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(calls):
+            bc.call(name, *c1[i % len(c1)])
+        b.record()
+        torch.cuda.synchronize()
+        return 1e3 * a.elapsed_time(b) / calls
+
+    per_call_eager()  # warm
+    eager_us = per_call_eager()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for st in c1:
+            bc.call(name, *st)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    per_graph = 64
+    with torch.cuda.graph(g, stream=side):
+        for i in range(per_graph):
+            bc.call(name, *c1[i % len(c1)])
+    g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, calls // per_graph)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    graph_us = 1e3 * a.elapsed_time(b) / (reps * per_graph)
+    del g
+    log(f"[bench] C1 [64,512] GAE: eager {eager_us:.2f} us/call (host-inclusive), "
+        f"graph replay {graph_us:.2f} us/call")
+
+    del c1
+    return {"c1_gae_64x512": {"eager_us_per_call": round(eager_us, 3),
+                              "graph_us_per_call": round(graph_us, 3)}}
+
+
 def cpu_baseline(torch, cpu_sets, budget_s):
     from oracle import torch_loops
     gae, vt = cpu_sets
@@ -431,6 +483,7 @@ def main(argv=None):
     graph_ms = time_graph_steps(torch, rl_triton, sets, a.steps)
     log(f"[bench] graph-replayed step: {graph_ms * 1e3:.2f} us "
         f"({2 * E * T / (graph_ms * 1e-3) / 1e9:.1f} Gelem/s)")
+    launch_paths = time_launch_paths(torch)
     del sets
     torch.cuda.empty_cache()
 
@@ -470,6 +523,7 @@ def main(argv=None):
         "extensions": extensions,
         "graph_replay": {"ms_per_step": round(graph_ms, 6),
                          "gelem_s": round(2 * E * T / (graph_ms * 1e-3) / 1e9, 3)},
+        "launch_paths": launch_paths,
         "parity_max_abs_err": errs, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

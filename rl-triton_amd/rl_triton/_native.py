@@ -160,6 +160,15 @@ def _check(status: int, what: str) -> None:
 # ---------------------------------------------------------------------------------------
 _workspaces: dict = {}
 _ws_need: dict = {}
+# Buffers of calls captured into a HIP graph.  A captured call gets its own, allocated (and
+# zero-filled, by a kernel the graph records) inside the capture, so every replay starts
+# from a clean buffer and no replay shares one with eager calls, whatever streams they run
+# on.  Kept alive here for the life of the process (a few KB each).
+_captured: list = []
+
+
+def _capturing() -> bool:
+    return torch.cuda.is_current_stream_capturing()
 
 
 def _workspace(dev: int, stream: int, n_env: int, n_t: int):
@@ -169,6 +178,10 @@ def _workspace(dev: int, stream: int, n_env: int, n_t: int):
         need = _ws_need[key] = load().rlk_workspace_bytes(n_env, n_t)
     if need == 0:
         return None, 0
+    if _capturing():
+        ws = torch.zeros((need + 255) // 256 * 256, dtype=torch.uint8, device=torch.device("cuda", dev))
+        _captured.append(ws)
+        return ws.data_ptr(), ws.numel()
     ws = _workspaces.get((dev, stream))
     if ws is None or ws.numel() < need:
         size = max(need, 2 * ws.numel() if ws is not None else 0)
@@ -200,6 +213,10 @@ _partials: dict = {}
 
 def _partials_buffer(dev: int, stream: int, n_env: int, n_t: int):
     need = load().rlk_gae_normalized_partials_bytes(n_env, n_t)
+    if _capturing():
+        buf = torch.empty(max(need, 256), dtype=torch.uint8, device=torch.device("cuda", dev))
+        _captured.append(buf)
+        return buf.data_ptr(), buf.numel()
     buf = _partials.get((dev, stream))
     if buf is None or buf.numel() < need:
         size = max(need, 2 * buf.numel() if buf is not None else 0, 256)
