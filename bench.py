@@ -178,7 +178,7 @@ def time_configs(torch, names, min_launches=200, batch=50, dtype=None):
                      "gelem_s": round(n_env * n_t / (us * 1e-6) / 1e9, 2), "gb_s": round(gbs, 1),
                      "pct_peak": round(100 * gbs / PEAK_GBS, 2), "bytes_per_elem": bpe,
                      "target_pct": (100 * bc.TARGETS[name]) if name in bc.TARGETS else None,
-                     "traffic": measured_traffic(name) if dtype is torch.float32 else None}
+                     "traffic": measured_traffic(name if dtype is torch.float32 else name + "_bf16")}
         tag = "" if dtype is torch.float32 else " bf16"
         log(f"[bench] {name}{tag}: {us:.2f} us/launch, {gbs:.0f} GB/s ({100 * gbs / PEAK_GBS:.1f}% of 8 TB/s)")
     torch.cuda.empty_cache()
@@ -263,7 +263,8 @@ def time_extensions(torch, min_launches=200, batch=50):
         "shape": [n_env, n_t], "device_us": round(us_m, 3), "unmasked_device_us": round(us_p, 3),
         "bytes_per_elem": 28,  # the C2 inputs and the mask read, advantages written
         "gb_s": round(elems * 28 / (us_m * 1e-6) / 1e9, 1),
-        "pct_peak": round(100 * elems * 28 / (us_m * 1e-6) / 1e9 / PEAK_GBS, 2)}
+        "pct_peak": round(100 * elems * 28 / (us_m * 1e-6) / 1e9 / PEAK_GBS, 2),
+        "traffic": measured_traffic("gae_masked_4096x128")}
     log(f"[bench] gae_masked [{n_env},{n_t}]: {us_m:.2f} us/call (unmasked {us_p:.2f} us), "
         f"{elems * 28 / (us_m * 1e-6) / 1e9:.0f} GB/s")
     del sets, msets, masks
@@ -286,7 +287,8 @@ def time_extensions(torch, min_launches=200, batch=50):
     gbs = E * T * 20 / (us_l * 1e-6) / 1e9
     out["gae_masked_16x131072"] = {"shape": [E, T], "device_us": round(us_l, 3),
                                    "bytes_per_elem": 20, "gb_s": round(gbs, 1),
-                                   "pct_peak": round(100 * gbs / PEAK_GBS, 2)}
+                                   "pct_peak": round(100 * gbs / PEAK_GBS, 2),
+                                   "traffic": measured_traffic("gae_masked_16x131072")}
     log(f"[bench] gae_masked [{E},{T}]: {us_l:.2f} us/call, {gbs:.0f} GB/s")
     del lsets
     torch.cuda.empty_cache()
