@@ -9,9 +9,10 @@ namespace rlk {
 namespace {
 
 // Launch geometry.
-constexpr int kNT = 256;          // short rows: threads per workgroup (4 wavefronts)
+constexpr int kNT = 256;          // short rows up to 1024 steps: threads per workgroup (4 wavefronts)
+constexpr int kNTWide = 512;      // rows of 1025..2048 steps: one row per workgroup (8 wavefronts)
 constexpr int kShortMaxT = 2048;  // rows up to this length are kept whole in one workgroup
-static_assert(kNT >= kShortMaxT / 8, "a short row (up to 256 threads of 8 steps) fits one workgroup");
+static_assert(kNTWide >= kShortMaxT / 4, "a short row (up to 512 threads of 4 steps) fits one workgroup");
 // Long rows: each op fixes its threads per workgroup (kLongThreads) and the most 4-step
 // segments per thread its registers hold without spilling (kLongMaxSegments, 2..8).  The
 // smallest tile any op uses sizes the workspace.
@@ -62,8 +63,8 @@ bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr
 
 // Short rows: S steps per thread, L = 2^ceil(log2(ceil(T/S))) threads per row, 256/L rows
 // per workgroup, grid = ceil(E / (256/L)).
-int64_t rows_grid(int64_t E, int64_t T, int S) {
-  const int64_t rows_per_block = kNT >> ceil_log2((T + S - 1) / S);
+int64_t rows_grid(int64_t E, int64_t T, int S, int NT) {
+  const int64_t rows_per_block = NT >> ceil_log2((T + S - 1) / S);
   return (E + rows_per_block - 1) / rows_per_block;
 }
 
@@ -77,17 +78,17 @@ int64_t chain_grid(int64_t E, int64_t T, int NT, int Q) {
 template <class Op>
 int64_t launch_grid(int64_t E, int64_t T) {
   if (T > kShortMaxT) return chain_grid(E, T, Op::kLongThreads, long_segments<Op>(E, T));
-  return rows_grid(E, T, T <= 1024 ? 4 : 8);
+  return rows_grid(E, T, 4, T <= 1024 ? kNT : kNTWide);
 }
 
-template <class Op, int S, bool VEC>
+template <class Op, int NT, int S, bool VEC>
 hipError_t launch_rows(const Op& op, int64_t E, int T, hipStream_t stream) {
   int log2L = ceil_log2((T + S - 1) / S);
-  const int64_t grid = rows_grid(E, T, S);
+  const int64_t grid = rows_grid(E, T, S, NT);
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   void* args[] = {const_cast<Op*>(&op), &E, &T, &log2L};
-  return hipLaunchKernel(reinterpret_cast<const void*>(&rows_kernel<Op, kNT, S, VEC>),
-                         dim3((unsigned)grid), dim3(kNT), args, 0, stream);
+  return hipLaunchKernel(reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC>),
+                         dim3((unsigned)grid), dim3(NT), args, 0, stream);
 }
 
 // Long rows: one tile of kLongThreads * 4 * Q steps per workgroup, grid = nslots * (tiles
@@ -129,9 +130,10 @@ int launch(const Op& op, int64_t E, int64_t T, bool vec, void* workspace, size_t
       return RLK_ERR_WORKSPACE;
     e = vec ? launch_long<Op, true>(op, E, Ti, ws, s) : launch_long<Op, false>(op, E, Ti, ws, s);
   } else if (T <= 1024) {
-    e = vec ? launch_rows<Op, 4, true>(op, E, Ti, s) : launch_rows<Op, 4, false>(op, E, Ti, s);
+    e = vec ? launch_rows<Op, kNT, 4, true>(op, E, Ti, s) : launch_rows<Op, kNT, 4, false>(op, E, Ti, s);
   } else {
-    e = vec ? launch_rows<Op, 8, true>(op, E, Ti, s) : launch_rows<Op, 8, false>(op, E, Ti, s);
+    e = vec ? launch_rows<Op, kNTWide, 4, true>(op, E, Ti, s)
+            : launch_rows<Op, kNTWide, 4, false>(op, E, Ti, s);
   }
   return e == hipSuccess ? RLK_OK : RLK_ERR_LAUNCH;
 }
