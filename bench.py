@@ -212,9 +212,10 @@ def time_extensions(torch, min_launches=200, batch=50):
       * compute_gae_normalized (GAE + returns + batch-normalised advantages) at the C2 shape,
         against the composition it replaces: compute_gae, then returns = A + values, then
         (A - A.mean()) / (A.std() + 1e-8) in torch;
-      * compute_gae(..., mask=...) (skipped steps) at the C2 shape and distribution with a
-        multi-turn mask (alternating kept/skipped spans, mean length 12), and at
-        [16, 131072] (C5 shape, done ~ Bern(1e-4), last_value)."""
+      * compute_gae(..., mask=...) (skipped steps) and compute_gae_normalized(..., mask=...)
+        at the C2 shape and distribution with a multi-turn mask (alternating kept/skipped
+        spans, mean length 12), and the masked GAE at [16, 131072] (C5 shape,
+        done ~ Bern(1e-4), last_value)."""
     import baseline_configs as bc
     import rl_triton
     dev = torch.device("cuda:0")
@@ -257,6 +258,18 @@ def time_extensions(torch, min_launches=200, batch=50):
                                      inp["truncateds"], bootstrap_values=inp["bootstrap_values"],
                                      mask=inp["mask"], **params)
 
+    def masked_norm(inp, params):
+        return rl_triton.compute_gae_normalized(inp["rewards"], inp["values"], inp["terminateds"],
+                                                inp["truncateds"],
+                                                bootstrap_values=inp["bootstrap_values"],
+                                                mask=inp["mask"], **params)
+
+    us_mn = _device_us(torch, masked_norm, msets, min_launches, batch)
+    out["gae_normalized_masked_4096x128"] = {
+        "shape": [n_env, n_t], "device_us": round(us_mn, 3),
+        "bytes_per_elem": 32,  # 6 inputs read, advantages and returns written, once each
+        "gb_s": round(elems * 32 / (us_mn * 1e-6) / 1e9, 1)}
+    log(f"[bench] gae_normalized masked [{n_env},{n_t}]: {us_mn:.2f} us/call")
     us_m = _device_us(torch, masked, msets, min_launches, batch)
     us_p = _device_us(torch, lambda inp, params: bc.call(name, inp, params), sets, min_launches, batch)
     out["gae_masked_4096x128"] = {

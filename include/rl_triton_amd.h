@@ -101,7 +101,7 @@ int rlk_gae_masked(const float *rewards, const float *values, const float *termi
  * with A the advantages of rlk_gae on the same arguments, mean and std over all
  * num_envs * seq_len elements (std unbiased, as torch's Tensor.std()), computed in float64
  * in a fixed order.  Two launches: the scan writes A, the returns and one float64
- * (sum, sum of squares) pair per workgroup into `partials` (at least
+ * (count, sum, sum of squares) triple per workgroup into `partials` (at least
  * rlk_gae_normalized_partials_bytes(num_envs, seq_len) bytes, 8-byte aligned, no
  * initialisation needed); a second kernel normalises A in place.  `workspace` as for
  * rlk_gae. */
@@ -112,6 +112,19 @@ int rlk_gae_normalized(const float *rewards, const float *values, const float *t
                        float gamma, float lambda_, float eps, void *workspace,
                        size_t workspace_bytes, void *partials, size_t partials_bytes,
                        void *stream);
+
+/* rlk_gae_normalized with skipped steps (rlk_gae_masked's mask, which must not be NULL): the
+ * advantages are rlk_gae_masked's, the returns A + values at every step, and mean and std
+ * are taken over the kept steps (mask != 0) only -- the masked whitening verl applies to
+ * multi-turn advantages -- then applied to every step.  Fewer than two kept steps give nan
+ * advantages, as above.  partials sized by rlk_gae_normalized_partials_bytes. */
+int rlk_gae_normalized_masked(const float *rewards, const float *values,
+                              const float *terminateds, const float *truncateds,
+                              const float *bootstrap, int boot_mode, const float *mask,
+                              float *advantages, float *returns, int64_t num_envs,
+                              int64_t seq_len, float gamma, float lambda_, float eps,
+                              void *workspace, size_t workspace_bytes, void *partials,
+                              size_t partials_bytes, void *stream);
 
 /* V-trace targets and advantages.  Replaces vtrace_fused_kernel in compute_vtrace_fused
  * (src/rl_triton/ops/vtrace_fused.py:161-219; kernel kernels/vtrace_fused.py:7-196) and
@@ -200,6 +213,14 @@ int rlk_gae_normalized_bf16(const rlk_bf16 *rewards, const rlk_bf16 *values,
                             rlk_bf16 *returns, int64_t num_envs, int64_t seq_len, float gamma,
                             float lambda_, float eps, void *workspace, size_t workspace_bytes,
                             void *partials, size_t partials_bytes, void *stream);
+
+int rlk_gae_normalized_masked_bf16(const rlk_bf16 *rewards, const rlk_bf16 *values,
+                                   const rlk_bf16 *terminateds, const rlk_bf16 *truncateds,
+                                   const rlk_bf16 *bootstrap, int boot_mode, const rlk_bf16 *mask,
+                                   rlk_bf16 *advantages, rlk_bf16 *returns, int64_t num_envs,
+                                   int64_t seq_len, float gamma, float lambda_, float eps,
+                                   void *workspace, size_t workspace_bytes, void *partials,
+                                   size_t partials_bytes, void *stream);
 
 int rlk_vtrace_bf16(const rlk_bf16 *log_pi_target, const rlk_bf16 *log_pi_behavior,
                     const rlk_bf16 *values, const rlk_bf16 *rewards, const rlk_bf16 *terminateds,

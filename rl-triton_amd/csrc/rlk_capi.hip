@@ -206,46 +206,31 @@ int gae_masked_impl(const E* rewards, const E* values, const E* terminateds, con
   return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
 }
 
+// Partials of compute_gae_normalized: kStatWords doubles per workgroup of the first launch,
+// for the larger of the two ops' grids (the masked op uses narrower long-row tiles).
 size_t gae_normalized_partials(int64_t num_envs, int64_t seq_len) {
   if (num_envs <= 0 || seq_len <= 0) return 0;
-  // every instantiation has GaeStatsOp<true>'s geometry (the same kLong* constants)
-  return (size_t)launch_grid<GaeStatsOp<true>>(num_envs, seq_len) * 2 * sizeof(double);
+  const int64_t a = launch_grid<GaeStatsOp<true>>(num_envs, seq_len);
+  const int64_t b = launch_grid<MaskedGaeStatsOp<true>>(num_envs, seq_len);
+  return (size_t)(a > b ? a : b) * kStatWords * sizeof(double);
 }
 
-template <class E>
-int gae_normalized_impl(const E* rewards, const E* values, const E* terminateds,
-                        const E* truncateds, const E* bootstrap, int boot_mode, E* advantages,
-                        E* returns, int64_t num_envs, int64_t seq_len, float gamma, float lambda_,
-                        float eps, void* workspace, size_t workspace_bytes, void* partials,
-                        size_t partials_bytes, void* stream) {
-  if (is_empty(num_envs, seq_len)) return RLK_OK;
-  if (!rewards || !values || !terminateds || !advantages || !returns ||
-      !valid_boot(bootstrap, boot_mode))
-    return RLK_ERR_INVALID_ARGUMENT;
+// The two launches of a normalised GAE: `op` (GaeStatsOp or MaskedGaeStatsOp, partials not
+// yet set) writes A, the returns and the per-workgroup statistics; normalize_kernel then
+// rewrites A as (A - mean) / (std + eps).
+template <class StatsOp, class E>
+int normalized_launch(StatsOp op, E* advantages, int64_t num_envs, int64_t seq_len, bool vec,
+                      float eps, void* workspace, size_t workspace_bytes, void* partials,
+                      size_t partials_bytes, void* stream) {
   if (num_envs < 0 || seq_len < 0 || seq_len > (int64_t{1} << 30)) return RLK_ERR_INVALID_ARGUMENT;
   double* parts = reinterpret_cast<double*>(partials);
-  const int64_t nparts = launch_grid<GaeStatsOp<true, E>>(num_envs, seq_len);
+  const int64_t nparts = launch_grid<StatsOp>(num_envs, seq_len);
   if (parts == nullptr || (reinterpret_cast<uintptr_t>(parts) & 7u) != 0 ||
-      partials_bytes < (size_t)nparts * 2 * sizeof(double) || nparts > 0x7fffffffLL)
+      partials_bytes < (size_t)nparts * kStatWords * sizeof(double) || nparts > 0x7fffffffLL)
     return RLK_ERR_WORKSPACE;
-  const E* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
-  const bool vec = seq_len % 4 == 0 &&
-                   quad_aligned(rewards, values, terminateds, truncateds, advantages, returns) &&
-                   (boot_mode != RLK_BOOT_FULL || quad_aligned(bootstrap));
-  int st;
-  if (truncateds) {
-    GaeStatsOp<true, E> op{{rewards, values, terminateds, truncateds, boot, advantages, boot_mode,
-                            gamma, gamma * lambda_},
-                           returns, parts};
-    st = launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
-  } else {
-    GaeStatsOp<false, E> op{{rewards, values, terminateds, nullptr, boot, advantages, boot_mode,
-                             gamma, gamma * lambda_},
-                            returns, parts};
-    st = launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
-  }
+  op.partials = parts;
+  const int st = launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
   if (st != RLK_OK) return st;
-  // second launch: the statistics, then (A - mean) / (std + eps) in place
   constexpr int kNormNT = 256;
   int64_t n = num_envs * seq_len;
   int np = (int)nparts;
@@ -259,6 +244,45 @@ int gae_normalized_impl(const E* rewards, const E* values, const E* terminateds,
   const hipError_t e = hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(kNormNT), args, 0,
                                        reinterpret_cast<hipStream_t>(stream));
   return e == hipSuccess ? RLK_OK : RLK_ERR_LAUNCH;
+}
+
+// mask == nullptr: every step counts (GaeStatsOp); otherwise the masked op
+template <class E>
+int gae_normalized_impl(const E* rewards, const E* values, const E* terminateds,
+                        const E* truncateds, const E* bootstrap, int boot_mode, const E* mask,
+                        E* advantages, E* returns, int64_t num_envs, int64_t seq_len, float gamma,
+                        float lambda_, float eps, void* workspace, size_t workspace_bytes,
+                        void* partials, size_t partials_bytes, void* stream) {
+  if (is_empty(num_envs, seq_len)) return RLK_OK;
+  if (!rewards || !values || !terminateds || !advantages || !returns ||
+      !valid_boot(bootstrap, boot_mode))
+    return RLK_ERR_INVALID_ARGUMENT;
+  const E* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
+  const bool vec = seq_len % 4 == 0 &&
+                   quad_aligned(rewards, values, terminateds, truncateds, mask, advantages,
+                                returns) &&
+                   (boot_mode != RLK_BOOT_FULL || quad_aligned(bootstrap));
+  const float gl = gamma * lambda_;
+  auto run = [&](auto op) {
+    return normalized_launch(op, advantages, num_envs, seq_len, vec, eps, workspace,
+                             workspace_bytes, partials, partials_bytes, stream);
+  };
+  if (mask) {
+    if (truncateds)
+      return run(MaskedGaeStatsOp<true, E>{{rewards, values, terminateds, truncateds, boot, mask,
+                                             advantages, boot_mode, gamma, gl},
+                                            returns, nullptr});
+    return run(MaskedGaeStatsOp<false, E>{{rewards, values, terminateds, nullptr, boot, mask,
+                                            advantages, boot_mode, gamma, gl},
+                                           returns, nullptr});
+  }
+  if (truncateds)
+    return run(GaeStatsOp<true, E>{{rewards, values, terminateds, truncateds, boot, advantages,
+                                     boot_mode, gamma, gl},
+                                    returns, nullptr});
+  return run(GaeStatsOp<false, E>{{rewards, values, terminateds, nullptr, boot, advantages,
+                                    boot_mode, gamma, gl},
+                                   returns, nullptr});
 }
 
 template <class E>
@@ -472,9 +496,10 @@ int rlk_gae_normalized(const float* rewards, const float* values, const float* t
                        float gamma, float lambda_, float eps, void* workspace,
                        size_t workspace_bytes, void* partials, size_t partials_bytes,
                        void* stream) {
-  return gae_normalized_impl(rewards, values, terminateds, truncateds, bootstrap, boot_mode,
-                             advantages, returns, num_envs, seq_len, gamma, lambda_, eps,
-                             workspace, workspace_bytes, partials, partials_bytes, stream);
+  return gae_normalized_impl<float>(rewards, values, terminateds, truncateds, bootstrap,
+                                    boot_mode, nullptr, advantages, returns, num_envs, seq_len,
+                                    gamma, lambda_, eps, workspace, workspace_bytes, partials,
+                                    partials_bytes, stream);
 }
 
 int rlk_gae_normalized_bf16(const rlk_bf16* rewards, const rlk_bf16* values,
@@ -483,10 +508,38 @@ int rlk_gae_normalized_bf16(const rlk_bf16* rewards, const rlk_bf16* values,
                             rlk_bf16* returns, int64_t num_envs, int64_t seq_len, float gamma,
                             float lambda_, float eps, void* workspace, size_t workspace_bytes,
                             void* partials, size_t partials_bytes, void* stream) {
-  return gae_normalized_impl(B(rewards), B(values), B(terminateds), B(truncateds), B(bootstrap),
-                             boot_mode, B(advantages), B(returns), num_envs, seq_len, gamma,
-                             lambda_, eps, workspace, workspace_bytes, partials, partials_bytes,
-                             stream);
+  return gae_normalized_impl<bf16>(B(rewards), B(values), B(terminateds), B(truncateds),
+                                   B(bootstrap), boot_mode, nullptr, B(advantages), B(returns),
+                                   num_envs, seq_len, gamma, lambda_, eps, workspace,
+                                   workspace_bytes, partials, partials_bytes, stream);
+}
+
+int rlk_gae_normalized_masked(const float* rewards, const float* values,
+                              const float* terminateds, const float* truncateds,
+                              const float* bootstrap, int boot_mode, const float* mask,
+                              float* advantages, float* returns, int64_t num_envs,
+                              int64_t seq_len, float gamma, float lambda_, float eps,
+                              void* workspace, size_t workspace_bytes, void* partials,
+                              size_t partials_bytes, void* stream) {
+  if (!is_empty(num_envs, seq_len) && !mask) return RLK_ERR_INVALID_ARGUMENT;
+  return gae_normalized_impl<float>(rewards, values, terminateds, truncateds, bootstrap,
+                                    boot_mode, mask, advantages, returns, num_envs, seq_len,
+                                    gamma, lambda_, eps, workspace, workspace_bytes, partials,
+                                    partials_bytes, stream);
+}
+
+int rlk_gae_normalized_masked_bf16(const rlk_bf16* rewards, const rlk_bf16* values,
+                                   const rlk_bf16* terminateds, const rlk_bf16* truncateds,
+                                   const rlk_bf16* bootstrap, int boot_mode, const rlk_bf16* mask,
+                                   rlk_bf16* advantages, rlk_bf16* returns, int64_t num_envs,
+                                   int64_t seq_len, float gamma, float lambda_, float eps,
+                                   void* workspace, size_t workspace_bytes, void* partials,
+                                   size_t partials_bytes, void* stream) {
+  if (!is_empty(num_envs, seq_len) && !mask) return RLK_ERR_INVALID_ARGUMENT;
+  return gae_normalized_impl<bf16>(B(rewards), B(values), B(terminateds), B(truncateds),
+                                   B(bootstrap), boot_mode, B(mask), B(advantages), B(returns),
+                                   num_envs, seq_len, gamma, lambda_, eps, workspace,
+                                   workspace_bytes, partials, partials_bytes, stream);
 }
 
 int rlk_vtrace(const float* log_pi_target, const float* log_pi_behavior, const float* values,

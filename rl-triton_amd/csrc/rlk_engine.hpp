@@ -375,63 +375,65 @@ __device__ __forceinline__ void replay(const M (&steps)[S], typename M::State x_
 }
 
 // ---------------------------------------------------------------------------------------
-// Per-workgroup output statistics (ops with kBlockStats): float64 sum and sum of squares of
-// the valid outputs, reduced in a fixed order (lanes by a fixed butterfly, waves in index
-// order), so the partial a workgroup writes is the same bit pattern on every run.
+// Per-workgroup output statistics (ops with kBlockStats): float64 count, sum and sum of
+// squares of the outputs the op counts (op.stats()), reduced in a fixed order (lanes by a
+// fixed butterfly, waves in index order), so the partial a workgroup writes is the same bit
+// pattern on every run.  kStatWords doubles per workgroup.
 // ---------------------------------------------------------------------------------------
-template <int S>
-__device__ __forceinline__ void accumulate_stats(const float (&xs)[S], int t0, int T, bool ok,
-                                                 double& sum, double& sq) {
-#pragma unroll
-  for (int i = 0; i < S; ++i) {
-    const double x = (ok && t0 + i < T) ? (double)xs[i] : 0.0;
+constexpr int kStatWords = 3;
+
+struct Stats {
+  double n = 0.0, sum = 0.0, sq = 0.0;
+  __device__ void add(float v) {
+    const double x = (double)v;
+    n += 1.0;
     sum += x;
     sq = fma(x, x, sq);
   }
-}
+};
 
-// Every thread of the workgroup calls this once; thread 0 writes partials[2*blockIdx.x + {0,1}].
+// Every thread of the workgroup calls this once; thread 0 writes
+// partials[kStatWords*blockIdx.x + {0,1,2}] = {n, sum, sum of squares}.
 template <int NT>
-__device__ __forceinline__ void block_stats(double sum, double sq, double* __restrict__ partials) {
+__device__ __forceinline__ void block_stats(Stats st, double* __restrict__ partials) {
   constexpr int NW = NT / kWave;
-  __shared__ double s_sum[NW], s_sq[NW];
+  __shared__ double s_st[kStatWords][NW];
 #pragma unroll
   for (int off = kWave / 2; off >= 1; off >>= 1) {
-    sum += __shfl_xor(sum, off, kWave);
-    sq += __shfl_xor(sq, off, kWave);
+    st.n += __shfl_xor(st.n, off, kWave);
+    st.sum += __shfl_xor(st.sum, off, kWave);
+    st.sq += __shfl_xor(st.sq, off, kWave);
   }
   const int wave = threadIdx.x / kWave;
   if (__lane_id() == 0) {
-    s_sum[wave] = sum;
-    s_sq[wave] = sq;
+    s_st[0][wave] = st.n;
+    s_st[1][wave] = st.sum;
+    s_st[2][wave] = st.sq;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    double a = 0.0, b = 0.0;
-    for (int w = 0; w < NW; ++w) {
-      a += s_sum[w];
-      b += s_sq[w];
-    }
-    partials[2 * blockIdx.x] = a;
-    partials[2 * blockIdx.x + 1] = b;
+  if (threadIdx.x < kStatWords) {
+    double a = 0.0;
+    for (int w = 0; w < NW; ++w) a += s_st[threadIdx.x][w];
+    partials[kStatWords * blockIdx.x + threadIdx.x] = a;
   }
 }
 
 // Second launch of the normalisation: every workgroup combines the per-workgroup partials
 // of the first launch in one fixed order (thread i sums partials i, i+NT, ...; a fixed lane
 // butterfly; the waves in index order), so all agree on the statistics, then rewrites its
-// share of x as
-// (x - mean) / (std + eps), std unbiased (n - 1), as torch computes x.std().
+// share of the n_all elements of x as (x - mean) / (std + eps): mean and std (unbiased,
+// count - 1, as torch computes x.std()) over the elements the first launch counted, which
+// are all of them, or the kept steps of a masked call.
 template <int NT, bool VEC, class E>
 __global__ __launch_bounds__(NT) void normalize_kernel(E* __restrict__ x,
                                                        const double* __restrict__ partials,
-                                                       int nparts, int64_t n, float eps) {
+                                                       int nparts, int64_t n_all, float eps) {
   constexpr int NW = NT / kWave;
-  __shared__ double s_a[NW], s_b[NW];
+  __shared__ double s_st[kStatWords][NW];
   const int tid = threadIdx.x;
   const int64_t stride = (int64_t)gridDim.x * NT;
   const int64_t first = (int64_t)blockIdx.x * NT + tid;
-  const int64_t units = VEC ? n / 4 : n;
+  const int64_t units = VEC ? n_all / 4 : n_all;
   // this thread's first element is loaded before the statistics, so the two round trips
   // overlap
   float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -439,30 +441,31 @@ __global__ __launch_bounds__(NT) void normalize_kernel(E* __restrict__ x,
     if constexpr (VEC) v0 = load_quad<true>(x + 4 * first);
     else v0.x = load_one_nt(x + first);
   }
-  double a = 0.0, b = 0.0;
+  double acc[kStatWords] = {0.0, 0.0, 0.0};
   for (int i = tid; i < nparts; i += NT) {
-    a += partials[2 * i];
-    b += partials[2 * i + 1];
+#pragma unroll
+    for (int k = 0; k < kStatWords; ++k) acc[k] += partials[kStatWords * i + k];
   }
 #pragma unroll
   for (int off = kWave / 2; off >= 1; off >>= 1) {
-    a += __shfl_xor(a, off, kWave);
-    b += __shfl_xor(b, off, kWave);
+#pragma unroll
+    for (int k = 0; k < kStatWords; ++k) acc[k] += __shfl_xor(acc[k], off, kWave);
   }
   if (__lane_id() == 0) {
-    s_a[tid / kWave] = a;
-    s_b[tid / kWave] = b;
+#pragma unroll
+    for (int k = 0; k < kStatWords; ++k) s_st[k][tid / kWave] = acc[k];
   }
   __syncthreads();
-  double sum = 0.0, sq = 0.0;
+  double n = 0.0, sum = 0.0, sq = 0.0;
   for (int w = 0; w < NW; ++w) {
-    sum += s_a[w];
-    sq += s_b[w];
+    n += s_st[0][w];
+    sum += s_st[1][w];
+    sq += s_st[2][w];
   }
-  const double mean = sum / (double)n;
-  double var = (sq - sum * mean) / (double)(n - 1);
+  const double mean = sum / n;  // nan when nothing was counted
+  double var = (sq - sum * mean) / (n - 1.0);
   var = var > 0.0 ? var : 0.0;
-  if (n < 2) var = __builtin_nan("");  // torch: the unbiased std of one element is nan
+  if (!(n >= 2.0)) var = __builtin_nan("");  // torch: the unbiased std of one element is nan
   const float m = (float)mean;
   const float d = (float)sqrt(var) + eps;
   if constexpr (VEC) {
@@ -611,9 +614,9 @@ __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T,
   replay<FWD, S>(steps, x_in, xs);
   if (active) op.template emit<S, VEC>(R, h, xs, x_in, row, t0, T);
   if constexpr (Op::kBlockStats) {
-    double sum = 0.0, sq = 0.0;
-    accumulate_stats<S>(xs, t0, T, active, sum, sq);
-    block_stats<NT>(sum, sq, op.partials);
+    Stats st;
+    if (active) op.template stats<S>(R, xs, t0, T, st);
+    block_stats<NT>(st, op.partials);
   }
 }
 
@@ -799,7 +802,7 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
     drawn = __hip_atomic_fetch_add(sc + 16, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
-  double st_sum = 0.0, st_sq = 0.0;  // output statistics (ops with kBlockStats)
+  Stats st;  // output statistics (ops with kBlockStats)
   if (q_t < tiles_in_slot) {
     const int64_t lr = (int64_t)(q_t / (uint64_t)tiles_per_row);
     const int j = (int)(q_t - (uint64_t)lr * tiles_per_row);
@@ -870,10 +873,10 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
       State xs[kSeg];
       replay<FWD, kSeg>(steps[r], x_in, xs);
       op.template emit<kSeg, VEC>(R[r], h[r], xs, x_in, row, seg_t0(r), T);
-      if constexpr (Op::kBlockStats) accumulate_stats<kSeg>(xs, seg_t0(r), T, true, st_sum, st_sq);
+      if constexpr (Op::kBlockStats) op.template stats<kSeg>(R[r], xs, seg_t0(r), T, st);
     }
   }
-  if constexpr (Op::kBlockStats) block_stats<NT>(st_sum, st_sq, op.partials);
+  if constexpr (Op::kBlockStats) block_stats<NT>(st, op.partials);
   if (tid == 0 && drawn == wgs_per_slot - 1) {
     atomic_st(sc + 0, 0);
     atomic_st(sc + 16, 0);

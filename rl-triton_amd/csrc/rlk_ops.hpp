@@ -95,8 +95,8 @@ struct GaeOp {
 // GAE with returns and batch statistics: the first half of compute_gae_normalized (no
 // counterpart in the reference, which has none of this; it is the "fused GAE + advantage
 // normalisation" item of its ROADMAP.md:75-81).  The scan is GaeOp's; the epilogue writes
-// the raw advantages A and the returns A + values, and each workgroup reduces the sum and
-// the sum of squares of its A in float64 into partials[2*blockIdx.x .. +1] (see
+// the raw advantages A and the returns A + values, and each workgroup reduces the count,
+// sum and sum of squares of its A in float64 into partials[3*blockIdx.x .. +2] (see
 // block_stats in rlk_engine.hpp).  normalize_kernel then turns A into
 // (A - mean) / (std + eps) in place.
 // ------------------------------------------------------------------------------------------
@@ -117,6 +117,13 @@ struct GaeStatsOp : GaeOp<TRUNC, E> {
     const int64_t o = row * (int64_t)T;
     store_seg<S, VEC>(this->out + o, t0, T, xs);
     store_seg<S, VEC>(returns + o, t0, T, rt);
+  }
+  // every step of the row counts
+  template <int S>
+  __device__ void stats(const Regs<S>&, const float (&xs)[S], int t0, int T, Stats& st) const {
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+      if (t0 + i < T) st.add(xs[i]);
   }
 };
 
@@ -203,6 +210,41 @@ struct MaskedGaeOp {
 #pragma unroll
     for (int i = 0; i < S; ++i) a[i] = xs[i].x;
     store_seg<S, VEC>(out + row * (int64_t)T, t0, T, a);
+  }
+};
+
+// ------------------------------------------------------------------------------------------
+// Masked GAE with returns and statistics over the kept steps: the first half of
+// compute_gae_normalized(..., mask=...), the masked whitening verl applies after its
+// compute_gae_advantage_return.  Returns are A + values at every step; count, sum and sum of
+// squares are of the kept steps only, and normalize_kernel rewrites every step's A.
+// ------------------------------------------------------------------------------------------
+template <bool TRUNC, class E = float>
+struct MaskedGaeStatsOp : MaskedGaeOp<TRUNC, E> {
+  static constexpr bool kBlockStats = true;
+  E* returns;
+  double* partials;
+  template <int S>
+  using Regs = typename MaskedGaeOp<TRUNC, E>::template Regs<S>;
+
+  template <int S, bool VEC>
+  __device__ void emit(const Regs<S>& R, NoHalo, const NvX (&xs)[S], NvX, int64_t row, int t0,
+                       int T) const {
+    float a[S], rt[S];
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      a[i] = xs[i].x;
+      rt[i] = xs[i].x + R.v[i];
+    }
+    const int64_t o = row * (int64_t)T;
+    store_seg<S, VEC>(this->out + o, t0, T, a);
+    store_seg<S, VEC>(returns + o, t0, T, rt);
+  }
+  template <int S>
+  __device__ void stats(const Regs<S>& R, const NvX (&xs)[S], int t0, int T, Stats& st) const {
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+      if (t0 + i < T && R.mk[i] != 0.f) st.add(xs[i].x);
   }
 };
 

@@ -182,9 +182,9 @@ PyObject* op_gae(PyObject* const* a, Py_ssize_t n) {
 }
 
 // gae_normalized(rewards, values, terminateds, truncateds, gamma, lambda_, bootstrap_values,
-//                last_value, eps) -> (advantages, returns)
+//                last_value, eps, mask) -> (advantages, returns)
 PyObject* op_gae_normalized(PyObject* const* a, Py_ssize_t n) {
-  if (!nargs_is(n, 9, "gae_normalized")) return nullptr;
+  if (!nargs_is(n, 10, "gae_normalized")) return nullptr;
   if (correctness_warnings()) return decline();
   Call c;
   const at::Tensor* r = c.lead(a[0]);
@@ -196,6 +196,7 @@ PyObject* op_gae_normalized(PyObject* const* a, Py_ssize_t n) {
   if (has_bv && has_lv) return decline();
   if (has_lv && tr) return decline();
   const at::Tensor* boot = has_lv ? c.need(a[7], 1) : c.opt(a[6]);
+  const at::Tensor* mask = c.opt(a[9]);
   if (!c.ok) return decline();
   const int mode = has_lv ? RLK_BOOT_ROW : has_bv ? RLK_BOOT_FULL : RLK_BOOT_NONE;
   at::Tensor adv = c.output(*r), ret = c.output(*r);
@@ -203,11 +204,16 @@ PyObject* op_gae_normalized(PyObject* const* a, Py_ssize_t n) {
   at::Tensor parts = at::empty({(int64_t)(pb > 0 ? pb : 8)}, r->options().dtype(at::kByte));
   const int st = dispatch(c, [&](auto z) {
     using T = decltype(z);
+    if (mask)
+      return pick<T>(rlk_gae_normalized_masked, rlk_gae_normalized_masked_bf16)(
+        in_ptr<T>(r), in_ptr<T>(v), in_ptr<T>(te), in_ptr<T>(tr), in_ptr<T>(boot), mode,
+        in_ptr<T>(mask), out_ptr<T>(adv), out_ptr<T>(ret), c.E, c.T, gamma, lam, eps, nullptr, 0,
+        parts.data_ptr(), pb, c.stream());
     return pick<T>(rlk_gae_normalized, rlk_gae_normalized_bf16)(in_ptr<T>(r), in_ptr<T>(v),
-      in_ptr<T>(te), in_ptr<T>(tr), in_ptr<T>(boot), mode, out_ptr<T>(adv), out_ptr<T>(ret), c.E,
-      c.T, gamma, lam, eps, nullptr, 0, parts.data_ptr(), pb, c.stream());
+      in_ptr<T>(te), in_ptr<T>(tr), in_ptr<T>(boot), mode, out_ptr<T>(adv), out_ptr<T>(ret),
+      c.E, c.T, gamma, lam, eps, nullptr, 0, parts.data_ptr(), pb, c.stream());
   });
-  return finish(st, "rlk_gae_normalized", pair(adv, ret));
+  return finish(st, mask ? "rlk_gae_normalized_masked" : "rlk_gae_normalized", pair(adv, ret));
 }
 
 // vtrace(log_pi_target, log_pi_behavior, values, rewards, terminateds, truncateds, gamma,

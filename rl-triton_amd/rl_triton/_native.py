@@ -36,6 +36,8 @@ SIGNATURES = {
     "rlk_gae_masked": [_P, _P, _P, _P, _P, _INT, _P, _P, _I64, _I64, _F, _F, _P, _SZ, _P],
     "rlk_gae_normalized": [_P, _P, _P, _P, _P, _INT, _P, _P, _I64, _I64, _F, _F, _F, _P, _SZ, _P,
                            _SZ, _P],
+    "rlk_gae_normalized_masked": [_P, _P, _P, _P, _P, _INT, _P, _P, _P, _I64, _I64, _F, _F, _F, _P,
+                                  _SZ, _P, _SZ, _P],
     "rlk_gae_normalized_partials_bytes": [_I64, _I64],
     "rlk_vtrace": [_P, _P, _P, _P, _P, _P, _P, _INT, _P, _P, _I64, _I64, _F, _F, _F, _P, _SZ, _P],
     "rlk_retrace": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _F, _F, _F, _P,
@@ -50,7 +52,7 @@ SIGNATURES = {
     "rlk_version": [],
 }
 # the bfloat16 twins take the same arguments (rlk_bf16 arrays in place of float ones)
-for _name in ("rlk_gae", "rlk_gae_masked", "rlk_gae_normalized", "rlk_vtrace", "rlk_retrace", "rlk_lambda_returns",
+for _name in ("rlk_gae", "rlk_gae_masked", "rlk_gae_normalized", "rlk_gae_normalized_masked", "rlk_vtrace", "rlk_retrace", "rlk_lambda_returns",
               "rlk_discounted_returns", "rlk_eligibility_traces", "rlk_prefix_sum",
               "rlk_affine_scan"):
     SIGNATURES[_name + "_bf16"] = SIGNATURES[_name]
@@ -280,27 +282,31 @@ def gae_masked(rewards, values, terminateds, truncateds, bootstrap, mask, out, g
 
 
 def gae_normalized(rewards, values, terminateds, truncateds, bootstrap, advantages, returns, gamma,
-                   lambda_, eps):
+                   lambda_, eps, mask=None):
     dev = _device_of(rewards)
     shape = rewards.shape
     dt = rewards.dtype
     n_env, n_t = shape
     lib = _lib or load()
     bp, mode = _boot_args(bootstrap, n_env, n_t, dev, dt)
-    args = (_ptr(rewards, "rewards", shape, dev, dt), _ptr(values, "values", shape, dev, dt),
-            _ptr(terminateds, "terminateds", shape, dev, dt), _opt(truncateds, "truncateds", shape, dev, dt),
-            bp, mode, _ptr(advantages, "advantages", shape, dev, dt), _ptr(returns, "returns", shape, dev, dt),
-            n_env, n_t, gamma, lambda_, eps)
+    head = (_ptr(rewards, "rewards", shape, dev, dt), _ptr(values, "values", shape, dev, dt),
+            _ptr(terminateds, "terminateds", shape, dev, dt),
+            _opt(truncateds, "truncateds", shape, dev, dt), bp, mode)
+    if mask is not None:
+        head = head + (_ptr(mask, "mask", shape, dev, dt),)
+    args = head + (_ptr(advantages, "advantages", shape, dev, dt),
+                   _ptr(returns, "returns", shape, dev, dt), n_env, n_t, gamma, lambda_, eps)
     if dev != _cur_device():
         with torch.cuda.device(dev):
             return gae_normalized(rewards, values, terminateds, truncateds, bootstrap, advantages,
-                                  returns, gamma, lambda_, eps)
+                                  returns, gamma, lambda_, eps, mask)
     stream = _raw_stream(dev)
     ws, wsb = _workspace(dev, stream, n_env, n_t)
     pp, ppb = _partials_buffer(dev, stream, n_env, n_t) if n_env * n_t > 0 else (None, 0)
-    status = _entry(lib, "rlk_gae_normalized", dt)(*args, ws, wsb, pp, ppb, stream)
+    name = "rlk_gae_normalized" if mask is None else "rlk_gae_normalized_masked"
+    status = _entry(lib, name, dt)(*args, ws, wsb, pp, ppb, stream)
     if status != 0:
-        _check(status, "rlk_gae_normalized")
+        _check(status, name)
     return advantages, returns
 
 

@@ -29,6 +29,8 @@ def compute_gae_normalized(
     bootstrap_values: torch.Tensor | None = None,
     last_value: torch.Tensor | None = None,
     eps: float = 1e-8,
+    *,
+    mask: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """
     Normalised GAE advantages and returns.
@@ -36,20 +38,25 @@ def compute_gae_normalized(
     Arguments, checks and the advantage recurrence are those of compute_gae (the same
     AssertionErrors, in the same order).
 
+    `mask` (keyword-only): A is compute_gae(..., mask=mask) and mean and std are taken over
+    the kept steps (mask != 0) only, then applied to every step -- the masked whitening verl
+    applies after compute_gae_advantage_return (with its response_mask).
+
     Returns:
         advantages: (A - mean(A)) / (std(A) + eps), A = compute_gae(...), mean and std over
-                    all num_envs * seq_len elements, [num_envs, seq_len], float32.
-        returns:    A + values, [num_envs, seq_len], float32.
+                    all num_envs * seq_len elements (the kept ones with a mask),
+                    [num_envs, seq_len], the inputs' dtype.
+        returns:    A + values, [num_envs, seq_len], the inputs' dtype.
     """
     # fast path: a well-formed call goes straight to the C ABI (rl_triton._rlk_torch)
     fast = _native.fast
     if fast is not None:
         res = fast.gae_normalized(rewards, values, terminateds, truncateds, gamma, lambda_,
-                                  bootstrap_values, last_value, eps)
+                                  bootstrap_values, last_value, eps, mask)
         if res is not None:
             return res
 
-    _check_gae_args(rewards, values, terminateds, truncateds, bootstrap_values, last_value)
+    _check_gae_args(rewards, values, terminateds, truncateds, bootstrap_values, last_value, mask)
     rewards = rewards.contiguous()
     values = values.contiguous()
     terminateds = terminateds.contiguous()
@@ -64,4 +71,5 @@ def compute_gae_normalized(
     advantages = torch.empty_like(rewards)
     returns = torch.empty_like(rewards)
     return _native.gae_normalized(rewards, values, terminateds, truncateds, bootstrap, advantages,
-                                  returns, gamma, lambda_, eps)
+                                  returns, gamma, lambda_, eps,
+                                  None if mask is None else mask.contiguous())

@@ -32,16 +32,20 @@ OUTPUTS = {
     "discounted_returns": ("returns",), "eligibility_traces": ("traces",),
     "prefix_sum": ("prefix_sums",), "backward_scan": ("out",), "forward_scan": ("out",),
     "gae_normalized": ("advantages", "returns"), "gae_masked": ("advantages",),
+    "gae_normalized_masked": ("advantages", "returns"),
 }
 
 
-def normalized_from_oracle(adv, values, eps):
+def normalized_from_oracle(adv, values, eps, mask=None):
     """The float64 composition compute_gae_normalized fuses: returns = A + values and
-    (A - mean) / (std + eps), std unbiased -- numpy's ddof=1, torch's Tensor.std()."""
+    (A - mean) / (std + eps), std unbiased -- numpy's ddof=1, torch's Tensor.std().  With a
+    mask, mean and std are over the kept steps (mask != 0) and applied to every step."""
     a = np.asarray(adv, dtype=np.float64)
     ret = a + np.asarray(values, dtype=np.float64)
-    std = a.std(ddof=1) if a.size > 1 else np.nan
-    return (a - a.mean()) / (std + eps), ret
+    kept = a if mask is None else a[np.asarray(mask) != 0]
+    mean = kept.mean() if kept.size else np.nan
+    std = kept.std(ddof=1) if kept.size > 1 else np.nan
+    return (a - mean) / (std + eps), ret
 
 
 def run_oracle(op, inp, params):
@@ -54,6 +58,13 @@ def run_oracle(op, inp, params):
         boot = g("last_value") if g("last_value") is not None else g("bootstrap_values")
         return (orc.gae_masked(g("rewards"), g("values"), g("terminateds"), g("mask"),
                                g("truncateds"), bootstrap=boot, **params),)
+    if op == "gae_normalized_masked":
+        boot = g("last_value") if g("last_value") is not None else g("bootstrap_values")
+        p = dict(params)
+        eps = p.pop("eps", 1e-8)
+        adv = orc.gae_masked(g("rewards"), g("values"), g("terminateds"), g("mask"),
+                             g("truncateds"), bootstrap=boot, **p)
+        return normalized_from_oracle(adv, g("values"), eps, g("mask"))
     if op == "gae_normalized":
         boot = g("last_value") if g("last_value") is not None else g("bootstrap_values")
         p = dict(params)
@@ -114,6 +125,12 @@ def run_api(op, inp, params, device, dtype=torch.float32):
         return (rl_triton.compute_gae(g("rewards"), g("values"), g("terminateds"), g("truncateds"),
                                       bootstrap_values=g("bootstrap_values"),
                                       last_value=g("last_value"), mask=g("mask"), **params),)
+    if op == "gae_normalized_masked":
+        return rl_triton.compute_gae_normalized(g("rewards"), g("values"), g("terminateds"),
+                                                g("truncateds"),
+                                                bootstrap_values=g("bootstrap_values"),
+                                                last_value=g("last_value"), mask=g("mask"),
+                                                **params)
     if op == "gae_normalized":
         return rl_triton.compute_gae_normalized(g("rewards"), g("values"), g("terminateds"),
                                                 g("truncateds"),
@@ -172,8 +189,8 @@ def make_inputs(op, n_env, n_t, seed=0, p_term=0.05, p_trunc=0.0, boot="none", n
     if p_trunc > 0:
         trunc = (ru(*shape) < p_trunc).float() * (1.0 - term)
     inp = {}
-    if op in ("gae", "gae_normalized", "gae_masked", "vtrace", "lambda_returns",
-              "discounted_returns"):
+    if op in ("gae", "gae_normalized", "gae_masked", "gae_normalized_masked", "vtrace",
+              "lambda_returns", "discounted_returns"):
         if boot == "row":
             inp["last_value"] = rn(n_env)
         elif boot == "full":
@@ -182,10 +199,10 @@ def make_inputs(op, n_env, n_t, seed=0, p_term=0.05, p_trunc=0.0, boot="none", n
                 bv = torch.where(trunc.bool(), rn(*shape), bv)
             bv[:, -1] = rn(n_env)
             inp["bootstrap_values"] = bv
-    if op in ("gae", "gae_normalized", "gae_masked"):
+    if op in ("gae", "gae_normalized", "gae_masked", "gae_normalized_masked"):
         inp.update(rewards=rn(*shape), values=rn(*shape), terminateds=term, truncateds=trunc)
         params = {"gamma": 0.99, "lambda_": 0.95}
-        if op == "gae_masked":
+        if op in ("gae_masked", "gae_normalized_masked"):
             inp["mask"] = span_mask(n_env, n_t, g)
     elif op == "vtrace":
         inp.update(log_pi_target=-ru(*shape), log_pi_behavior=-ru(*shape), values=rn(*shape),

@@ -15,13 +15,13 @@ from _common import make_inputs, run_api, to_device
 
 pytestmark = pytest.mark.gpu
 
-OPS = ["gae", "gae_masked", "gae_normalized", "vtrace", "retrace", "lambda_returns",
+OPS = ["gae", "gae_masked", "gae_normalized", "gae_normalized_masked", "vtrace", "retrace", "lambda_returns",
        "discounted_returns", "eligibility_traces", "prefix_sum", "backward_scan", "forward_scan"]
 
 
 def _inputs(op, shape, seed):
-    boot = ("full" if op in ("gae", "gae_masked", "gae_normalized", "vtrace", "lambda_returns",
-                             "discounted_returns") else "row")
+    boot = ("full" if op in ("gae", "gae_masked", "gae_normalized", "gae_normalized_masked",
+                             "vtrace", "lambda_returns", "discounted_returns") else "row")
     return make_inputs(op, *shape, seed=seed, p_trunc=0.02 if op != "retrace" else 0.0, boot=boot)
 
 
@@ -38,11 +38,12 @@ def _call(op, d, params):
         return (rl_triton.compute_gae(g("rewards"), g("values"), g("terminateds"), g("truncateds"),
                                       bootstrap_values=g("bootstrap_values"),
                                       last_value=g("last_value"), mask=g("mask"), **params),)
-    if op == "gae_normalized":
+    if op in ("gae_normalized", "gae_normalized_masked"):
         return rl_triton.compute_gae_normalized(g("rewards"), g("values"), g("terminateds"),
                                                 g("truncateds"),
                                                 bootstrap_values=g("bootstrap_values"),
-                                                last_value=g("last_value"), **params)
+                                                last_value=g("last_value"), mask=g("mask"),
+                                                **params)
     if op == "vtrace":
         return rl_triton.compute_vtrace(g("log_pi_target"), g("log_pi_behavior"), g("values"),
                                         g("rewards"), g("terminateds"), g("truncateds"),

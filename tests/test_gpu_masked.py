@@ -90,3 +90,55 @@ def test_masked_gae_repeatable(device):
     a = run_api("gae_masked", inp, params, device)[0]
     b = run_api("gae_masked", inp, params, device)[0]
     assert torch.equal(a, b)
+
+
+# ---------------------------------------------------------------------------------------
+# compute_gae_normalized(..., mask=...): statistics over the kept steps (verl's masked
+# whitening), against the float64 composition of the masked GAE oracle
+# (tests/_common.normalized_from_oracle with the mask)
+# ---------------------------------------------------------------------------------------
+def _check_normalized_masked(inp, params, device, what):
+    got = run_api("gae_normalized_masked", inp, params, device)
+    adv_exp, ret_exp = run_oracle("gae_normalized_masked", inp, params)
+    raw = run_oracle("gae_masked", inp, {k: v for k, v in params.items() if k != "eps"})[0]
+    kept = raw[np.asarray(inp["mask"]) != 0]
+    std = float(np.std(kept, ddof=1))
+    T = raw.shape[1]
+    base = 1e-5 * max(1.0, float(np.max(np.abs(raw))))
+    if T > 2048:
+        base *= math.sqrt(max(1.0 / (1.0 - 0.99 * 0.95), 128) / 128.0)
+    scale = max(1.0, float(np.max(np.abs(ret_exp))))
+    assert_close(got[1].cpu().numpy(), ret_exp, 1e-5, base + 1e-6 * scale, f"{what}:returns")
+    assert_close(got[0].cpu().numpy(), adv_exp, 1e-5, base / min(std, 1.0) + 1e-6,
+                 f"{what}:advantages")
+    return got
+
+
+@pytest.mark.parametrize("boot", ["none", "row", "full"])
+@pytest.mark.parametrize("shape", [(4, 128), (33, 257), (16, 2048), (3, 5000), (2, 40000)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_masked_gae_normalized_parity(shape, boot, device):
+    trunc = 0.0 if boot == "row" else 0.03
+    inp, params = make_inputs("gae_normalized_masked", *shape, seed=15, p_trunc=trunc, boot=boot)
+    params = dict(params, eps=1e-8)
+    _check_normalized_masked(inp, params, device, f"normalized masked {shape} boot={boot}")
+
+
+def test_masked_gae_normalized_statistics_are_over_kept_steps(device):
+    """C2 shape with a span mask: the kept steps come out with mean 0 and std 1, the skipped
+    ones are normalised with the same statistics; an all-ones mask reproduces the unmasked
+    call."""
+    inp, params = make_inputs("gae_normalized_masked", 4096, 128, seed=16, p_trunc=0.005,
+                              boot="full")
+    params = dict(params, eps=1e-8)
+    adv, ret = _check_normalized_masked(inp, params, device, "C2 masked normalized")
+    kept = torch.as_tensor(inp["mask"], device=device) != 0
+    a = adv.double()[kept]
+    assert abs(float(a.mean())) < 1e-6 and abs(float(a.std()) - 1.0) < 1e-5
+    ones = dict(inp, mask=np.ones_like(inp["mask"]))
+    m_adv, m_ret = run_api("gae_normalized_masked", ones, params, device)
+    u_adv, u_ret = run_api("gae_normalized", {k: v for k, v in inp.items() if k != "mask"},
+                           params, device)
+    scale = max(1.0, float(u_ret.abs().max()))
+    torch.testing.assert_close(m_ret, u_ret, rtol=1e-5, atol=1e-5 * scale)
+    torch.testing.assert_close(m_adv, u_adv, rtol=1e-5, atol=1e-5 * scale)

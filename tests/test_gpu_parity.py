@@ -272,9 +272,9 @@ def test_max_abs_error_report(device):
 # ---------------------------------------------------------------------------------------
 # the tensor-level fast path (rl_triton._rlk_torch) against the general Python path
 # ---------------------------------------------------------------------------------------
-FAST_OPS = ["gae", "gae_masked", "gae_normalized", "vtrace", "retrace", "lambda_returns",
-            "discounted_returns", "eligibility_traces", "prefix_sum", "backward_scan",
-            "forward_scan"]
+FAST_OPS = ["gae", "gae_masked", "gae_normalized", "gae_normalized_masked", "vtrace", "retrace",
+            "lambda_returns", "discounted_returns", "eligibility_traces", "prefix_sum",
+            "backward_scan", "forward_scan"]
 
 
 @pytest.mark.parametrize("op", FAST_OPS)
@@ -286,8 +286,8 @@ def test_fast_path_matches_python_path(op, shape, device, monkeypatch):
     the results are bit-identical."""
     from rl_triton import _native
     assert _native.fast is not None, "rl_triton._rlk_torch is not built"
-    boot = ("full" if op in ("gae", "gae_masked", "gae_normalized", "vtrace", "lambda_returns",
-                             "discounted_returns")
+    boot = ("full" if op in ("gae", "gae_masked", "gae_normalized", "gae_normalized_masked",
+                             "vtrace", "lambda_returns", "discounted_returns")
             else "row")
     inp, params = make_inputs(op, *shape, seed=21, p_trunc=0.02 if op != "retrace" else 0.0,
                               boot=boot)
