@@ -496,7 +496,10 @@ template <bool NV, bool TRUNC, class E = float>
 struct ReturnsOp {
   static constexpr bool kForward = false;
   static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
-  static constexpr int kLongThreads = 1024, kLongMaxSegments = (NV || TRUNC) ? 4 : 8;
+  // plain discounted returns (two arrays read): 512-thread tiles of up to 8 segments per
+  // thread measured 3% faster at [16,131072] than 1024 threads of 2 (same tile size)
+  static constexpr int kLongThreads = (NV || TRUNC) ? 1024 : 512;
+  static constexpr int kLongMaxSegments = (NV || TRUNC) ? 4 : 8;
   using Halo = NoHalo;
   using Map = Affine;  // one carried value
   const E* r;
