@@ -526,9 +526,11 @@ __device__ __forceinline__ typename Op::Halo scan_export(const Op& op, const typ
 }
 
 template <int D, class M>
-__device__ __forceinline__ M scan_step_rows(M m, int li) {
+__device__ __forceinline__ M scan_step_rows(M m, int li, int W) {
   M prev = dpp_map<kDppRowShr + D, 0xf>(m);
-  if (li < D) prev = M::identity();  // groups narrower than a DPP row: the source is in another group
+  // groups narrower than a DPP row: the source may be in another group.  (From 16 lanes up
+  // a group starts a row, where row_shr already leaves the identity.)
+  if (W < 16 && li < D) prev = M::identity();
   return compose(m, prev);
 }
 
@@ -538,10 +540,10 @@ __device__ __forceinline__ M scan_step_rows(M m, int li) {
 template <class M>
 __device__ __forceinline__ M lane_scan(M m, int W) {
   const int li = __lane_id() & (W - 1);
-  if (W > 1) m = scan_step_rows<1>(m, li);
-  if (W > 2) m = scan_step_rows<2>(m, li);
-  if (W > 4) m = scan_step_rows<4>(m, li);
-  if (W > 8) m = scan_step_rows<8>(m, li);
+  if (W > 1) m = scan_step_rows<1>(m, li, W);
+  if (W > 2) m = scan_step_rows<2>(m, li, W);
+  if (W > 4) m = scan_step_rows<4>(m, li, W);
+  if (W > 8) m = scan_step_rows<8>(m, li, W);
   if (W > 16) m = compose(m, dpp_map<kDppRowBcast15, 0xa>(m));
   if (W > 32) m = compose(m, dpp_map<kDppRowBcast31, 0xc>(m));
   return m;
@@ -581,13 +583,13 @@ __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T,
   const int64_t row = active ? row_id : E - 1;  // idle lanes of the last workgroup read a real row
   const int t0 = (FWD ? li : L - 1 - li) * S;
 
+  Regs R;
+  op.template load<S, VEC>(row, t0, T, R);
   // the first lane of a wave that is not the first of its row reads the neighbour step
   Halo edge{};
   if constexpr (HAS_HALO) {
     if (lane == 0 && li > 0) edge = op.halo_load(row, clamp_step(FWD ? t0 - 1 : t0 + S, T), T);
   }
-  Regs R;
-  op.template load<S, VEC>(row, t0, T, R);
   State carry = row_carry(op, row, T);
   op.template prepare<S, VEC>(R, row, t0, T);
   Halo h{};
