@@ -1,0 +1,74 @@
+"""The look-back path (rows longer than 2048 steps) in the layouts the BASELINE shapes do not
+reach: more rows than ticket slots (64), so that several rows share a slot's counter and
+its tickets run row after row; one workspace serving calls of changing shapes in stream
+order; and every op at those shapes.  Against the float64 oracle with the long-row
+tolerance of test_gpu_parity.py (atol = 1e-5 * sqrt(L_eff / 128) * max(1, max|expected|)),
+and no look-back wait may give up (the workspace error flag stays clear).
+"""
+import math
+
+import numpy as np
+import pytest
+
+from _common import OUTPUTS, assert_close, make_inputs, run_api, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+OPS = ["gae", "gae_masked", "vtrace", "retrace", "lambda_returns", "discounted_returns",
+       "eligibility_traces", "prefix_sum", "backward_scan", "forward_scan"]
+
+
+def _longest_run(d):
+    best = 0
+    for row in np.asarray(d) > 0:
+        idx = np.flatnonzero(np.concatenate(([True], row, [True])))
+        best = max(best, int(np.max(np.diff(idx))))
+    return best
+
+
+def _atol(op, inp, exp):
+    scale = max(1.0, float(np.max(np.abs(exp))))
+    if op == "prefix_sum":
+        l_eff = _longest_run(inp["dones"])
+    elif op in ("discounted_returns", "backward_scan", "forward_scan"):
+        l_eff = 1.0 / (1.0 - 0.99)
+    else:
+        l_eff = 1.0 / (1.0 - 0.99 * 0.95)
+    return 1e-5 * math.sqrt(max(l_eff, 128) / 128.0) * scale
+
+
+def _inputs(op, E, T, seed):
+    kw = {"p_done": 1e-3} if op in ("prefix_sum", "eligibility_traces") else {}
+    boot = "full" if op in ("gae", "gae_masked", "vtrace", "lambda_returns",
+                            "discounted_returns") else "row"
+    return make_inputs(op, E, T, seed=seed, p_trunc=0.01 if op != "retrace" else 0.0, boot=boot,
+                       **kw)
+
+
+def _check(op, E, T, seed, device):
+    inp, params = _inputs(op, E, T, seed)
+    got = run_api(op, inp, params, device)
+    exp = run_oracle(op, inp, params)
+    for name, g, e in zip(OUTPUTS[op], got, exp):
+        assert_close(g.cpu().numpy(), e, 1e-5, _atol(op, inp, e), f"{op}[{E},{T}]:{name}")
+
+
+@pytest.mark.parametrize("op", OPS)
+@pytest.mark.parametrize("shape", [(65, 2049), (130, 4100), (200, 2052)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_more_rows_than_slots(op, shape, device):
+    from rl_triton import _native
+    _check(op, *shape, seed=21, device=device)
+    assert not _native.workspace_error(device)
+
+
+def test_one_workspace_across_changing_shapes(device):
+    """Calls of different shapes and ops back to back on one stream share the cached
+    workspace; each leaves it ready for the next."""
+    from rl_triton import _native
+    seq = [("prefix_sum", 3, 70000), ("gae", 130, 2100), ("vtrace", 2, 131073),
+           ("discounted_returns", 64, 4096), ("prefix_sum", 1, 300000), ("gae_masked", 5, 9000),
+           ("retrace", 70, 2500), ("forward_scan", 9, 33333)]
+    for i, (op, E, T) in enumerate(seq * 2):
+        _check(op, E, T, seed=100 + i, device=device)
+    assert not _native.workspace_error(device)
