@@ -63,6 +63,30 @@ def test_entry_points_reject_bad_arguments_without_launching():
     assert lib.rlk_gae(fake, fake, fake, None, fake, 9, fake, 4, 8, 0.99, 0.95, None, 0, None) == -1
     # long rows without a workspace
     assert lib.rlk_prefix_sum(fake, fake, None, fake, 2, 1 << 20, 1, None, 0, None) == -2
+    # masked entry points need their mask; the bfloat16 twins check like their float32 ones
+    assert lib.rlk_gae_masked(fake, fake, fake, None, None, 0, None, fake, 4, 8, 0.99, 0.95,
+                              None, 0, None) == -1
+    assert lib.rlk_gae_normalized_masked(fake, fake, fake, None, None, 0, None, fake, fake, 4, 8,
+                                         0.99, 0.95, 1e-8, None, 0, fake, 1 << 20, None) == -1
+    assert lib.rlk_gae_bf16(fake, fake, fake, None, fake, 9, fake, 4, 8, 0.99, 0.95, None, 0,
+                            None) == -1
+    assert lib.rlk_prefix_sum_bf16(fake, fake, None, fake, 2, 1 << 20, 1, None, 0, None) == -2
+    assert lib.rlk_affine_scan_bf16(None, None, None, None, 2, 8, 7, None, 0, None) == -1
+    # empty shapes are a no-op for every twin
+    for name in ("rlk_gae_bf16", "rlk_gae_masked", "rlk_gae_masked_bf16"):
+        argc = len(_native.SIGNATURES[name])
+        args = [None] * argc
+        i_e = [i for i, t in enumerate(_native.SIGNATURES[name]) if t is ctypes.c_int64]
+        args[i_e[0]], args[i_e[1]] = 0, 8
+        for i, t in enumerate(_native.SIGNATURES[name]):
+            if args[i] is None and t is not ctypes.c_void_p:
+                args[i] = 0
+        assert getattr(lib, name)(*args) == 0, name
+    # a normalised call's partials must hold three float64 per workgroup of the first launch
+    need = lib.rlk_gae_normalized_partials_bytes(4096, 128)
+    assert need > 0 and need % 24 == 0
+    assert lib.rlk_gae_normalized(fake, fake, fake, None, None, 0, fake, fake, 4096, 128, 0.99,
+                                  0.95, 1e-8, None, 0, fake, need - 8, None) == -2
 
 
 def _cpu(*shape):
