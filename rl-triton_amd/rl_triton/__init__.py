@@ -6,12 +6,24 @@ the reference lists it on its ROADMAP.md:75-81 but does not have it).
 """
 __version__ = "0.1.3"
 
-from rl_triton.ops.gae import compute_gae
-from rl_triton.ops.gae_norm import compute_gae_normalized
-from rl_triton.ops.retrace import compute_retrace
-from rl_triton.ops.prefix_sum import compute_episodic_prefix_sum
-from rl_triton.ops.returns import compute_discounted_returns, compute_eligibility_traces, compute_lambda_returns
-from rl_triton.ops.vtrace import compute_vtrace
+from rl_triton import _native
+from rl_triton.ops import gae as _gae
+from rl_triton.ops import gae_norm as _gae_norm
+from rl_triton.ops import prefix_sum as _prefix_sum
+from rl_triton.ops import retrace as _retrace
+from rl_triton.ops import returns as _returns
+from rl_triton.ops import vtrace as _vtrace
+
+# The public functions: the Python implementations in rl_triton.ops, each behind the C++
+# fast path that launches well-formed calls without a Python frame (_native.public_entry).
+compute_gae = _native.public_entry(_gae.compute_gae, "gae")
+compute_gae_normalized = _native.public_entry(_gae_norm.compute_gae_normalized, "gae_normalized")
+compute_retrace = _native.public_entry(_retrace.compute_retrace, "retrace")
+compute_episodic_prefix_sum = _native.public_entry(_prefix_sum.compute_episodic_prefix_sum, "prefix_sum")
+compute_discounted_returns = _native.public_entry(_returns.compute_discounted_returns, "discounted_returns")
+compute_eligibility_traces = _native.public_entry(_returns.compute_eligibility_traces, "eligibility_traces")
+compute_lambda_returns = _native.public_entry(_returns.compute_lambda_returns, "lambda_returns")
+compute_vtrace = _native.public_entry(_vtrace.compute_vtrace, "vtrace")
 
 __all__ = [
     "compute_discounted_returns",

@@ -75,6 +75,23 @@ else:
     fast = None
 
 
+def public_entry(pyfunc, op):
+    """`pyfunc` (a compute_* implementation) behind the C++ fast path: a callable with the
+    same signature, defaults, name and docstring that launches well-formed calls directly
+    and passes every other call, arguments untouched, to `pyfunc` (see Entry in
+    csrc/rlk_torch.cpp).  `pyfunc` itself when the fast path is not built."""
+    if fast is None:
+        return pyfunc
+    import functools
+    import inspect
+    params = list(inspect.signature(pyfunc).parameters.values())
+    names = tuple(p.name for p in params)
+    npos = sum(p.kind in (p.POSITIONAL_ONLY, p.POSITIONAL_OR_KEYWORD) for p in params)
+    defaults = tuple(p.default for p in params)
+    entry = fast.entry(op, names, npos, defaults, inspect.Parameter.empty, pyfunc)
+    return functools.update_wrapper(entry, pyfunc)
+
+
 class NativeLibraryError(RuntimeError):
     """The HIP library is missing or failed to load; there is no other backend."""
 

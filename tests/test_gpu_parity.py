@@ -281,9 +281,9 @@ FAST_OPS = ["gae", "gae_masked", "gae_normalized", "gae_normalized_masked", "vtr
 @pytest.mark.parametrize("shape", [(1, 1), (33, 257), (4096, 128), (16, 2048)],
                          ids=lambda s: f"{s[0]}x{s[1]}")
 def test_fast_path_matches_python_path(op, shape, device, monkeypatch):
-    """With RL_TRITON_CORRECTNESS_WARNINGS unset a well-formed call takes the C++ fast path;
-    with it set, the Python path.  Both launch the same kernel with the same arguments, so
-    the results are bit-identical."""
+    """With RL_TRITON_CORRECTNESS_WARNINGS unset a well-formed call takes the C++ fast path
+    (the public functions are its entries); with it set, the Python path.  Both launch the
+    same kernel with the same arguments, so the results are bit-identical."""
     from rl_triton import _native
     assert _native.fast is not None, "rl_triton._rlk_torch is not built"
     boot = ("full" if op in ("gae", "gae_masked", "gae_normalized", "gae_normalized_masked",
@@ -291,31 +291,44 @@ def test_fast_path_matches_python_path(op, shape, device, monkeypatch):
             else "row")
     inp, params = make_inputs(op, *shape, seed=21, p_trunc=0.02 if op != "retrace" else 0.0,
                               boot=boot)
+    before = _native.fast.launched()
     slow = run_api(op, inp, params, device)
+    assert _native.fast.launched() == before, "the flag should keep calls off the fast path"
     monkeypatch.delenv("RL_TRITON_CORRECTNESS_WARNINGS")
-    calls = []
-    real = _native.fast
-    monkeypatch.setattr(_native, "fast", _Spy(real, calls))
     fast = run_api(op, inp, params, device)
-    assert calls and all(taken for _, taken in calls), f"fast path declined: {calls}"
+    assert _native.fast.launched() == before + 1, "the call did not take the fast path"
     for s, f in zip(slow, fast):  # bit-identical (nan where both are: one-element batch std)
         torch.testing.assert_close(s, f, rtol=0, atol=0, equal_nan=True)
 
 
-class _Spy:
-    """Wraps the fast-path module and records (function, taken) per call."""
+def test_public_functions_keep_the_python_contract(device, monkeypatch):
+    """The public functions bind arguments like their Python implementations: keywords in any
+    order, defaults, and every malformed call (unknown keyword, missing argument, bad
+    boundary) raising the Python implementation's error."""
+    import inspect
 
-    def __init__(self, mod, calls):
-        self._mod, self._calls = mod, calls
-
-    def __getattr__(self, name):
-        fn = getattr(self._mod, name)
-
-        def wrapped(*a):
-            res = fn(*a)
-            self._calls.append((name, res is not None))
-            return res
-        return wrapped
+    import rl_triton
+    from rl_triton.ops import gae as gae_mod
+    monkeypatch.delenv("RL_TRITON_CORRECTNESS_WARNINGS")
+    assert inspect.signature(rl_triton.compute_gae) == inspect.signature(gae_mod.compute_gae)
+    assert rl_triton.compute_gae.__doc__ == gae_mod.compute_gae.__doc__
+    inp, params = make_inputs("gae", 16, 64, seed=3, boot="row")
+    r, v, te, lv = (torch.as_tensor(inp[k]).to(device) for k in ("rewards", "values",
+                                                                 "terminateds", "last_value"))
+    a = rl_triton.compute_gae(r, v, te, None, 0.99, 0.95, None, lv)
+    b = rl_triton.compute_gae(r, v, te, last_value=lv, lambda_=0.95, gamma=0.99)
+    c = gae_mod.compute_gae(r, v, te, last_value=lv)
+    assert torch.equal(a, b) and torch.equal(a, c)
+    with pytest.raises(TypeError, match="unexpected keyword"):
+        rl_triton.compute_gae(r, v, te, lamda=0.9)
+    with pytest.raises(TypeError, match="multiple values"):
+        rl_triton.compute_gae(r, v, te, None, gamma=0.9, truncateds=None)
+    with pytest.raises(TypeError, match="missing"):
+        rl_triton.compute_eligibility_traces(r, te)
+    with pytest.raises(ValueError, match="boundary"):
+        rl_triton.compute_episodic_prefix_sum(r, te, boundary="middle")
+    with pytest.raises(AssertionError, match="not both"):
+        rl_triton.compute_gae(r, v, te, bootstrap_values=r, last_value=lv)
 
 
 def test_fast_path_declines_what_it_cannot_take(device, monkeypatch):
