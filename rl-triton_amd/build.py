@@ -91,7 +91,7 @@ def build_ext(force: bool = True, verbose: bool = False) -> str:
            "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
            *[f"-I{i}" for i in incs], EXT_SRC, "-o", tmp,
            f"-L{torch_lib}", f"-L{os.path.dirname(LIB)}",
-           "-ltorch_python", "-ltorch", "-ltorch_cpu", "-lc10_hip", "-lc10",
+           "-ltorch_python", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-lc10_hip", "-lc10",
            "-l:librl_triton_amd.so", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}"]
     _run(cmd, verbose)
     os.replace(tmp, EXT)

@@ -16,6 +16,7 @@
 #include <Python.h>
 
 #include <ATen/ATen.h>
+#include <ATen/hip/EmptyTensor.h>
 #include <c10/hip/HIPFunctions.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/csrc/autograd/python_variable.h>
@@ -100,7 +101,10 @@ struct Call {
     return nullptr;
   }
   void* stream() const { return c10::hip::getCurrentHIPStream(dev).stream(); }
-  at::Tensor output(const at::Tensor& like) const { return at::empty({E, T}, like.options()); }
+  // the output, allocated directly by the HIP backend (no operator dispatch)
+  at::Tensor output(const at::Tensor& like) const {
+    return at::Tensor(at::detail::empty_cuda({E, T}, like.scalar_type(), like.device(), std::nullopt));
+  }
 };
 
 // Typed data pointers (T = float or rlk_bf16) of an input (nullable) and of an output.
