@@ -9,7 +9,8 @@
  * reference's AssertionErrors itself.
  *
  * Conventions shared by every entry point
- *   - Tensors are contiguous row-major float32 [num_envs, seq_len] device arrays
+ *   - Tensors are contiguous row-major float32 [num_envs, seq_len] device arrays (the
+ *     `_bf16` twins: bfloat16)
  *     (Retrace: [num_envs, seq_len, num_actions] for the per-action inputs, int64
  *     actions).  Outputs are written, never read; inputs are never written.
  *   - All work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the

@@ -6,7 +6,7 @@
 // evaluated as a scan over affine maps m(x) = add + mul * x.  Composition:
 //     (m1 o m2)(x) = m1.add + m1.mul * m2.add  +  (m1.mul * m2.mul) * x.
 //
-// Work decomposition (rows are contiguous, row-major [E, T] fp32):
+// Work decomposition (rows are contiguous, row-major [E, T]; float32 arithmetic):
 //   * a thread owns S consecutive steps of one row ("segment") and keeps its
 //     inputs in registers; it folds them into one affine map serially;
 //   * L threads (L = 2^k) form a row tile of L*S steps; their maps are combined by a

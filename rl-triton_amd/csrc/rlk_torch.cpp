@@ -3,16 +3,17 @@
 // Python module rl_triton._rlk_torch.  One function per estimator takes the public API's
 // arguments as they were passed.  When the call can go to the C ABI as it stands, the
 // function allocates the outputs, launches on torch's current stream and returns them.
-// That needs every tensor to be a contiguous tensor of the expected dtype and shape on the
-// current GPU, a row that one workgroup scans whole (no look-back workspace), and
-// RL_TRITON_CORRECTNESS_WARNINGS unset.  Any other call returns None, and the Python
-// wrapper takes its general path: the reference's assertions, contiguous copies and the
-// workspace.  A call that is taken gives the results the general path would give, and a
-// malformed call never reaches a kernel from here.
+// That needs every tensor to be a contiguous tensor of the expected dtype (float32, or
+// bfloat16 throughout) and shape on the current GPU, a row that one workgroup scans whole
+// (no look-back workspace), and RL_TRITON_CORRECTNESS_WARNINGS unset.  Any other call
+// returns None, and the Python implementation takes its general path: the reference's
+// assertions, contiguous copies and the workspace.  A call that is taken gives the results
+// the general path would give, and a malformed call never reaches a kernel from here.
+// The public functions themselves are Entry objects (below) over these functions.
 //
-// The point is host time.  At [4096, 128] a kernel runs ~5 us, while the Python path costs
-// ~10 us per call (argument checks in Python, ctypes conversion).  This path does the
-// checks in C++ and makes no Python-level calls.
+// The point is host time.  At [4096, 128] a kernel runs ~4 us; the Python path costs ~10 us
+// per call (argument checks in Python, ctypes conversion), this one ~3.5 us, most of it the
+// HIP runtime's own launch.
 #include <Python.h>
 
 #include <ATen/ATen.h>

@@ -1,8 +1,14 @@
 """rl_triton for AMD MI355X (gfx950): drop-in return-estimation ops on hand-written HIP kernels.
 
-Same public surface as simonsays1980/rl-triton v0.1.3 (src/rl_triton/__init__.py:1-17),
-plus compute_gae_normalized (GAE, returns and batch-normalised advantages in one fused call;
-the reference lists it on its ROADMAP.md:75-81 but does not have it).
+Same public surface as simonsays1980/rl-triton v0.1.3 (src/rl_triton/__init__.py:1-17).
+Beyond it, items the reference lists on its ROADMAP.md but does not have:
+  * compute_gae_normalized: GAE, returns and batch-normalised advantages (ROADMAP.md:75-81);
+  * bfloat16 I/O: every op also takes bfloat16 tensors (all float tensors of a call alike)
+    and returns bfloat16, computing in float32 (ROADMAP.md:82-99);
+  * skipped steps: compute_gae(..., mask=...) and compute_gae_normalized(..., mask=...) pass
+    the recurrence through steps with mask == 0, as verl does for observation tokens
+    (ROADMAP.md:131-140).
+Where the docstrings of rl_triton.ops say float32, bfloat16 throughout is accepted too.
 """
 __version__ = "0.1.3"
 
