@@ -599,7 +599,7 @@ __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T,
   }
 
   Map steps[S];
-  op.template coef<S>(R, h, row, t0, T, steps);
+  op.template coef<S, VEC>(R, h, row, t0, T, steps);
   const Map m = lane_scan(fold_segment<FWD, S>(steps), W);
 
   if (L > kWave) {
@@ -847,7 +847,7 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
     Map rowagg[Q];  // map of each segment row (wave-uniform)
 #pragma unroll
     for (int r = 0; r < Q; ++r) {
-      op.template coef<kSeg>(R[r], h[r], row, seg_t0(r), T, steps[r]);
+      op.template coef<kSeg, VEC>(R[r], h[r], row, seg_t0(r), T, steps[r]);
       m[r] = lane_scan(fold_segment<FWD, kSeg>(steps[r]), kWave);
       rowagg[r] = lane_bcast(m[r], kWave - 1);
     }

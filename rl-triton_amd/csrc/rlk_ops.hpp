@@ -68,16 +68,19 @@ struct GaeOp {
   __device__ float export_first(const Regs<S>& R) const { return R.v[0]; }
   __device__ float halo_load(int64_t row, int t, int T) const { return to_f32(v[row * (int64_t)T + t]); }
 
-  template <int S>
+  template <int S, bool VEC = false>
   __device__ void coef(const Regs<S>& R, float vh, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
       const float raw = (i + 1 < S) ? R.v[i + 1] : vh;
-      const float vn = (t == T - 1 || R.tr[i] == 1.f) ? R.bt[i] : raw;
+      // VEC: T % 4 == 0 and t0 % 4 == 0, so a segment is all in or all padding, and only
+      // its last step can be T - 1 (one comparison per segment instead of one per step)
+      const bool at_end = VEC ? (i == S - 1 && t0 + S == T) : (t == T - 1);
+      const float vn = (at_end || R.tr[i] == 1.f) ? R.bt[i] : raw;
       const float done = TRUNC ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
       const float a = fmaf(gamma * vn, 1.f - R.te[i], R.r[i]) - R.v[i];
-      const bool in = t < T;  // padding steps are the identity map
+      const bool in = VEC ? t0 < T : t < T;  // padding steps are the identity map
       m[i].add = in ? a : 0.f;
       m[i].mul = in ? gl * (1.f - done) : 1.f;
     }
@@ -189,7 +192,7 @@ struct MaskedGaeOp {
     return NvX{to_f32(*boot_last(boot, boot_mode, row, T)), 0.f};
   }
 
-  template <int S>
+  template <int S, bool VEC = false>
   __device__ void coef(const Regs<S>& R, NoHalo, int64_t, int t0, int T, SkipAffine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
@@ -197,7 +200,7 @@ struct MaskedGaeOp {
       const float done = TRUNC ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
       const float g1 = gamma * (1.f - R.te[i]);
       const float d = sel ? fmaf(gamma * R.bt[i], 1.f - R.te[i], R.r[i]) - R.v[i] : R.r[i] - R.v[i];
-      const bool kept = t0 + i < T && R.mk[i] != 0.f;  // padding steps are skipped too
+      const bool kept = (VEC ? t0 < T : t0 + i < T) && R.mk[i] != 0.f;  // padding steps too
       m[i] = kept ? SkipAffine{0.f, R.v[i], sel ? 0.f : g1, gl * (1.f - done), d}
                   : SkipAffine::identity();
     }
@@ -311,20 +314,22 @@ struct VtraceOp {
   __device__ float halo_load(int64_t row, int t, int T) const { return to_f32(v[row * (int64_t)T + t]); }
 
   // continuation value at step t from the raw next-step value (values or targets)
-  __device__ __forceinline__ float next_value(float raw, float tr, float bt, int t, int T) const {
-    if constexpr (TRUNC) return ((t < T - 1 && tr == 0.f) ? raw : 0.f) + bt;
-    return (t == T - 1) ? bt : raw;
+  // last: t == T - 1
+  __device__ __forceinline__ float next_value(float raw, float tr, float bt, bool last) const {
+    if constexpr (TRUNC) return ((!last && tr == 0.f) ? raw : 0.f) + bt;
+    return last ? bt : raw;
   }
 
-  template <int S>
+  template <int S, bool VEC = false>
   __device__ void coef(const Regs<S>& R, float vh, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
-      const float vn = next_value((i + 1 < S) ? R.v[i + 1] : vh, R.tr[i], R.bt[i], t, T);
+      const bool last = VEC ? (i == S - 1 && t0 + S == T) : (t == T - 1);
+      const float vn = next_value((i + 1 < S) ? R.v[i + 1] : vh, R.tr[i], R.bt[i], last);
       const float done = TRUNC ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
       const float a = R.rho[i] * (fmaf(gamma * vn, 1.f - R.te[i], R.r[i]) - R.v[i]);
-      const bool in = t < T;
+      const bool in = VEC ? t0 < T : t < T;
       m[i].add = in ? a : 0.f;
       m[i].mul = in ? gamma * R.c[i] * (1.f - done) : 1.f;
     }
@@ -340,7 +345,8 @@ struct VtraceOp {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const float raw = (i + 1 < S) ? tg[i + 1] : x_next + vh;
-      const float nt = next_value(raw, R.tr[i], R.bt[i], t0 + i, T);
+      const bool last = VEC ? (i == S - 1 && t0 + S == T) : (t0 + i == T - 1);
+      const float nt = next_value(raw, R.tr[i], R.bt[i], last);
       ad[i] = R.rho[i] * (fmaf(gamma * nt, 1.f - R.te[i], R.r[i]) - R.v[i]);
     }
     const int64_t o = row * (int64_t)T;
@@ -452,15 +458,16 @@ struct RetraceOp {
     return Halo2{c, to_f32(q[i])};
   }
 
-  template <int S>
+  template <int S, bool VEC = false>
   __device__ void coef(const Regs<S>& R, Halo2 h, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
-      const float c_next = (t < T - 1) ? ((i + 1 < S) ? R.c[i + 1] : h.a) : 0.f;
+      const bool before_end = VEC ? (i < S - 1 ? t0 < T : t0 + S < T) : (t < T - 1);
+      const float c_next = before_end ? ((i + 1 < S) ? R.c[i + 1] : h.a) : 0.f;
       const float done = fminf(R.te[i] + R.tr[i], 1.f);
       const float a = fmaf(gamma * R.enq[i], 1.f - R.te[i], R.r[i]) - R.q[i];
-      const bool in = t < T;
+      const bool in = VEC ? t0 < T : t < T;  // vector segments are all-in or all-out
       m[i].add = in ? a : 0.f;
       m[i].mul = in ? gamma * c_next * (1.f - done) : 1.f;
     }
@@ -476,7 +483,8 @@ struct RetraceOp {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
-      const float nxt = (t < T - 1) ? ((i + 1 < S) ? tg[i + 1] : x_next + h.b) : 0.f;
+      const bool before_end = VEC ? (i < S - 1 ? t0 < T : t0 + S < T) : (t < T - 1);
+      const float nxt = before_end ? ((i + 1 < S) ? tg[i + 1] : x_next + h.b) : 0.f;
       ad[i] = R.rho[i] * (fmaf(gamma * nxt, 1.f - R.te[i], R.r[i]) - R.q[i]);
     }
     const int64_t o = row * (int64_t)T;
@@ -537,7 +545,7 @@ struct ReturnsOp {
     if constexpr (TRUNC) boot_prepare<S, true>(boot_mode, t0, T, R.bt, R.blast);
   }
 
-  template <int S>
+  template <int S, bool VEC = false>
   __device__ void coef(const Regs<S>& R, NoHalo, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
@@ -545,7 +553,7 @@ struct ReturnsOp {
       const float nd = 1.f - (TRUNC ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i]);
       float a = NV ? fmaf(g1l * nd, R.nv[i], R.r[i]) : R.r[i];
       if constexpr (TRUNC) a = fmaf(gamma * R.tr[i], R.bt[i], a);
-      const bool in = t < T;
+      const bool in = VEC ? t0 < T : t < T;  // vector segments are all-in or all-out
       m[i].add = in ? a : 0.f;
       m[i].mul = in ? gl * nd : 1.f;
     }
@@ -600,7 +608,7 @@ struct DoneGatedForwardOp {
   __device__ float export_last(const Regs<S>& R) const { return R.d[S - 1]; }
   __device__ float halo_load(int64_t row, int t, int T) const { return to_f32(dones[row * (int64_t)T + t]); }
 
-  template <int S>
+  template <int S, bool VEC = false>
   __device__ void coef(const Regs<S>& R, float dh, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
@@ -608,7 +616,7 @@ struct DoneGatedForwardOp {
       float gate;
       if (ends_at) gate = (i > 0) ? R.d[i - 1] : (t == 0 ? 0.f : dh);
       else gate = R.d[i];
-      const bool in = t < T;
+      const bool in = VEC ? t0 < T : t < T;  // vector segments are all-in or all-out
       m[i].mul = in ? decay * (1.f - gate) : 1.f;
       m[i].add = in ? R.x[i] : 0.f;
     }
@@ -650,11 +658,11 @@ struct AffineScanOp {
   }
   template <int S, bool VEC>
   __device__ void prepare(Regs<S>&, int64_t, int, int) const {}
-  template <int S>
+  template <int S, bool VEC = false>
   __device__ void coef(const Regs<S>& R, NoHalo, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
-      const bool in = t0 + i < T;
+      const bool in = VEC ? t0 < T : t0 + i < T;
       m[i].mul = in ? R.v[i] : 1.f;
       m[i].add = in ? R.u[i] : 0.f;
     }
