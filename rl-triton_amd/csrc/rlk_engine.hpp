@@ -346,18 +346,22 @@ __device__ __forceinline__ uint64_t pack(uint32_t tag, float v) {
 // Segment pieces shared by both kernels.
 // ---------------------------------------------------------------------------------------
 
-// The segment's map: steps composed in scan order.
+// The segment's map: steps composed in scan order, starting from the first step itself
+// (composing with the identity would cost a multiply and an fma the compiler cannot drop:
+// x * 1 and fma(x, 0, y) are not exact identities for inf or nan).
 template <bool FWD, int S, class M>
 __device__ __forceinline__ M fold_segment(const M (&steps)[S]) {
-  M m = M::identity();
   if constexpr (FWD) {
+    M m = steps[0];
 #pragma unroll
-    for (int i = 0; i < S; ++i) m = compose(steps[i], m);
+    for (int i = 1; i < S; ++i) m = compose(steps[i], m);
+    return m;
   } else {
+    M m = steps[S - 1];
 #pragma unroll
-    for (int i = S - 1; i >= 0; --i) m = compose(steps[i], m);
+    for (int i = S - 2; i >= 0; --i) m = compose(steps[i], m);
+    return m;
   }
-  return m;
 }
 
 // Every step's state from the state entering the segment.
