@@ -20,6 +20,12 @@ Printed JSON (one line, stdout):
                  (profiles/traffic_baseline_configs.json)
   graph_replay   the same steps replayed from a captured HIP graph (no host work per call)
   ops            per-op device time, Gelem/s, GB/s and %-of-peak for both kernels
+  stream_ceiling the same byte pattern streamed with no scan (librlk_stream_ceiling.so:
+                 5 reads + 1 write for GAE, 5 reads + 2 writes for V-trace, one 16-byte
+                 non-temporal access per array per thread, 512-thread workgroups), timed
+                 the same way; kernel_frac_of_ceiling = ceiling time / kernel time;
+                 vtrace_pattern_sweep: the same 5r+2w kernel at 1x-64x the headline size,
+                 fitted as time = fixed_us + bytes / asymptotic_gb_s
   configs        the same figures for every BASELINE configuration (C1-C5,
                  tests/baseline_configs.py), each its own rotating input sets
   extensions     compute_gae_normalized (fused GAE + returns + advantage normalisation) at
@@ -27,7 +33,8 @@ Printed JSON (one line, stdout):
   cpu_baseline   the reference's sequential torch loops (restated in
                  oracle/torch_loops.py) on the host CPU, 1 thread, bounded sample; this
                  CPU leg also checks the headline outputs against the float64 oracle
-                 (parity_max_abs_err)
+                 (parity_max_abs_err) and against those float32 loops
+                 (parity_vs_reference_loops_max_abs_err)
 """
 from __future__ import annotations
 
@@ -118,6 +125,21 @@ def parity(np, cpu_sets, outs):
     return errs
 
 
+def parity_vs_loops(torch, cpu_sets, outs):
+    """Max abs difference of set 0's outputs from the reference's own float32 sequential
+    loops (restated in oracle/torch_loops.py), run on the host."""
+    from oracle import torch_loops
+    gae, vt = cpu_sets
+    adv = torch_loops.gae_loop(gae["rewards"], gae["values"], gae["terminateds"], gae["truncateds"],
+                               0.99, 0.95, bootstrap_values=gae["bootstrap_values"])
+    tg, ad = torch_loops.vtrace_loop(vt["log_pi_target"], vt["log_pi_behavior"], vt["values"],
+                                     vt["rewards"], vt["terminateds"], 0.99, 1.0, 1.0,
+                                     last_value=vt["last_value"])
+    d = lambda a, b: float((a.cpu() - b).abs().max())  # noqa: E731
+    return {"gae_advantages": d(outs[0], adv), "vtrace_targets": d(outs[1][0], tg),
+            "vtrace_advantages": d(outs[1][1], ad)}
+
+
 def time_ops(torch, rl, sets, iters, batch=100):
     """Average device duration of each op's kernel, from HIP events on the launch stream.
     Each batch of `batch` calls is queued behind a GPU spin, so the GPU runs the kernels
@@ -204,6 +226,74 @@ def _device_us(torch, fn, sets, min_launches=200, batch=50):
         total_ms += a.elapsed_time(b)
         n += batch
     return 1e3 * total_ms / n
+
+
+def time_stream_ceiling(torch, sets):
+    """Device time of the streaming ceiling of each headline kernel's byte pattern
+    (librlk_stream_ceiling.so: the same reads and writes, one 16-byte non-temporal access
+    per array per thread in 512-thread workgroups, no scan) on the same rotating input
+    sets, timed like the kernels themselves."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "rl-triton_amd", "rl_triton", "librlk_stream_ceiling.so"))
+    fn = lib.rlk_stream_ceiling
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.POINTER(ctypes.c_void_p),
+                   ctypes.c_int, ctypes.c_int64, ctypes.c_void_p]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    res = {}
+    for name, key, n_out in (("gae", 0, 1), ("vtrace", 1, 2)):
+        calls, keep = [], []
+        for s in sets:
+            ins = [t for t in s[key].values() if t.dim() == 2]
+            outs = [torch.empty(E, T, device=ins[0].device) for _ in range(n_out)]
+            keep.append((ins, outs))
+            calls.append(((ctypes.c_void_p * len(ins))(*[t.data_ptr() for t in ins]), len(ins),
+                          (ctypes.c_void_p * n_out)(*[t.data_ptr() for t in outs]), n_out))
+
+        def run(pin, n_in, pout, n_o):
+            if fn(pin, n_in, pout, n_o, E * T, stream) != 0:
+                raise RuntimeError("rlk_stream_ceiling failed")
+
+        run(*calls[0])
+        ins, outs = keep[0]
+        total = sum(ins[1:], ins[0].clone())
+        for k, o in enumerate(outs):
+            if not torch.allclose(o, total * (k + 1), rtol=1e-6, atol=1e-5):
+                raise SystemExit(f"stream ceiling kernel wrote wrong values ({name})")
+        us = _device_us(torch, run, calls)
+        res[name] = {"device_us": round(us, 3), "reads": len(keep[0][0]), "writes": n_out,
+                     "gb_s": round(E * T * 4 * (len(keep[0][0]) + n_out) / (us * 1e-6) / 1e9, 1)}
+        log(f"[bench] stream ceiling {name} ({len(keep[0][0])} reads + {n_out} writes): {us:.2f} us/launch")
+        del keep, calls
+
+    # the V-trace pattern at 1x to 64x the headline size: t = fixed + bytes / bandwidth
+    sweep = {"elements": [], "device_us": []}
+    dev = torch.device("cuda:0")
+    for scale in (1, 4, 16, 64):
+        n = E * T * scale
+        n_sets = max(2, -(-3 * MALL_BYTES // (7 * 4 * n)) + 1)
+        keep = [([torch.randn(n, device=dev) for _ in range(5)], [torch.empty(n, device=dev) for _ in range(2)])
+                for _ in range(n_sets)]
+        calls = [((ctypes.c_void_p * 5)(*[t.data_ptr() for t in i]), 5,
+                  (ctypes.c_void_p * 2)(*[t.data_ptr() for t in o]), 2) for i, o in keep]
+
+        def run_n(pin, n_in, pout, n_o, n=n):
+            if fn(pin, n_in, pout, n_o, n, stream) != 0:
+                raise RuntimeError("rlk_stream_ceiling failed")
+
+        sweep["elements"].append(n)
+        sweep["device_us"].append(round(_device_us(torch, run_n, calls, min_launches=100), 3))
+        del keep, calls
+        torch.cuda.empty_cache()
+    xs = [28.0 * n for n in sweep["elements"]]
+    ys = sweep["device_us"]
+    mx, my = sum(xs) / len(xs), sum(ys) / len(ys)
+    slope = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
+    sweep["fixed_us"] = round(my - slope * mx, 3)
+    sweep["asymptotic_gb_s"] = round(1e-3 / slope, 1)
+    log(f"[bench] stream ceiling sweep (V-trace pattern): {sweep}")
+    res["vtrace_pattern_sweep"] = sweep
+    return res
 
 
 def time_extensions(torch, min_launches=200, batch=50):
@@ -495,6 +585,10 @@ def main(argv=None):
                 "unit": "GB/s", "frac": round(ops[dom]["gb_s"] / PEAK_GBS, 4),
                 "traffic": measured_traffic({"gae": "C2_gae_4096x128", "vtrace": "C3_vtrace_4096x128"}[dom])}
 
+    ceiling = time_stream_ceiling(torch, sets)
+    for name in ("gae", "vtrace"):
+        ceiling[name]["kernel_frac_of_ceiling"] = round(ceiling[name]["device_us"] / ops[name]["device_us"], 3)
+
     graph_ms = time_graph_steps(torch, rl_triton, sets, a.steps)
     log(f"[bench] graph-replayed step: {graph_ms * 1e3:.2f} us "
         f"({2 * E * T / (graph_ms * 1e-3) / 1e9:.1f} Gelem/s)")
@@ -514,12 +608,16 @@ def main(argv=None):
 
     # CPU leg: the float64 oracle checks set 0's outputs, then the reference's sequential
     # loops are timed on the host
-    cpu, errs = None, None
+    cpu, errs, errs_loops = None, None, None
     if not a.no_cpu_baseline:
         errs = parity(np, cpu_sets, outs)
         log(f"[bench] parity vs float64 oracle (max abs err): {errs}")
         if max(errs.values()) > 1e-4:
             raise SystemExit(f"parity check failed: {errs}")
+        errs_loops = parity_vs_loops(torch, cpu_sets, outs)
+        log(f"[bench] parity vs the reference's float32 loops (max abs err): {errs_loops}")
+        if max(errs_loops.values()) > 1e-4:
+            raise SystemExit(f"parity check failed: {errs_loops}")
         log(f"[bench] CPU baseline ({a.cpu_seconds:.0f} s sample) ...")
         cpu = cpu_baseline(torch, cpu_sets, a.cpu_seconds)
         log(f"[bench] CPU baseline: {cpu['value']:.4f} Gelem/s ({cpu['ms_per_step']:.1f} ms/step)")
@@ -534,12 +632,13 @@ def main(argv=None):
                                f"{n_sets} HBM-resident sets",
                    "num_envs": E, "seq_len": T, "gamma": 0.99, "lambda": 0.95,
                    "rho_bar": 1.0, "c_bar": 1.0, "timing": "value: eager public-API calls, HIP events around the timed region"},
-        "roofline": roofline, "ops": ops, "configs": configs, "configs_bf16_io": configs_bf16,
+        "roofline": roofline, "ops": ops, "stream_ceiling": ceiling, "configs": configs, "configs_bf16_io": configs_bf16,
         "extensions": extensions,
         "graph_replay": {"ms_per_step": round(graph_ms, 6),
                          "gelem_s": round(2 * E * T / (graph_ms * 1e-3) / 1e9, 3)},
         "launch_paths": launch_paths,
-        "parity_max_abs_err": errs, "cpu_baseline": cpu,
+        "parity_max_abs_err": errs, "parity_vs_reference_loops_max_abs_err": errs_loops,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     return 0

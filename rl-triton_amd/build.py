@@ -7,6 +7,9 @@
                         hipcc, cross-compiled for gfx950 on a machine without a GPU
   _rlk_torch.so         the PyTorch-ROCm extension module over that C ABI
                         (csrc/rlk_torch.cpp), host code only, g++ against torch's headers
+  librlk_stream_ceiling.so
+                        the benchmark's streaming-ceiling kernel (csrc/bench/,
+                        include/rlk_stream_ceiling.h); not used by the package
 
 Both land next to the Python package (rl-triton_amd/rl_triton/), which loads them from
 its own directory.
@@ -26,6 +29,8 @@ INCLUDE = os.path.join(REPO, "include")
 LIB = os.path.join(HERE, "rl_triton", "librl_triton_amd.so")
 EXT = os.path.join(HERE, "rl_triton", "_rlk_torch.so")
 EXT_SRC = os.path.join(CSRC, "rlk_torch.cpp")
+CEILING = os.path.join(HERE, "rl_triton", "librlk_stream_ceiling.so")
+CEILING_SRC = os.path.join(CSRC, "bench", "stream_ceiling.hip")
 ARCH = os.environ.get("RLK_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [
@@ -72,6 +77,17 @@ def build_lib(force: bool = True, verbose: bool = False) -> str:
     return LIB
 
 
+def build_ceiling(force: bool = True, verbose: bool = False) -> str:
+    inputs = [CEILING_SRC, os.path.join(INCLUDE, "rlk_stream_ceiling.h"), os.path.abspath(__file__)]
+    if not force and up_to_date(CEILING, inputs):
+        return CEILING
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    tmp = CEILING + ".tmp"
+    _run([hipcc, *FLAGS, f"-I{INCLUDE}", CEILING_SRC, "-o", tmp], verbose)
+    os.replace(tmp, CEILING)
+    return CEILING
+
+
 def build_ext(force: bool = True, verbose: bool = False) -> str:
     """_rlk_torch.so: a CPython extension module (no pybind11) linked against torch's
     libraries and against librl_triton_amd.so, found next to it at run time."""
@@ -99,7 +115,7 @@ def build_ext(force: bool = True, verbose: bool = False) -> str:
 
 
 def build(force: bool = True, verbose: bool = False) -> list[str]:
-    return [build_lib(force, verbose), build_ext(force, verbose)]
+    return [build_lib(force, verbose), build_ext(force, verbose), build_ceiling(force, verbose)]
 
 
 def main(argv=None) -> int:

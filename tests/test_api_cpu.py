@@ -36,6 +36,32 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_native.SIGNATURES), "binding signatures out of sync with the header"
 
 
+CEILING_HEADER = os.path.join(ROOT, "include", "rlk_stream_ceiling.h")
+CEILING_LIB = os.path.join(ROOT, "rl-triton_amd", "rl_triton", "librlk_stream_ceiling.so")
+
+
+def test_stream_ceiling_library_exports_and_rejects_bad_arguments():
+    """The benchmark's streaming-ceiling library: its one declared symbol is exported and
+    invalid arguments are refused before any launch."""
+    text = open(CEILING_HEADER).read()
+    names = re.findall(r"^\s*int\s+(rlk_\w+)\s*\(", text, re.M)
+    assert names == ["rlk_stream_ceiling"]
+    lib = ctypes.CDLL(CEILING_LIB)
+    fn = lib.rlk_stream_ceiling
+    fn.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.POINTER(ctypes.c_void_p),
+                   ctypes.c_int, ctypes.c_int64, ctypes.c_void_p]
+    P = ctypes.c_void_p
+    ins, outs = (P * 6)(*[16 * (i + 1) for i in range(6)]), (P * 2)(1024, 2048)
+    assert fn(ins, 0, outs, 1, 16, None) == -1          # no inputs
+    assert fn(ins, 7, outs, 1, 16, None) == -1          # too many inputs
+    assert fn(ins, 5, outs, 3, 16, None) == -1          # too many outputs
+    assert fn(ins, 5, outs, 1, 18, None) == -1          # n not a multiple of 4
+    assert fn(ins, 5, outs, 1, -4, None) == -1
+    assert fn((P * 1)(8), 1, outs, 1, 16, None) == -1   # misaligned input
+    assert fn((P * 1)(None), 1, outs, 1, 16, None) == -1
+    assert fn(ins, 5, outs, 2, 0, None) == 0            # empty: no launch
+
+
 def test_host_only_entry_points():
     lib = _native.load()
     assert lib.rlk_version() >= 100
