@@ -99,23 +99,34 @@ def run_oracle(op, inp, params):
     raise KeyError(op)
 
 
-def to_device(inp, device, dtype=torch.float32):
-    """Float inputs as `dtype` (float32 or bfloat16, rounded to nearest even), int64 actions."""
+def _placed(t, offset):
+    """`t` as a contiguous view that starts `offset` elements into a larger buffer, so its
+    data pointer is only element-aligned (offset 1: not 16-byte aligned)."""
+    if not offset:
+        return t
+    buf = torch.empty(t.numel() + offset, dtype=t.dtype, device=t.device)
+    buf[offset:].copy_(t.reshape(-1))
+    return buf[offset:].view(t.shape)
+
+
+def to_device(inp, device, dtype=torch.float32, offset=0):
+    """Float inputs as `dtype` (float32 or bfloat16, rounded to nearest even), int64 actions;
+    offset > 0 places every array that many elements into a larger buffer."""
     out = {}
     for k, v in inp.items():
         if v is None:
             out[k] = None
         elif k == "actions":
-            out[k] = torch.as_tensor(np.asarray(v, dtype=np.int64)).to(device)
+            out[k] = _placed(torch.as_tensor(np.asarray(v, dtype=np.int64)).to(device), offset)
         else:
-            out[k] = torch.as_tensor(np.asarray(v, dtype=np.float32)).to(dtype).to(device)
+            out[k] = _placed(torch.as_tensor(np.asarray(v, dtype=np.float32)).to(dtype).to(device), offset)
     return out
 
 
-def run_api(op, inp, params, device, dtype=torch.float32):
+def run_api(op, inp, params, device, dtype=torch.float32, offset=0):
     import rl_triton
     from rl_triton.ops._scan import _run_scan, _run_scan_forward
-    d = to_device(inp, device, dtype)
+    d = to_device(inp, device, dtype, offset)
     g = lambda k: d.get(k)  # noqa: E731
     if op == "gae":
         return (rl_triton.compute_gae(g("rewards"), g("values"), g("terminateds"), g("truncateds"),

@@ -187,6 +187,29 @@ def test_non_contiguous_inputs(device):
     assert_close(got.cpu().numpy(), exp, 1e-5, 1e-5, "gae non-contiguous")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("op", ["gae", "vtrace", "retrace", "lambda_returns", "discounted_returns",
+                                "eligibility_traces", "prefix_sum", "backward_scan"])
+@pytest.mark.parametrize("shape", [(64, 128), (3, 1024), (2, 8192)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_misaligned_inputs(op, shape, dtype, device):
+    """Inputs that are contiguous but start one element into their buffer (not 16-byte
+    aligned) take the element-wise load path (the 16-byte path needs every array on a
+    four-element boundary, rlk_capi.hip quad_aligned).  Its results equal the aligned
+    call's bit for bit: both paths fold the same four-step segments in the same order."""
+    inp, params = make_inputs(op, *shape, seed=17, p_trunc=0.02 if op in ("gae", "vtrace") else 0.0,
+                              boot="full" if op in ("gae", "lambda_returns") else "none")
+    ref = run_api(op, inp, params, device, dtype)
+    got = run_api(op, inp, params, device, dtype, offset=1)
+    torch.cuda.synchronize()
+    for name, g, r in zip(OUTPUTS[op], got, ref):
+        assert torch.equal(g, r), f"{op}{shape} {dtype}: {name} differs between aligned and offset inputs"
+    if dtype is torch.float32:
+        exp = run_oracle(op, inp, params)
+        for name, g, e in zip(OUTPUTS[op], got, exp):
+            scale = max(1.0, float(np.max(np.abs(e))))
+            assert_close(g.cpu().numpy(), e, 1e-5, 1e-4 * scale, f"{op}{shape} offset:{name}")
+
+
 @pytest.mark.parametrize("shape", [(0, 16), (4, 0), (0, 0)])
 def test_empty_inputs(shape, device):
     import rl_triton
