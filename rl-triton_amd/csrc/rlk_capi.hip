@@ -83,10 +83,15 @@ int64_t chain_grid(int64_t E, int64_t T, int NT, int Q) {
   return nslots * (((E + nslots - 1) / nslots) * ((T + tile - 1) / tile));
 }
 
+// Short rows: steps per segment.  Four (one quad per array per thread) from four steps
+// up; rows of 1-3 steps take one step per thread, element by element.
+int rows_seg(int64_t T) { return T < 4 ? 1 : 4; }
+
 // Workgroups of the launch that launch() makes for Op at [E, T] (E, T > 0).
 template <class Op>
 int64_t launch_grid(int64_t E, int64_t T) {
   if (T > kShortMaxT) return chain_grid(E, T, Op::kLongThreads, long_segments<Op>(E, T));
+  if (rows_seg(T) == 1) return rows_grid(E, T, 1, kNT);
   return rows_grid(E, T, 4, rows_threads(E, T));
 }
 
@@ -138,6 +143,8 @@ int launch(const Op& op, int64_t E, int64_t T, bool vec, void* workspace, size_t
     if (ws == nullptr || workspace_bytes_given < workspace_bytes(E, T) || !aligned16(ws))
       return RLK_ERR_WORKSPACE;
     e = vec ? launch_long<Op, true>(op, E, Ti, ws, s) : launch_long<Op, false>(op, E, Ti, ws, s);
+  } else if (rows_seg(T) == 1) {
+    e = launch_rows<Op, kNT, 1, false>(op, E, Ti, s);
   } else if (rows_threads(E, T) == kNT) {
     e = vec ? launch_rows<Op, kNT, 4, true>(op, E, Ti, s) : launch_rows<Op, kNT, 4, false>(op, E, Ti, s);
   } else {
