@@ -30,6 +30,9 @@ Printed JSON (one line, stdout):
                  tests/baseline_configs.py), each its own rotating input sets
   extensions     compute_gae_normalized (fused GAE + returns + advantage normalisation) at
                  [4096,128] against the torch composition it replaces
+  element_aligned_rows
+                 C2, C3 and the C5 prefix sum one step short of a multiple of four
+                 ([4096,127], [8,2^20-1]): quads that are only element-aligned
   cpu_baseline   the reference's sequential torch loops (restated in
                  oracle/torch_loops.py) on the host CPU, 1 thread, bounded sample; this
                  CPU leg also checks the headline outputs against the float64 oracle
@@ -226,6 +229,29 @@ def _device_us(torch, fn, sets, min_launches=200, batch=50):
         total_ms += a.elapsed_time(b)
         n += batch
     return 1e3 * total_ms / n
+
+
+def time_element_aligned(torch, configs, min_launches=200):
+    """Three BASELINE configurations one step short of a multiple of four (T % 4 != 0), so
+    that their quads are only element-aligned, beside the aligned configuration's time."""
+    import baseline_configs as bc
+    dev = torch.device("cuda:0")
+    res = {}
+    for name, (E_, T_) in (("C2_gae_4096x128", (4096, 127)), ("C3_vtrace_4096x128", (4096, 127)),
+                           ("C5_prefix_sum_8x1048576", (8, (1 << 20) - 1))):
+        bpe = bc.bytes_per_elem(name)
+        n_sets = min(64, max(2, -(-3 * MALL_BYTES // (E_ * T_ * bpe)) + 1))
+        sets = [bc.make(name, seed=200 + i, device=dev, shape=(E_, T_)) for i in range(n_sets)]
+        us = _device_us(torch, lambda inp, params: bc.call(name, inp, params), sets, min_launches)
+        del sets
+        gbs = E_ * T_ * bpe / (us * 1e-6) / 1e9
+        res[f"{name.split('_')[0]}_{bc.CONFIGS[name][0]}_{E_}x{T_}"] = {
+            "shape": [E_, T_], "device_us": round(us, 3), "gb_s": round(gbs, 1),
+            "pct_peak": round(100 * gbs / PEAK_GBS, 2),
+            "aligned_config_us": configs[name]["device_us"] if configs and name in configs else None}
+        log(f"[bench] element-aligned {name} at [{E_},{T_}]: {us:.2f} us/launch ({100 * gbs / PEAK_GBS:.1f}% of 8 TB/s)")
+    torch.cuda.empty_cache()
+    return res
 
 
 def time_stream_ceiling(torch, sets):
@@ -605,6 +631,7 @@ def main(argv=None):
     configs = time_configs(torch, cfg_names) if cfg_names else None
     configs_bf16 = time_configs(torch, cfg_names, dtype=torch.bfloat16) if cfg_names else None
     extensions = time_extensions(torch) if a.configs != "none" else None
+    element_aligned = time_element_aligned(torch, configs) if a.configs != "none" else None
 
     # CPU leg: the float64 oracle checks set 0's outputs, then the reference's sequential
     # loops are timed on the host
@@ -633,7 +660,7 @@ def main(argv=None):
                    "num_envs": E, "seq_len": T, "gamma": 0.99, "lambda": 0.95,
                    "rho_bar": 1.0, "c_bar": 1.0, "timing": "value: eager public-API calls, HIP events around the timed region"},
         "roofline": roofline, "ops": ops, "stream_ceiling": ceiling, "configs": configs, "configs_bf16_io": configs_bf16,
-        "extensions": extensions,
+        "extensions": extensions, "element_aligned_rows": element_aligned,
         "graph_replay": {"ms_per_step": round(graph_ms, 6),
                          "gelem_s": round(2 * E * T / (graph_ms * 1e-3) / 1e9, 3)},
         "launch_paths": launch_paths,

@@ -48,11 +48,14 @@ TARGETS = {"C2_gae_4096x128": 0.60, "C3_vtrace_4096x128": 0.60,
            "C5_discounted_returns_16x131072": 0.50, "C5_vtrace_16x131072": 0.50}
 
 
-def make(name: str, seed: int = 0, device="cpu"):
+def make(name: str, seed: int = 0, device="cpu", shape=None):
     """Inputs (dict of float32 / int64 tensors on `device`) and keyword params of `name`.
     With device="cpu" the draw is a seeded CPU generator (the parity sets); on a GPU the
-    same distributions come from a seeded device generator (the bench's rotating sets)."""
+    same distributions come from a seeded device generator (the bench's rotating sets).
+    shape=(E, T) draws the same distributions at another shape."""
     op, E, T, _ = CONFIGS[name]
+    if shape is not None:
+        E, T = shape
     g = torch.Generator(device=device).manual_seed(seed)
     kw = {"generator": g, "device": device}
     rn = lambda *s: torch.randn(*s, **kw)           # noqa: E731
