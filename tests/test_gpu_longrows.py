@@ -72,3 +72,30 @@ def test_one_workspace_across_changing_shapes(device):
     for i, (op, E, T) in enumerate(seq * 2):
         _check(op, E, T, seed=100 + i, device=device)
     assert not _native.workspace_error(device)
+
+
+def test_concurrent_streams(device):
+    """Long-row calls queued on two streams at once, with no synchronisation between them:
+    each stream has its own workspace (ticket counters, epoch and status words), and the two
+    grids may share the GPU in any proportion, so a tile can wait on a predecessor whose
+    workgroup is not resident yet (tickets order each row's tiles by start).  Every result
+    matches the oracle and no wait gives up."""
+    import torch
+    from rl_triton import _native
+    jobs = [[("prefix_sum", 4, 150000), ("discounted_returns", 3, 200001), ("vtrace", 2, 131072)],
+            [("eligibility_traces", 6, 90000), ("gae", 5, 70000), ("forward_scan", 8, 65537)]]
+    streams = [torch.cuda.Stream(device), torch.cuda.Stream(device)]
+    pending = []
+    for rep in range(2):
+        for k in range(3):
+            for j, s in enumerate(streams):
+                op, E, T = jobs[j][k]
+                inp, params = _inputs(op, E, T, seed=300 + 10 * rep + 3 * j + k)
+                with torch.cuda.stream(s):
+                    pending.append((op, E, T, inp, params, run_api(op, inp, params, device)))
+    torch.cuda.synchronize()
+    for op, E, T, inp, params, got in pending:
+        exp = run_oracle(op, inp, params)
+        for name, g, e in zip(OUTPUTS[op], got, exp):
+            assert_close(g.cpu().numpy(), e, 1e-5, _atol(op, inp, e), f"{op}[{E},{T}] concurrent:{name}")
+    assert not _native.workspace_error(device)
