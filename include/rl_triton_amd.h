@@ -15,6 +15,10 @@
  *     actions).  Outputs are written, never read; inputs are never written.
  *   - All work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the
  *     default stream).  Nothing allocates and nothing synchronises.
+ *   - Any element-aligned pointers are accepted.  The fastest form is seq_len % 4 == 0
+ *     with every [num_envs, seq_len] array 16-byte aligned (bfloat16: 8-byte), which
+ *     the kernels read and write with aligned non-temporal 16-byte accesses; otherwise
+ *     they use element-aligned 16-byte accesses (about 15% slower).
  *   - Bootstrap mode: RLK_BOOT_NONE (bootstrap == NULL, value 0), RLK_BOOT_ROW
  *     (bootstrap is [num_envs]: the continuation value after step seq_len-1, the
  *     reference's `last_value`), RLK_BOOT_FULL (bootstrap is [num_envs, seq_len], the
