@@ -99,3 +99,16 @@ def test_concurrent_streams(device):
         for name, g, e in zip(OUTPUTS[op], got, exp):
             assert_close(g.cpu().numpy(), e, 1e-5, _atol(op, inp, e), f"{op}[{E},{T}] concurrent:{name}")
     assert not _native.workspace_error(device)
+
+
+@pytest.mark.parametrize("op,shape", [("prefix_sum", (1, 1 << 23)), ("vtrace", (1, 1 << 21)),
+                                      ("gae_masked", (1, 1 << 20)), ("backward_scan", (1, 3 << 20)),
+                                      ("discounted_returns", (2, 1 << 21)),
+                                      ("eligibility_traces", (1, (1 << 22) + 3))],
+                         ids=lambda v: v if isinstance(v, str) else f"{v[0]}x{v[1]}")
+def test_many_tiles_per_row(op, shape, device):
+    """Rows of 128-512 tiles: the look-back walks back over several 64-tile windows of maps
+    before it meets a tile's state."""
+    from rl_triton import _native
+    _check(op, *shape, seed=41, device=device)
+    assert not _native.workspace_error(device)
