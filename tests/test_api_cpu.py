@@ -36,6 +36,20 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_native.SIGNATURES), "binding signatures out of sync with the header"
 
 
+@pytest.mark.parametrize("lang", ["c", "c++"])
+def test_headers_compile_as_plain_c_and_cpp(lang, tmp_path):
+    """The C ABI headers need nothing beyond the C standard headers: a C99 (and a C++17)
+    translation unit that includes them compiles with every warning an error."""
+    import subprocess
+    src = tmp_path / ("t.c" if lang == "c" else "t.cpp")
+    src.write_text('#include "rl_triton_amd.h"\n#include "rlk_stream_ceiling.h"\n'
+                   "int main(void) { return rlk_version() > 0 ? 0 : 1; }\n")
+    cc, std = ("gcc", "-std=c99") if lang == "c" else ("g++", "-std=c++17")
+    r = subprocess.run([cc, std, "-Wall", "-Wextra", "-Werror", "-pedantic", "-fsyntax-only",
+                        "-I", os.path.join(ROOT, "include"), str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
 CEILING_HEADER = os.path.join(ROOT, "include", "rlk_stream_ceiling.h")
 CEILING_LIB = os.path.join(ROOT, "rl-triton_amd", "rl_triton", "librlk_stream_ceiling.so")
 
