@@ -4,11 +4,12 @@
 // arguments as they were passed.  When the call can go to the C ABI as it stands, the
 // function allocates the outputs, launches on torch's current stream and returns them.
 // That needs every tensor to be a contiguous tensor of the expected dtype (float32, or
-// bfloat16 throughout) and shape on the current GPU, a row that one workgroup scans whole
-// (no look-back workspace), and RL_TRITON_CORRECTNESS_WARNINGS unset.  Any other call
+// bfloat16 throughout) and shape on the current GPU, RL_TRITON_CORRECTNESS_WARNINGS unset,
+// and, for rows long enough to need a look-back workspace, a stream that is not capturing
+// a graph (captured calls get buffers of their own on the Python path).  Any other call
 // returns None, and the Python implementation takes its general path: the reference's
-// assertions, contiguous copies and the workspace.  A call that is taken gives the results
-// the general path would give, and a malformed call never reaches a kernel from here.
+// assertions and contiguous copies.  A call that is taken gives the results the general
+// path would give, and a malformed call never reaches a kernel from here.
 // The public functions themselves are Entry objects (below) over these functions.
 //
 // The point is host time.  At [4096, 128] a kernel runs ~4 us; the Python path costs ~10 us
@@ -22,17 +23,18 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/csrc/autograd/python_variable.h>
 
+#include <algorithm>
 #include <cstddef>
+#include <cstdint>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <type_traits>
+#include <utility>
 
 #include "rl_triton_amd.h"
 
 namespace {
-
-// rows up to this length are scanned whole by one workgroup and need no workspace
-constexpr int64_t kNoWorkspaceMaxT = 2048;
 
 bool correctness_warnings() {
   const char* v = std::getenv("RL_TRITON_CORRECTNESS_WARNINGS");
@@ -62,7 +64,7 @@ struct Call {
     dev = t.get_device();
     E = t.size(0);
     T = t.size(1);
-    if (dev != c10::hip::current_device() || T > kNoWorkspaceMaxT) return fail();
+    if (dev != c10::hip::current_device()) return fail();
     return &t;
   }
   // A tensor of shape [E, T] (or [E] / [E, T, A]) on the same device, of the call's storage
@@ -107,6 +109,42 @@ struct Call {
     return at::Tensor(at::detail::empty_cuda({E, T}, like.scalar_type(), like.device(), std::nullopt));
   }
 };
+
+// Look-back workspaces of the calls this module launches, one per (device, stream):
+// zero-filled when allocated (on that stream), grown by doubling, and left ready by every
+// call for the next.  Calls on one stream are ordered, so one buffer serves them all, and
+// the caching allocator keeps a replaced buffer until the stream's earlier work is done.
+// (The Python path keeps workspaces of its own; a workspace is only ever shared by calls
+// on one stream, whichever path they take.)  The GIL guards the map.
+std::map<std::pair<int, uintptr_t>, at::Tensor> g_workspaces;
+
+struct Workspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  bool ok = true;  // false: decline (a graph capture is in progress on the stream)
+};
+
+Workspace workspace(const Call& c, const at::Tensor& like) {
+  Workspace w;
+  if (!c.ok) return w;
+  const size_t need = rlk_workspace_bytes(c.E, c.T);
+  if (need == 0) return w;
+  hipStream_t s = static_cast<hipStream_t>(c.stream());
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+    w.ok = false;
+    return w;
+  }
+  at::Tensor& buf = g_workspaces[{(int)c.dev, reinterpret_cast<uintptr_t>(s)}];
+  if (!buf.defined() || (size_t)buf.numel() < need) {
+    size_t size = buf.defined() ? std::max(need, 2 * (size_t)buf.numel()) : need;
+    size = (size + 255) / 256 * 256;
+    buf = at::zeros({(int64_t)size}, like.options().dtype(at::kByte));
+  }
+  w.ptr = buf.data_ptr();
+  w.bytes = (size_t)buf.numel();
+  return w;
+}
 
 // Typed data pointers (T = float or rlk_bf16) of an input (nullable) and of an output.
 template <class T>
@@ -178,15 +216,17 @@ PyObject* op_gae(PyObject* const* a, Py_ssize_t n) {
   const at::Tensor* mask = c.opt(a[8]);
   if (!c.ok) return decline();
   const int mode = has_lv ? RLK_BOOT_ROW : has_bv ? RLK_BOOT_FULL : RLK_BOOT_NONE;
+  const Workspace ws = workspace(c, *r);
+  if (!ws.ok) return decline();
   at::Tensor out = c.output(*r);
   const int st = dispatch(c, [&](auto z) {
     using T = decltype(z);
     if (mask)
       return pick<T>(rlk_gae_masked, rlk_gae_masked_bf16)(in_ptr<T>(r), in_ptr<T>(v),
         in_ptr<T>(te), in_ptr<T>(tr), in_ptr<T>(boot), mode, in_ptr<T>(mask), out_ptr<T>(out),
-        c.E, c.T, gamma, lam, nullptr, 0, c.stream());
+        c.E, c.T, gamma, lam, ws.ptr, ws.bytes, c.stream());
     return pick<T>(rlk_gae, rlk_gae_bf16)(in_ptr<T>(r), in_ptr<T>(v), in_ptr<T>(te), in_ptr<T>(tr),
-      in_ptr<T>(boot), mode, out_ptr<T>(out), c.E, c.T, gamma, lam, nullptr, 0, c.stream());
+      in_ptr<T>(boot), mode, out_ptr<T>(out), c.E, c.T, gamma, lam, ws.ptr, ws.bytes, c.stream());
   });
   return finish(st, mask ? "rlk_gae_masked" : "rlk_gae", THPVariable_Wrap(std::move(out)));
 }
@@ -209,6 +249,8 @@ PyObject* op_gae_normalized(PyObject* const* a, Py_ssize_t n) {
   const at::Tensor* mask = c.opt(a[9]);
   if (!c.ok) return decline();
   const int mode = has_lv ? RLK_BOOT_ROW : has_bv ? RLK_BOOT_FULL : RLK_BOOT_NONE;
+  const Workspace ws = workspace(c, *r);
+  if (!ws.ok) return decline();
   at::Tensor adv = c.output(*r), ret = c.output(*r);
   const size_t pb = rlk_gae_normalized_partials_bytes(c.E, c.T);
   at::Tensor parts = at::empty({(int64_t)(pb > 0 ? pb : 8)}, r->options().dtype(at::kByte));
@@ -217,11 +259,11 @@ PyObject* op_gae_normalized(PyObject* const* a, Py_ssize_t n) {
     if (mask)
       return pick<T>(rlk_gae_normalized_masked, rlk_gae_normalized_masked_bf16)(
         in_ptr<T>(r), in_ptr<T>(v), in_ptr<T>(te), in_ptr<T>(tr), in_ptr<T>(boot), mode,
-        in_ptr<T>(mask), out_ptr<T>(adv), out_ptr<T>(ret), c.E, c.T, gamma, lam, eps, nullptr, 0,
+        in_ptr<T>(mask), out_ptr<T>(adv), out_ptr<T>(ret), c.E, c.T, gamma, lam, eps, ws.ptr, ws.bytes,
         parts.data_ptr(), pb, c.stream());
     return pick<T>(rlk_gae_normalized, rlk_gae_normalized_bf16)(in_ptr<T>(r), in_ptr<T>(v),
       in_ptr<T>(te), in_ptr<T>(tr), in_ptr<T>(boot), mode, out_ptr<T>(adv), out_ptr<T>(ret),
-      c.E, c.T, gamma, lam, eps, nullptr, 0, parts.data_ptr(), pb, c.stream());
+      c.E, c.T, gamma, lam, eps, ws.ptr, ws.bytes, parts.data_ptr(), pb, c.stream());
   });
   return finish(st, mask ? "rlk_gae_normalized_masked" : "rlk_gae_normalized", pair(adv, ret));
 }
@@ -244,12 +286,14 @@ PyObject* op_vtrace(PyObject* const* a, Py_ssize_t n) {
   const at::Tensor* boot = has_lv ? c.need(a[10], 1) : c.opt(a[9]);
   if (!c.ok) return decline();
   const int mode = has_lv ? RLK_BOOT_ROW : has_bv ? RLK_BOOT_FULL : RLK_BOOT_NONE;
+  const Workspace ws = workspace(c, *r);
+  if (!ws.ok) return decline();
   at::Tensor tg = c.output(*r), adv = c.output(*r);
   const int st = dispatch(c, [&](auto z) {
     using T = decltype(z);
     return pick<T>(rlk_vtrace, rlk_vtrace_bf16)(in_ptr<T>(lpt), in_ptr<T>(lpb), in_ptr<T>(v),
       in_ptr<T>(r), in_ptr<T>(te), in_ptr<T>(tr), in_ptr<T>(boot), mode, out_ptr<T>(tg),
-      out_ptr<T>(adv), c.E, c.T, gamma, rho_bar, c_bar, nullptr, 0, c.stream());
+      out_ptr<T>(adv), c.E, c.T, gamma, rho_bar, c_bar, ws.ptr, ws.bytes, c.stream());
   });
   return finish(st, "rlk_vtrace", pair(tg, adv));
 }
@@ -277,12 +321,14 @@ PyObject* op_retrace(PyObject* const* a, Py_ssize_t n) {
   const float gamma = c.scalar(a[8]), lam = c.scalar(a[9]), c_bar = c.scalar(a[10]),
               rho_bar = c.scalar(a[11]);
   if (!c.ok) return decline();
+  const Workspace ws = workspace(c, *r);
+  if (!ws.ok) return decline();
   at::Tensor tg = c.output(*r), adv = c.output(*r);
   const int st = dispatch(c, [&](auto z) {
     using T = decltype(z);
     return pick<T>(rlk_retrace, rlk_retrace_bf16)(in_ptr<T>(pi), in_ptr<T>(mu), in_ptr<T>(q),
       in_ptr<T>(nq), act->data_ptr<int64_t>(), in_ptr<T>(r), in_ptr<T>(te), in_ptr<T>(tr),
-      out_ptr<T>(tg), out_ptr<T>(adv), c.E, c.T, A, gamma, lam, c_bar, rho_bar, nullptr, 0,
+      out_ptr<T>(tg), out_ptr<T>(adv), c.E, c.T, A, gamma, lam, c_bar, rho_bar, ws.ptr, ws.bytes,
       c.stream());
   });
   return finish(st, "rlk_retrace", pair(tg, adv));
@@ -300,12 +346,14 @@ PyObject* op_lambda_returns(PyObject* const* a, Py_ssize_t n) {
   const float gamma = c.scalar(a[4]), lam = c.scalar(a[5]);
   const at::Tensor* boot = c.opt(a[6]);
   if (!c.ok) return decline();
+  const Workspace ws = workspace(c, *r);
+  if (!ws.ok) return decline();
   at::Tensor out = c.output(*r);
   const int st = dispatch(c, [&](auto z) {
     using T = decltype(z);
     return pick<T>(rlk_lambda_returns, rlk_lambda_returns_bf16)(in_ptr<T>(r), in_ptr<T>(nv),
       in_ptr<T>(te), in_ptr<T>(tr), in_ptr<T>(boot), boot ? RLK_BOOT_FULL : RLK_BOOT_NONE,
-      out_ptr<T>(out), c.E, c.T, gamma, lam, nullptr, 0, c.stream());
+      out_ptr<T>(out), c.E, c.T, gamma, lam, ws.ptr, ws.bytes, c.stream());
   });
   return finish(st, "rlk_lambda_returns", THPVariable_Wrap(std::move(out)));
 }
@@ -321,12 +369,14 @@ PyObject* op_discounted_returns(PyObject* const* a, Py_ssize_t n) {
   const float gamma = c.scalar(a[3]);
   const at::Tensor* boot = c.opt(a[4]);
   if (!c.ok) return decline();
+  const Workspace ws = workspace(c, *r);
+  if (!ws.ok) return decline();
   at::Tensor out = c.output(*r);
   const int st = dispatch(c, [&](auto z) {
     using T = decltype(z);
     return pick<T>(rlk_discounted_returns, rlk_discounted_returns_bf16)(in_ptr<T>(r), in_ptr<T>(te),
       in_ptr<T>(tr), in_ptr<T>(boot), boot ? RLK_BOOT_FULL : RLK_BOOT_NONE, out_ptr<T>(out), c.E,
-      c.T, gamma, nullptr, 0, c.stream());
+      c.T, gamma, ws.ptr, ws.bytes, c.stream());
   });
   return finish(st, "rlk_discounted_returns", THPVariable_Wrap(std::move(out)));
 }
@@ -341,11 +391,13 @@ PyObject* op_eligibility_traces(PyObject* const* a, Py_ssize_t n) {
   const float gamma = c.scalar(a[2]), lam = c.scalar(a[3]);
   const at::Tensor* seed = c.opt(a[4], 1);
   if (!c.ok) return decline();
+  const Workspace ws = workspace(c, *g);
+  if (!ws.ok) return decline();
   at::Tensor out = c.output(*g);
   const int st = dispatch(c, [&](auto z) {
     using T = decltype(z);
     return pick<T>(rlk_eligibility_traces, rlk_eligibility_traces_bf16)(in_ptr<T>(g), in_ptr<T>(d),
-      in_ptr<T>(seed), out_ptr<T>(out), c.E, c.T, gamma, lam, nullptr, 0, c.stream());
+      in_ptr<T>(seed), out_ptr<T>(out), c.E, c.T, gamma, lam, ws.ptr, ws.bytes, c.stream());
   });
   return finish(st, "rlk_eligibility_traces", THPVariable_Wrap(std::move(out)));
 }
@@ -359,11 +411,13 @@ PyObject* op_prefix_sum(PyObject* const* a, Py_ssize_t n) {
   const at::Tensor* d = c.need(a[1]);
   const at::Tensor* seed = c.opt(a[2], 1);
   if (!c.ok || !PyBool_Check(a[3])) return decline();
+  const Workspace ws = workspace(c, *x);
+  if (!ws.ok) return decline();
   at::Tensor out = c.output(*x);
   const int st = dispatch(c, [&](auto z) {
     using T = decltype(z);
     return pick<T>(rlk_prefix_sum, rlk_prefix_sum_bf16)(in_ptr<T>(x), in_ptr<T>(d), in_ptr<T>(seed),
-      out_ptr<T>(out), c.E, c.T, a[3] == Py_True ? 1 : 0, nullptr, 0, c.stream());
+      out_ptr<T>(out), c.E, c.T, a[3] == Py_True ? 1 : 0, ws.ptr, ws.bytes, c.stream());
   });
   return finish(st, "rlk_prefix_sum", THPVariable_Wrap(std::move(out)));
 }
@@ -378,11 +432,13 @@ PyObject* op_affine_scan(PyObject* const* a, Py_ssize_t n) {
   const at::Tensor* carry = c.opt(a[2], 1);
   const long dir = PyLong_CheckExact(a[3]) ? PyLong_AsLong(a[3]) : -1;
   if (!c.ok || (dir != RLK_BACKWARD && dir != RLK_FORWARD)) return decline();
+  const Workspace ws = workspace(c, *u);
+  if (!ws.ok) return decline();
   at::Tensor out = c.output(*u);
   const int st = dispatch(c, [&](auto z) {
     using T = decltype(z);
     return pick<T>(rlk_affine_scan, rlk_affine_scan_bf16)(in_ptr<T>(u), in_ptr<T>(v),
-      in_ptr<T>(carry), out_ptr<T>(out), c.E, c.T, (int)dir, nullptr, 0, c.stream());
+      in_ptr<T>(carry), out_ptr<T>(out), c.E, c.T, (int)dir, ws.ptr, ws.bytes, c.stream());
   });
   return finish(st, "rlk_affine_scan", THPVariable_Wrap(std::move(out)));
 }
@@ -552,9 +608,31 @@ PyObject* make_entry(PyObject*, PyObject* args) {
 
 PyObject* launched(PyObject*, PyObject*) { return PyLong_FromUnsignedLongLong(g_launched); }
 
+// workspace_error(device) -> True if a workspace of this module on that device recorded a
+// look-back wait that gave up (header word 3).  Reads the flags back: synchronises.
+PyObject* workspace_error(PyObject*, PyObject* arg) {
+  const long dev = PyLong_AsLong(arg);
+  if (dev == -1 && PyErr_Occurred()) return nullptr;
+  try {
+    for (auto& kv : g_workspaces) {
+      if (kv.first.first != dev || !kv.second.defined()) continue;
+      const at::Tensor flag = kv.second.narrow(0, 3 * 8, 8).to(at::kCPU);
+      const uint8_t* b = flag.data_ptr<uint8_t>();
+      for (int i = 0; i < 8; ++i)
+        if (b[i] != 0) Py_RETURN_TRUE;
+    }
+  } catch (const std::exception& e) {
+    PyErr_SetString(PyExc_RuntimeError, e.what());
+    return nullptr;
+  }
+  Py_RETURN_FALSE;
+}
+
 PyMethodDef kMethods[] = {
     {"entry", make_entry, METH_VARARGS, "entry(op, names, npos, defaults, required, fallback)"},
     {"launched", launched, METH_NOARGS, "launched() -> calls the fast path has launched so far"},
+    {"workspace_error", workspace_error, METH_O,
+     "workspace_error(device) -> True if a look-back wait of this module's calls gave up"},
     RLK_METHOD(gae),
     RLK_METHOD(gae_normalized),
     RLK_METHOD(vtrace),

@@ -214,13 +214,17 @@ def _workspace(dev: int, stream: int, n_env: int, n_t: int):
 
 
 def workspace_error(device=None) -> bool:
-    """True if any cached workspace on `device` recorded a look-back wait that gave up."""
+    """True if any cached workspace on `device` (this module's and the fast path's) recorded
+    a look-back wait that gave up."""
     want = None if device is None else torch.device(device).index
     for (dev, _), ws in list(_workspaces.items()):
         if want is not None and dev != want:
             continue
         if ws[24:32].cpu().view(torch.int64).item() != 0:
             return True
+    if fast is not None:
+        devs = [want] if want is not None else range(torch.cuda.device_count())
+        return any(fast.workspace_error(d) for d in devs)
     return False
 
 

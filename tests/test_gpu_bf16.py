@@ -60,8 +60,6 @@ def _bits(t):
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
 def test_bf16_is_float32_result_rounded(op, shape, path, device, monkeypatch):
     if path == "fast":
-        if shape[1] > 2048:
-            pytest.skip("the fast path declines rows that need the look-back workspace")
         monkeypatch.delenv("RL_TRITON_CORRECTNESS_WARNINGS")
     inp, params = _inputs(op, shape, seed=31)
     inp = _bf16_values(inp)

@@ -301,12 +301,15 @@ FAST_OPS = ["gae", "gae_masked", "gae_normalized", "gae_normalized_masked", "vtr
 
 
 @pytest.mark.parametrize("op", FAST_OPS)
-@pytest.mark.parametrize("shape", [(1, 1), (33, 257), (4096, 128), (16, 2048)],
+@pytest.mark.parametrize("shape", [(1, 1), (33, 257), (4096, 128), (16, 2048), (3, 5000),
+                                   (2, 131073)],
                          ids=lambda s: f"{s[0]}x{s[1]}")
 def test_fast_path_matches_python_path(op, shape, device, monkeypatch):
     """With RL_TRITON_CORRECTNESS_WARNINGS unset a well-formed call takes the C++ fast path
     (the public functions are its entries); with it set, the Python path.  Both launch the
-    same kernel with the same arguments, so the results are bit-identical."""
+    same kernel with the same arguments, so the results are bit-identical -- also for long
+    rows, where each path uses a look-back workspace of its own (the look-back gives the
+    same bits whatever the timing)."""
     from rl_triton import _native
     assert _native.fast is not None, "rl_triton._rlk_torch is not built"
     boot = ("full" if op in ("gae", "gae_masked", "gae_normalized", "gae_normalized_masked",
@@ -322,6 +325,7 @@ def test_fast_path_matches_python_path(op, shape, device, monkeypatch):
     assert _native.fast.launched() == before + 1, "the call did not take the fast path"
     for s, f in zip(slow, fast):  # bit-identical (nan where both are: one-element batch std)
         torch.testing.assert_close(s, f, rtol=0, atol=0, equal_nan=True)
+    assert not _native.workspace_error(device)
 
 
 def test_public_functions_keep_the_python_contract(device, monkeypatch):
@@ -355,7 +359,8 @@ def test_public_functions_keep_the_python_contract(device, monkeypatch):
 
 
 def test_fast_path_declines_what_it_cannot_take(device, monkeypatch):
-    """Non-contiguous inputs, long rows and the correctness flag go to the Python path."""
+    """Non-contiguous inputs, the correctness flag, and long rows inside a graph capture go
+    to the Python path (which gives a captured call a workspace of its own)."""
     from rl_triton import _native
     f = _native.fast
     x = torch.zeros(8, 64, device=device)
@@ -364,9 +369,16 @@ def test_fast_path_declines_what_it_cannot_take(device, monkeypatch):
     assert f.gae(x, x, x, None, 0.99, 0.95, None, None, None) is not None
     assert f.gae(x.t(), x.t(), x.t(), None, 0.99, 0.95, None, None, None) is None
     long = torch.zeros(2, 4096, device=device)
-    assert f.gae(long, long, long, None, 0.99, 0.95, None, None, None) is None
+    assert f.gae(long, long, long, None, 0.99, 0.95, None, None, None) is not None
     assert f.gae(x, x, x, None, 0.99, 0.95, x, torch.zeros(8, device=device), None) is None
     assert f.gae(x, x, x.double(), None, 0.99, 0.95, None, None, None) is None
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        assert f.gae(long, long, long, None, 0.99, 0.95, None, None, None) is None
+        assert f.gae(x, x, x, None, 0.99, 0.95, None, None, None) is not None
+    g.replay()
+    torch.cuda.synchronize()
 
 
 # ---------------------------------------------------------------------------------------
