@@ -456,7 +456,8 @@ def time_graph_steps(torch, rl, sets, steps):
 def time_launch_paths(torch, calls=2000):
     """The launch-bound path (the reference's ROADMAP.md:125-130 graph item): C1 [64, 512]
     GAE calls issued eagerly back to back (host-inclusive time per call) against the same
-    calls replayed from a captured HIP graph (device time per call)."""
+    calls replayed from a captured HIP graph (device time per call); and two C5 long-row
+    configurations issued eagerly back to back (host-inclusive)."""
     import baseline_configs as bc
     dev = torch.device("cuda:0")
     name = "C1_gae_64x512"
@@ -501,8 +502,30 @@ def time_launch_paths(torch, calls=2000):
         f"graph replay {graph_us:.2f} us/call")
 
     del c1
-    return {"c1_gae_64x512": {"eager_us_per_call": round(eager_us, 3),
-                              "graph_us_per_call": round(graph_us, 3)}}
+    res = {"c1_gae_64x512": {"eager_us_per_call": round(eager_us, 3),
+                             "graph_us_per_call": round(graph_us, 3)}}
+
+    # long rows (look-back workspace) issued eagerly: host-inclusive time per call, to set
+    # beside the configurations' device time
+    for name in ("C5_discounted_returns_16x131072", "C5_vtrace_16x131072"):
+        n_sets = max(2, -(-3 * MALL_BYTES // bc.set_bytes(name)) + 1)
+        sets = [bc.make(name, seed=600 + i, device=dev) for i in range(n_sets)]
+        for st in sets:
+            bc.call(name, *st)
+        torch.cuda.synchronize()
+        n = 400
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(n):
+            bc.call(name, *sets[i % n_sets])
+        b.record()
+        torch.cuda.synchronize()
+        us = 1e3 * a.elapsed_time(b) / n
+        del sets
+        log(f"[bench] {name}: eager {us:.2f} us/call (host-inclusive)")
+        res[name] = {"eager_us_per_call": round(us, 3)}
+    torch.cuda.empty_cache()
+    return res
 
 
 def cpu_baseline(torch, cpu_sets, budget_s):
