@@ -62,15 +62,22 @@ def test_more_rows_than_slots(op, shape, device):
     assert not _native.workspace_error(device)
 
 
-def test_one_workspace_across_changing_shapes(device):
+@pytest.mark.parametrize("path", ["python", "fast"])
+def test_one_workspace_across_changing_shapes(path, device, monkeypatch):
     """Calls of different shapes and ops back to back on one stream share the cached
-    workspace; each leaves it ready for the next."""
+    workspace (the Python path's, or the C++ fast path's), which grows as the shapes need;
+    each call leaves it ready for the next."""
     from rl_triton import _native
+    if path == "fast":
+        monkeypatch.delenv("RL_TRITON_CORRECTNESS_WARNINGS")
     seq = [("prefix_sum", 3, 70000), ("gae", 130, 2100), ("vtrace", 2, 131073),
            ("discounted_returns", 64, 4096), ("prefix_sum", 1, 300000), ("gae_masked", 5, 9000),
            ("retrace", 70, 2500), ("forward_scan", 9, 33333)]
+    before = _native.fast.launched() if _native.fast is not None else 0
     for i, (op, E, T) in enumerate(seq * 2):
         _check(op, E, T, seed=100 + i, device=device)
+    if path == "fast":
+        assert _native.fast.launched() - before == 2 * len(seq), "a call left the fast path"
     assert not _native.workspace_error(device)
 
 
