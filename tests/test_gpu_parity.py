@@ -170,6 +170,21 @@ def test_lookback_deterministic_and_clean(device):
     assert not _native.workspace_error(device)
 
 
+@pytest.mark.parametrize("op", OPS)
+@pytest.mark.parametrize("shape", [(4096, 128), (256, 2048), (16, 131072)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_repeat_runs_bit_identical(op, shape, device):
+    """The reference's assert_deterministic (tests/bench_utils.py:308-329): repeated calls on
+    the same inputs give the same bits, short rows and look-back rows alike."""
+    from rl_triton import _native
+    inp, params = make_inputs(op, *shape, seed=5)
+    first = [t.clone() for t in run_api(op, inp, params, device)]
+    for _ in range(2):
+        again = run_api(op, inp, params, device)
+        for a, b in zip(first, again):
+            assert torch.equal(a, b), f"{op}{shape}: repeat differs"
+    assert not _native.workspace_error(device)
+
+
 # ---------------------------------------------------------------------------------------
 # API behaviour on the GPU
 # ---------------------------------------------------------------------------------------
