@@ -77,6 +77,14 @@ const char *rlk_status_string(int status);
 /* Workspace bytes a call on [num_envs, seq_len] needs (0 when none is needed). */
 size_t rlk_workspace_bytes(int64_t num_envs, int64_t seq_len);
 
+/* For tests of the give-up path only; no counterpart in the reference.  Sets how many
+ * polls a look-back wait makes before it gives up (polls < 0: the default, about one
+ * second of polling) for the long-row calls launched after it, process-wide, and returns
+ * the previous value.  A wait that gives up sets the workspace error flag and writes NaN
+ * for its tile and every tile that chains through it; with the default it is never reached
+ * by a correct run. */
+int rlk_debug_spin_limit(int polls);
+
 /* GAE advantages.  Replaces the gae_fused_kernel launch in compute_gae
  * (src/rl_triton/ops/gae.py:164-190; kernel src/rl_triton/kernels/gae.py:62-180), and
  * its chunked fallback for seq_len > 131072 (ops/gae.py:192-215).

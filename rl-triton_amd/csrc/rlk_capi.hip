@@ -105,6 +105,9 @@ hipError_t launch_rows(const Op& op, int64_t E, int T, hipStream_t stream) {
                          dim3((unsigned)grid), dim3(NT), args, 0, stream);
 }
 
+// Polls before a look-back wait gives up (rlk_debug_spin_limit; kSpinLimit, ~1 s, otherwise).
+int g_spin_limit = kSpinLimit;
+
 // Long rows: one tile of kLongThreads * 4 * Q steps per workgroup, grid = nslots * (tiles
 // of the fullest slot) (see chain_kernel in rlk_engine.hpp).
 template <class Op, int Q, bool VEC>
@@ -115,7 +118,8 @@ hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_
   int tpr = (int)((T + tile - 1) / tile);
   const int64_t grid = chain_grid(E, T, NT, Q);
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-  void* args[] = {const_cast<Op*>(&op), &E, &T, &tpr, &ws};
+  int spin_limit = g_spin_limit;
+  void* args[] = {const_cast<Op*>(&op), &E, &T, &tpr, &ws, &spin_limit};
   return hipLaunchKernel(reinterpret_cast<const void*>(&chain_kernel<Op, NT, Q, VEC>),
                          dim3((unsigned)grid), dim3(NT), args, 0, stream);
 }
@@ -463,6 +467,12 @@ const char* rlk_status_string(int status) {
 
 size_t rlk_workspace_bytes(int64_t num_envs, int64_t seq_len) {
   return workspace_bytes(num_envs, seq_len);
+}
+
+int rlk_debug_spin_limit(int polls) {
+  const int prev = g_spin_limit;
+  g_spin_limit = polls < 0 ? kSpinLimit : polls;
+  return prev;
 }
 
 int rlk_gae(const float* rewards, const float* values, const float* terminateds,

@@ -393,6 +393,14 @@ constexpr uint32_t kAgg = 1, kInc = 2;
 constexpr uint32_t kEpochMask = 0x3fffffffu;
 constexpr int kSpinLimit = 1 << 20;  // polls before a wait gives up (~1 s), never reached when correct
 
+// The carry of a tile whose look-back gave up: NaN in every component.
+template <class S>
+__device__ __forceinline__ S nan_state();
+template <>
+__device__ __forceinline__ float nan_state<float>() { return __builtin_nanf(""); }
+template <>
+__device__ __forceinline__ NvX nan_state<NvX>() { return NvX{__builtin_nanf(""), __builtin_nanf("")}; }
+
 __device__ __forceinline__ uint64_t atomic_ld(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -705,13 +713,15 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 // Once the nearest published inclusive state X has only aggregates between it and this
 // tile, they are applied to X one at a time, nearest last, so every published X equals the
 // sequential chain X_k = A_k(X_{k+1}) however far the look-back reached: results are
-// bit-reproducible.  A bounded wait gives up (error flag, carry 0) rather than hang.
+// bit-reproducible.  A bounded wait (spin_limit polls) gives up rather than hang: it sets
+// the error flag and takes a NaN carry, so the tile's outputs, and those of every tile that
+// chains through its state, are NaN instead of plausible values.
 // The first tile of a row (in scan order) takes `row_c`, the row's own carry.
 // Tile k's status words are st[M::kWords * k + i] (kStatusWords bounds M::kWords).
 template <bool FWD, class M>
 __device__ __forceinline__ typename M::State tile_carry(M tm, typename M::State row_c, int64_t row,
                                                         int k, int tiles_per_row, uint32_t epoch,
-                                                        uint64_t* ws, int lane) {
+                                                        uint64_t* ws, int lane, int spin_limit) {
   using State = typename M::State;
   constexpr int NWD = M::kWords, NSW = M::kStateWords;
   static_assert(NWD <= kStatusWords && NSW <= NWD, "status words per tile");
@@ -779,8 +789,9 @@ __device__ __forceinline__ typename M::State tile_carry(M tm, typename M::State 
       c = x;
       break;
     }
-    if (spins >= kSpinLimit) {
+    if (spins >= spin_limit) {
       if (lane == 0) atomic_st(ws + 3, (uint64_t)1);
+      c = nan_state<State>();
       break;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -826,7 +837,7 @@ constexpr int kSeg = 4;  // steps per segment of the long-row path
 
 template <class Op, int NT, int Q, bool VEC>
 __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T, int tiles_per_row,
-                                                   uint64_t* __restrict__ ws) {
+                                                   uint64_t* __restrict__ ws, int spin_limit) {
   constexpr bool FWD = Op::kForward;
   constexpr int NW = NT / kWave;
   constexpr int WSTEPS = Q * kWave * kSeg;  // steps per wave chunk
@@ -925,7 +936,7 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
     if (wave == 0) {
       Map tm = Map::identity();
       for (int v = 0; v < NW; ++v) tm = compose(s_map[v], tm);
-      const State c = tile_carry<FWD>(tm, rc, row, k, tiles_per_row, epoch, ws, lane);
+      const State c = tile_carry<FWD>(tm, rc, row, k, tiles_per_row, epoch, ws, lane, spin_limit);
       if (lane == 0) s_carry = c;
     }
     __syncthreads();

@@ -119,3 +119,34 @@ def test_many_tiles_per_row(op, shape, device):
     from rl_triton import _native
     _check(op, *shape, seed=41, device=device)
     assert not _native.workspace_error(device)
+
+
+def test_lookback_give_up_poisons_with_nan(device):
+    """A look-back wait that gives up -- forced here from the host with a budget of zero
+    polls (rlk_debug_spin_limit), so that every tile whose predecessors are not all
+    published at its first poll gives up at once -- sets the workspace error flag and writes
+    NaN for its tile and every tile chained through it, never plausible wrong values.  Every
+    other element is still right, and nothing waits: the kernel ends normally."""
+    import torch
+    from rl_triton import _native
+    lib = _native.load()
+    op, E, T = "prefix_sum", 1, 1 << 23  # 256 tiles: most cannot see a state at their first poll
+    inp, params = _inputs(op, E, T, seed=13)
+    exp = run_oracle(op, inp, params)[0]
+    stream = torch.cuda.Stream(device)
+    prev = lib.rlk_debug_spin_limit(0)
+    try:
+        with torch.cuda.stream(stream):
+            got = run_api(op, inp, params, device)[0]
+        torch.cuda.synchronize()
+    finally:
+        lib.rlk_debug_spin_limit(-1)
+    assert prev == 1 << 20
+    key = (torch.device(device).index, stream.cuda_stream)
+    ws = _native._workspaces.pop(key)  # this stream's workspace, made for this call
+    flagged = int(ws[24:32].cpu().view(torch.int64).item()) != 0
+    g = got.cpu().numpy()
+    nan = np.isnan(g)
+    print(f"gave up: {flagged}, NaN elements: {int(nan.sum())} of {g.size}")
+    assert flagged == bool(nan.any())
+    assert_close(g[~nan], exp[~nan], 1e-5, _atol(op, inp, exp), f"{op}[{E},{T}] outside the NaN tiles")
