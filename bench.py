@@ -25,7 +25,8 @@ Printed JSON (one line, stdout):
                  non-temporal access per array per thread, 512-thread workgroups), timed
                  the same way; kernel_frac_of_ceiling = ceiling time / kernel time;
                  vtrace_pattern_sweep: the same 5r+2w kernel at 1x-64x the headline size,
-                 fitted as time = fixed_us + bytes / asymptotic_gb_s
+                 fitted as time = fixed_us + bytes / asymptotic_gb_s; every configuration
+                 below carries that fit at its bytes (stream_fit_us, frac_of_stream_fit)
   configs        the same figures for every BASELINE configuration (C1-C5,
                  tests/baseline_configs.py), each its own rotating input sets
   extensions     compute_gae_normalized (fused GAE + returns + advantage normalisation) at
@@ -655,6 +656,14 @@ def main(argv=None):
     configs_bf16 = time_configs(torch, cfg_names, dtype=torch.bfloat16) if cfg_names else None
     extensions = time_extensions(torch) if a.configs != "none" else None
     element_aligned = time_element_aligned(torch, configs) if a.configs != "none" else None
+    # every configuration against the streaming fit of this run (fixed cost + bytes / rate)
+    fit = ceiling["vtrace_pattern_sweep"]
+    for table in (configs, configs_bf16):
+        for r in (table or {}).values():
+            nbytes = r["shape"][0] * r["shape"][1] * r["bytes_per_elem"]
+            fit_us = fit["fixed_us"] + nbytes / (fit["asymptotic_gb_s"] * 1e3)
+            r["stream_fit_us"] = round(fit_us, 3)
+            r["frac_of_stream_fit"] = round(fit_us / r["device_us"], 3)
 
     # CPU leg: the float64 oracle checks set 0's outputs, then the reference's sequential
     # loops are timed on the host
