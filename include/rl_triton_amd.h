@@ -31,8 +31,8 @@
  *     stream (concurrent use races).  Calls that need no workspace ignore the argument
  *     (NULL is fine).  Layout (uint64 words): [0..7] header, word [3] the error flag --
  *     nonzero if a look-back wait gave up or the counters were not at rest (results of
- *     that call are invalid); [8..2055] 64 ticket-counter slots; then up to five status
- *     words per tile.
+ *     that call are invalid); [8..2055] 64 counter slots; then two places of up to five
+ *     status words per tile.
  *   - Return value: RLK_OK or a negative RLK_ERR_* code; rlk_status_string() names it.
  *     Empty inputs (num_envs == 0 or seq_len == 0) return RLK_OK without a launch.
  *   - bfloat16 I/O: every estimator has an `_bf16` twin whose float arrays (inputs,
@@ -77,13 +77,15 @@ const char *rlk_status_string(int status);
 /* Workspace bytes a call on [num_envs, seq_len] needs (0 when none is needed). */
 size_t rlk_workspace_bytes(int64_t num_envs, int64_t seq_len);
 
-/* For tests of the give-up path only; no counterpart in the reference.  Sets how many
- * polls a look-back wait makes before it gives up (polls < 0: the default, about one
- * second of polling) for the long-row calls launched after it, process-wide, and returns
- * the previous value.  A wait that gives up sets the workspace error flag and writes NaN
- * for its tile and every tile that chains through it; with the default it is never reached
- * by a correct run. */
-int rlk_debug_spin_limit(int polls);
+/* For tests of the look-back's rare paths only; no counterpart in the reference.  Sets,
+ * for the long-row calls launched after it (process-wide), how many polls a look-back wait
+ * makes before it gives up (give_up_polls; default about one second) and before a wait on
+ * a predecessor tile that has published nothing computes that tile itself, or a wait for
+ * a state walks further back (fallback_polls; default 256).  Negative values restore the
+ * defaults.  A wait that gives up sets the workspace error flag and writes NaN for its
+ * tile and every tile that chains through it; with the defaults a correct run never gets
+ * there.  The fallback paths give the same bits as the ordinary one.  Returns RLK_OK. */
+int rlk_debug_lookback(int give_up_polls, int fallback_polls);
 
 /* GAE advantages.  Replaces the gae_fused_kernel launch in compute_gae
  * (src/rl_triton/ops/gae.py:164-190; kernel src/rl_triton/kernels/gae.py:62-180), and

@@ -52,11 +52,12 @@ int long_segments(int64_t E, int64_t T) {
   return kMinQ;
 }
 
-// Workspace for a long-row call: status words for its tiles, counted at the smallest tile.
+// Workspace for a long-row call: two places of status words for its tiles (the tile's own,
+// and the one other workgroups publish into), counted at the smallest tile.
+int64_t status_tiles(int64_t E, int64_t T) { return E * ((T + kMinTile - 1) / kMinTile); }
 size_t workspace_bytes(int64_t E, int64_t T) {
   if (E <= 0 || T <= kShortMaxT) return 0;
-  const int64_t tiles = E * ((T + kMinTile - 1) / kMinTile);
-  return (size_t)(kStatusOffset + kStatusWords * tiles) * sizeof(uint64_t);
+  return (size_t)(kStatusOffset + 2 * kStatusWords * status_tiles(E, T)) * sizeof(uint64_t);
 }
 
 bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -105,8 +106,11 @@ hipError_t launch_rows(const Op& op, int64_t E, int T, hipStream_t stream) {
                          dim3((unsigned)grid), dim3(NT), args, 0, stream);
 }
 
-// Polls before a look-back wait gives up (rlk_debug_spin_limit; kSpinLimit, ~1 s, otherwise).
+// Look-back poll budgets (rlk_debug_lookback): polls before a wait gives up (~1 s), and
+// polls before a wait on a predecessor that has published nothing computes it instead.
+constexpr int kFallbackPolls = 256;
 int g_spin_limit = kSpinLimit;
+int g_fallback_polls = kFallbackPolls;
 
 // Long rows: one tile of kLongThreads * 4 * Q steps per workgroup, grid = nslots * (tiles
 // of the fullest slot) (see chain_kernel in rlk_engine.hpp).
@@ -118,8 +122,9 @@ hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_
   int tpr = (int)((T + tile - 1) / tile);
   const int64_t grid = chain_grid(E, T, NT, Q);
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-  int spin_limit = g_spin_limit;
-  void* args[] = {const_cast<Op*>(&op), &E, &T, &tpr, &ws, &spin_limit};
+  uint64_t* fb = ws + kStatusOffset + kStatusWords * status_tiles(E, T);
+  int spin_limit = g_spin_limit, fallback_polls = g_fallback_polls;
+  void* args[] = {const_cast<Op*>(&op), &E, &T, &tpr, &ws, &fb, &spin_limit, &fallback_polls};
   return hipLaunchKernel(reinterpret_cast<const void*>(&chain_kernel<Op, NT, Q, VEC>),
                          dim3((unsigned)grid), dim3(NT), args, 0, stream);
 }
@@ -469,10 +474,10 @@ size_t rlk_workspace_bytes(int64_t num_envs, int64_t seq_len) {
   return workspace_bytes(num_envs, seq_len);
 }
 
-int rlk_debug_spin_limit(int polls) {
-  const int prev = g_spin_limit;
-  g_spin_limit = polls < 0 ? kSpinLimit : polls;
-  return prev;
+int rlk_debug_lookback(int give_up_polls, int fallback_polls) {
+  g_spin_limit = give_up_polls < 0 ? kSpinLimit : give_up_polls;
+  g_fallback_polls = fallback_polls < 0 ? kFallbackPolls : fallback_polls;
+  return RLK_OK;
 }
 
 int rlk_gae(const float* rewards, const float* values, const float* terminateds,

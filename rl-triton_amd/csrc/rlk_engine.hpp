@@ -13,9 +13,10 @@
 //     wavefront shuffle scan (width min(L, 64)) and, when L > 64, through LDS;
 //   * short rows: a workgroup of NT threads holds NT/L whole rows, no inter-workgroup
 //     traffic;
-//   * long rows: a row is split into tiles, one per workgroup, handed out by per-slot
-//     atomic tickets in scan order and chained by a decoupled look-back over per-tile
-//     status words in a caller-provided workspace.
+//   * long rows: a row is split into tiles, one per workgroup (by block index), chained
+//     by a decoupled look-back over per-tile status words in a caller-provided workspace;
+//     a workgroup that would wait on a predecessor not yet started computes that
+//     predecessor's map itself.
 //
 // An estimator ("Op") supplies:
 //   Regs                      per-thread registers for S steps
@@ -373,16 +374,16 @@ struct Halo2 {
 //   header   [0..7]               [1] finished-slot counter, [2] epoch of the call,
 //                                 [3] error flag (a bounded wait gave up, or counters were
 //                                 not at rest); others reserved
-//   slots    [8 + 32*s], s < 64   ticket counter slot s (256 bytes each): +0 ticket,
-//                                 +16 drawn-workgroup counter (its own 128-byte line)
+//   slots    [8 + 32*s], s < 64   slot s (256 bytes each): +16 counter of the workgroups
+//                                 of rows r = s mod 64 that have started (its own line)
 //   status   [8 + 32*64 ...]      kStatusWords words per tile, tiles of row r at
-//                                 r*tiles_per_row
-// Device-scope atomics on one address serialise (~12 ns each on MI355X), so tickets come
-// from up to 64 counters: row r draws from slot r % 64, and since a tile only ever waits
-// on tiles of its own row, handing out each slot's tiles in scan order is enough for
-// forward progress.  The epoch is global and advances once per call, after every
-// workgroup has read it, so a status word left by any earlier call never matches the
-// current one.
+//                                 r*tiles_per_row: what the tile's own workgroup publishes
+//   second   [status + kStatusWords*tiles ...]  the same layout: what other workgroups
+//                                 publish for a tile they computed in its place
+// (tiles counted at the smallest tile; see rlk_workspace_bytes).  Device-scope atomics on
+// one address serialise (~12 ns each on MI355X), so the start counters are spread over 64
+// slots.  The epoch is global and advances once per call, after every workgroup has read
+// it, so a status word left by any earlier call never matches the current one.
 // ---------------------------------------------------------------------------------------
 constexpr int kHeaderWords = 8;
 constexpr int kSlots = 64;
@@ -700,33 +701,118 @@ __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T,
 // ---------------------------------------------------------------------------------------
 __host__ __device__ inline int lookback_slots(int64_t E) { return E < kSlots ? (int)E : kSlots; }
 
-__device__ __forceinline__ uint64_t draw_ticket(uint64_t* sc) {
-  return __hip_atomic_fetch_add(sc, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // s_waitcnt vmcnt(0): the look-back wave's own traffic is complete before its path rejoins
 // the other waves', so nothing it issued looks pending to the compiler afterwards.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// Carry entering tile k of `row` (one wave, all 64 lanes): publish the tile's
-// map and look back.  Predecessors are read 64 at a time (lane i <-> i+1 tiles away).
-// Once the nearest published inclusive state X has only aggregates between it and this
-// tile, they are applied to X one at a time, nearest last, so every published X equals the
-// sequential chain X_k = A_k(X_{k+1}) however far the look-back reached: results are
-// bit-reproducible.  A bounded wait (spin_limit polls) gives up rather than hang: it sets
-// the error flag and takes a NaN carry, so the tile's outputs, and those of every tile that
-// chains through its state, are NaN instead of plausible values.
+// What one look-back read finds for a tile: lane l examines tile k -/+ (1 + base + l) of
+// the row, in its own status words (st) and in those another workgroup published for it
+// (sf, see chain_kernel).  kind: 0 (nothing usable yet), kAgg or kInc; absent: nothing of
+// this call in either place (its workgroup has not published yet).
+template <class M>
+struct Probe {
+  uint32_t kind;
+  bool absent;
+  float w[M::kWords];
+};
+
+template <bool FWD, class M>
+__device__ __forceinline__ Probe<M> probe_tiles(const uint64_t* st, const uint64_t* sf, int k,
+                                                int base, int tiles_per_row, uint32_t epoch,
+                                                int lane) {
+  constexpr int NWD = M::kWords, NSW = M::kStateWords;
+  const uint32_t tag_agg = (epoch << 2) | kAgg, tag_inc = (epoch << 2) | kInc;
+  Probe<M> p;
+  p.kind = 0;
+  p.absent = false;
+#pragma unroll
+  for (int i = 0; i < NWD; ++i) p.w[i] = 0.f;
+  const int jj = FWD ? k - 1 - base - lane : k + 1 + base + lane;
+  if (FWD ? jj >= 0 : jj < tiles_per_row) {
+    // All words in flight at once.  Each word is written at most once per call, kind and
+    // place (by identical values when two workgroups write one place), so words that all
+    // carry the current AGG tag (or INC tag) are one consistent map (or state); a word
+    // with another tag just means "not yet".
+    uint64_t a[NWD], b[NWD];
+#pragma unroll
+    for (int i = 0; i < NWD; ++i) a[i] = atomic_ld(st + NWD * jj + i);
+#pragma unroll
+    for (int i = 0; i < NWD; ++i) b[i] = atomic_ld(sf + NWD * jj + i);
+    auto kind_of = [&](const uint64_t(&x)[NWD]) -> uint32_t {
+      const uint32_t tag0 = (uint32_t)(x[0] >> 32);
+      const uint32_t kd = tag0 & 3u;
+      if ((tag0 >> 2) != epoch || (kd != kAgg && kd != kInc)) return 0u;
+      const uint32_t want = kd == kAgg ? tag_agg : tag_inc;
+      const int nw = kd == kAgg ? NWD : NSW;
+#pragma unroll
+      for (int i = 1; i < NWD; ++i)
+        if (i < nw && (uint32_t)(x[i] >> 32) != want) return 0u;
+      return kd;
+    };
+    auto touched = [&](uint64_t w0) {  // word 0 (written last) names this call's publish
+      const uint32_t tag0 = (uint32_t)(w0 >> 32);
+      return (tag0 >> 2) == epoch && (tag0 & 3u) != 0u;
+    };
+    const uint32_t ka = kind_of(a), kb = kind_of(b);
+    const bool use_b = kb == kInc ? ka != kInc : (ka == 0u && kb != 0u);  // a state first
+    p.kind = use_b ? kb : ka;
+#pragma unroll
+    for (int i = 0; i < NWD; ++i) p.w[i] = __uint_as_float((uint32_t)(use_b ? b[i] : a[i]));
+    p.absent = !touched(a[0]) && !touched(b[0]);
+  }
+  return p;
+}
+
+// The state a lane's tile publishes (INC words), as seen by every lane.
+template <class M>
+__device__ __forceinline__ typename M::State probe_state(const Probe<M>& p, int l) {
+  float iw[M::kStateWords];
+#pragma unroll
+  for (int i = 0; i < M::kStateWords; ++i) iw[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p.w[i]), l));
+  return state_from_words<typename M::State>(iw);
+}
+// The map a lane's tile publishes (AGG words), as seen by every lane.
+template <class M>
+__device__ __forceinline__ M probe_map(const Probe<M>& p, int l) {
+  float aw[M::kWords];
+#pragma unroll
+  for (int i = 0; i < M::kWords; ++i) aw[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p.w[i]), l));
+  return M::from_words(aw);
+}
+
+// Carry entering tile k of `row` (one wave, all 64 lanes): publish the tile's map and look
+// back.  Predecessors are read 64 at a time (lane i <-> i+1 tiles away).  Once the nearest
+// published state X has only maps between it and this tile, they are applied to X one at a
+// time, nearest last, so every published state equals the sequential chain
+// X_k = A_k(X_{k+1}) however far the look-back reached, and whichever state it found:
+// results are bit-reproducible.
+//
+// Tiles come from the block index, not from an ordered ticket, so a predecessor's
+// workgroup may not have started.  The look-back never depends on it: after
+// `fallback_polls` polls,
+//   * a predecessor with nothing published is handed back (need = its tile): the
+//     workgroup computes that tile's map itself, publishes it in the predecessor's second
+//     place (sf), and looks back again;
+//   * a window of 64 maps and no state makes the look-back walk further back, window by
+//     window, to a state, and then apply every map from there, one by one.
+// A bounded wait (spin_limit polls in all) gives up rather than hang: it sets the error
+// flag and takes a NaN carry, so the tile's outputs, and those of every tile that chains
+// through its state, are NaN instead of plausible values.
 // The first tile of a row (in scan order) takes `row_c`, the row's own carry.
 // Tile k's status words are st[M::kWords * k + i] (kStatusWords bounds M::kWords).
 template <bool FWD, class M>
 __device__ __forceinline__ typename M::State tile_carry(M tm, typename M::State row_c, int64_t row,
                                                         int k, int tiles_per_row, uint32_t epoch,
-                                                        uint64_t* ws, int lane, int spin_limit) {
+                                                        uint64_t* ws, uint64_t* fb, int lane,
+                                                        int spin_limit, int fallback_polls,
+                                                        int& need) {
   using State = typename M::State;
   constexpr int NWD = M::kWords, NSW = M::kStateWords;
   static_assert(NWD <= kStatusWords && NSW <= NWD, "status words per tile");
   uint64_t* st = ws + kStatusOffset + NWD * (row * (int64_t)tiles_per_row);
+  const uint64_t* sf = fb + NWD * (row * (int64_t)tiles_per_row);
   const uint32_t tag_agg = (epoch << 2) | kAgg, tag_inc = (epoch << 2) | kInc;
+  need = -1;
   // word 0 last: it names the kind
   auto publish_inc = [&](State x) {
 #pragma unroll
@@ -746,59 +832,118 @@ __device__ __forceinline__ typename M::State tile_carry(M tm, typename M::State 
       for (int i = NWD - 1; i >= 0; --i) atomic_st(st + NWD * k + i, pack(tag_agg, tm.word(i)));
     }
   }
+  auto tile_at = [&](int base, int l) { return FWD ? k - 1 - base - l : k + 1 + base + l; };
+  auto first_of = [](uint64_t mask) { return mask ? __ffsll((long long)mask) - 1 : kWave; };
   State c{};
-  for (int spins = 0;; ++spins) {
-    const int jj = FWD ? k - 1 - lane : k + 1 + lane;
-    const bool inr = FWD ? (jj >= 0) : (jj < tiles_per_row);
-    uint32_t kind = 0;
-    float w[NWD];
-#pragma unroll
-    for (int i = 0; i < NWD; ++i) w[i] = 0.f;
-    if (inr) {
-      // All words in flight at once.  Each word is written at most once per call and kind,
-      // so words that all carry the current AGG tag (or INC tag) are one consistent map (or
-      // state); a word with another tag just means "not yet".
-      uint64_t raw[NWD];
-#pragma unroll
-      for (int i = 0; i < NWD; ++i) raw[i] = atomic_ld(st + NWD * jj + i);
-      const uint32_t tag0 = (uint32_t)(raw[0] >> 32);
-      if ((tag0 >> 2) == epoch) kind = tag0 & 3u;
-      const uint32_t want = kind == kAgg ? tag_agg : tag_inc;
-      const int nw = kind == kAgg ? NWD : NSW;
-#pragma unroll
-      for (int i = 1; i < NWD; ++i)
-        if (i < nw && (uint32_t)(raw[i] >> 32) != want) kind = 0;
-#pragma unroll
-      for (int i = 0; i < NWD; ++i) w[i] = __uint_as_float((uint32_t)raw[i]);
-    }
-    const uint64_t inc_mask = __ballot(kind == kInc);
-    const uint64_t bad_mask = __ballot(kind == 0);
-    const int first_inc = inc_mask ? __ffsll((long long)inc_mask) - 1 : kWave;
-    const int first_bad = bad_mask ? __ffsll((long long)bad_mask) - 1 : kWave;
+  bool done = false;
+  int spins = 0;
+  // the nearest 64 tiles
+  bool walk = false;
+  for (;; ++spins) {
+    const Probe<M> p = probe_tiles<FWD, M>(st, sf, k, 0, tiles_per_row, epoch, lane);
+    const int first_inc = first_of(__ballot(p.kind == kInc));
+    const int first_bad = first_of(__ballot(p.kind == 0u));
+    const uint64_t absent = __ballot(p.absent);
     if (first_inc < first_bad) {
-      float iw[NSW];
-#pragma unroll
-      for (int i = 0; i < NSW; ++i) iw[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[i]), first_inc));
-      State x = state_from_words<State>(iw);
-      for (int l = first_inc - 1; l >= 0; --l) {
-        float aw[NWD];
-#pragma unroll
-        for (int i = 0; i < NWD; ++i) aw[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[i]), l));
-        x = M::from_words(aw).apply(x);
-      }
+      State x = probe_state(p, first_inc);
+      for (int l = first_inc - 1; l >= 0; --l) x = probe_map(p, l).apply(x);
       c = x;
+      done = true;
       break;
     }
-    if (spins >= spin_limit) {
-      if (lane == 0) atomic_st(ws + 3, (uint64_t)1);
-      c = nan_state<State>();
-      break;
+    if (spins >= spin_limit) break;
+    if (spins >= fallback_polls) {
+      if (first_bad < kWave && ((absent >> first_bad) & 1u)) {
+        need = tile_at(0, first_bad);
+        wait_vmem();
+        return c;
+      }
+      if (first_bad == kWave) {  // 64 maps, no state: walk back
+        walk = true;
+        break;
+      }
     }
     __builtin_amdgcn_s_sleep(1);
+  }
+  if (walk) {
+    // windows further back, to the first that holds a state before anything unusable
+    int base = kWave, found = -1;
+    Probe<M> p{};
+    for (; spins < spin_limit; ++spins) {
+      p = probe_tiles<FWD, M>(st, sf, k, base, tiles_per_row, epoch, lane);
+      const int first_inc = first_of(__ballot(p.kind == kInc));
+      const int first_bad = first_of(__ballot(p.kind == 0u));
+      const uint64_t absent = __ballot(p.absent);
+      if (first_inc < first_bad) {
+        found = first_inc;
+        break;
+      }
+      if (first_bad < kWave) {
+        if ((absent >> first_bad) & 1u) {
+          need = tile_at(base, first_bad);
+          wait_vmem();
+          return c;
+        }
+        __builtin_amdgcn_s_sleep(1);  // published, not complete yet: read this window again
+        continue;
+      }
+      base += kWave;
+    }
+    if (found >= 0) {
+      // from that state, every map between it and this tile, one by one, nearest last (a
+      // tile that has published its state meanwhile gives that state: the same bits)
+      State x = probe_state(p, found);
+      for (int l = found - 1; l >= 0; --l) x = probe_map(p, l).apply(x);
+      for (base -= kWave; base >= 0 && spins < spin_limit; base -= kWave) {
+        for (; spins < spin_limit; ++spins) {
+          p = probe_tiles<FWD, M>(st, sf, k, base, tiles_per_row, epoch, lane);
+          if (__ballot(p.kind == 0u) == 0) break;
+          __builtin_amdgcn_s_sleep(1);
+        }
+        if (spins >= spin_limit) break;
+        for (int l = kWave - 1; l >= 0; --l) {
+          const uint32_t kl = (uint32_t)__builtin_amdgcn_readlane((int)p.kind, l);
+          x = kl == kInc ? probe_state(p, l) : probe_map(p, l).apply(x);
+        }
+      }
+      if (base < 0) {
+        c = x;
+        done = true;
+      }
+    }
+  }
+  if (!done) {
+    if (lane == 0) atomic_st(ws + 3, (uint64_t)1);
+    c = nan_state<State>();
   }
   wait_vmem();
   if (lane == 0 && !tm.constant()) publish_inc(tm.apply(c));
   return c;
+}
+
+// A tile's map (or, for a row's first tile or a tile whose map ignores its carry, its
+// state) computed by a workgroup that is not the tile's own: published in the tile's second
+// place, which only such workgroups write, all with the same values.
+template <bool FWD, class M>
+__device__ __forceinline__ void publish_for(M tm, typename M::State row_c, int64_t row, int k,
+                                            int tiles_per_row, uint32_t epoch, uint64_t* fb,
+                                            int lane) {
+  using State = typename M::State;
+  constexpr int NWD = M::kWords, NSW = M::kStateWords;
+  uint64_t* sf = fb + NWD * (row * (int64_t)tiles_per_row);
+  const uint32_t tag_agg = (epoch << 2) | kAgg, tag_inc = (epoch << 2) | kInc;
+  const bool first = FWD ? (k == 0) : (k == tiles_per_row - 1);
+  if (lane == 0) {
+    if (first || tm.constant()) {
+      const State x = tm.apply(first ? row_c : State{});
+#pragma unroll
+      for (int i = NSW - 1; i >= 0; --i) atomic_st(sf + NWD * k + i, pack(tag_inc, state_word(x, i)));
+    } else {
+#pragma unroll
+      for (int i = NWD - 1; i >= 0; --i) atomic_st(sf + NWD * k + i, pack(tag_agg, tm.word(i)));
+    }
+  }
+  wait_vmem();
 }
 
 // ---------------------------------------------------------------------------------------
@@ -812,13 +957,15 @@ __device__ __forceinline__ typename M::State tile_carry(M tm, typename M::State 
 // the lanes are all taken in reverse.  Each of the Q segment rows is scanned across the 64
 // lanes by DPP, and the rows are chained in scan order.
 //
-// A workgroup draws one ticket from its slot's counter (slot = blockIdx % nslots), which
-// names the tile (row, position) in scan order; it loads and scans the tile, wave 0
-// publishes the tile's map and looks back for the carry, then every thread replays and
-// stores.  A tile only waits on earlier tickets of its slot, held by workgroups that have
-// started, so any residency makes progress.  Large tiles keep the look-back chain along a
-// row short for the shapes this path serves (a few rows of 10^4..10^6 steps).
-// Launch: grid = nslots * (tiles of the fullest slot), block = NT.
+// A workgroup's tile (row, position in scan order) follows from its block index
+// (slot = blockIdx % nslots); it loads and scans the tile, wave 0 publishes the tile's map
+// and looks back for the carry, then every thread replays and stores.  Any residency makes
+// progress: when a predecessor's workgroup has published nothing after a while, the
+// look-back hands that tile back, and the workgroup loads and scans it, publishes its map
+// in the predecessor's second place, and looks back again (tile_carry).  No ordered ticket
+// is drawn, so a row's tiles do not queue on one counter.  Large tiles keep the look-back
+// chain along a row short for the shapes this path serves (a few rows of 10^4..10^6
+// steps).  Launch: grid = nslots * (tiles of the fullest slot), block = NT.
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ float lane_bcast(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
@@ -837,7 +984,8 @@ constexpr int kSeg = 4;  // steps per segment of the long-row path
 
 template <class Op, int NT, int Q, bool VEC>
 __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T, int tiles_per_row,
-                                                   uint64_t* __restrict__ ws, int spin_limit) {
+                                                   uint64_t* __restrict__ ws, uint64_t* __restrict__ fb,
+                                                   int spin_limit, int fallback_polls) {
   constexpr bool FWD = Op::kForward;
   constexpr int NW = NT / kWave;
   constexpr int WSTEPS = Q * kWave * kSeg;  // steps per wave chunk
@@ -849,7 +997,7 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
   constexpr bool HAS_HALO = !std::is_same<Halo, NoHalo>::value;
   __shared__ Map s_map[NW];
   __shared__ State s_carry;
-  __shared__ uint64_t s_q;
+  __shared__ int s_next;
   __shared__ uint32_t s_epoch;
 
   const int tid = threadIdx.x;
@@ -861,108 +1009,133 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
   uint64_t* sc = ws + kHeaderWords + kSlotWords * slot;
   const int64_t rows_in_slot = (E - slot + nslots - 1) / nslots;
   const uint64_t tiles_in_slot = (uint64_t)rows_in_slot * (uint64_t)tiles_per_row;
+  // The workgroup's tile, from its block index: slot, then position in the slot's scan
+  // order (lower block indices first, so a tile's predecessors are normally dispatched
+  // before it; the look-back does not rely on that).
+  const uint64_t q_t = blockIdx.x / (unsigned)nslots;
 
-  if (tid == 0) {
-    s_q = draw_ticket(sc);
-    s_epoch = (uint32_t)atomic_ld(ws + 2) & kEpochMask;
-  }
-  __syncthreads();
-  const uint64_t q_t = s_q;
-  const uint32_t epoch = s_epoch;
-  // Each workgroup draws exactly one ticket, so the slot's last drawer is known the moment
-  // it draws: having read the epoch (above), every workgroup counts itself drawn, and the
-  // one that completes the count resets the slot (and, last of all slots, advances the
-  // epoch) when it finishes.  The count's result is only read at the end, by which time
-  // it has returned, so no workgroup waits on an atomic on its way out.
-  uint64_t drawn = 0;
-  if (tid == 0) {
-    if (q_t >= wgs_per_slot) atomic_st(ws + 3, (uint64_t)1);  // counters were not at rest
+  // The epoch is read first and used once the tile's loads are in flight.  Every workgroup
+  // counts itself in the slot's counter once it has the epoch; the one that completes the
+  // count resets it (and, last of all slots, advances the epoch) when it finishes, after
+  // every workgroup of the call has read the epoch.  The count's result is only read at the
+  // end, so no workgroup waits on an atomic on its way out.
+  uint64_t e_raw = 0, drawn = 0;
+  if (tid == 0) e_raw = atomic_ld(ws + 2);
+  auto count_drawn = [&]() {
     drawn = __hip_atomic_fetch_add(sc + 16, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+    if (drawn >= wgs_per_slot) atomic_st(ws + 3, (uint64_t)1);  // counters were not at rest
+  };
 
   Stats st;  // output statistics (ops with kBlockStats)
   if (q_t < tiles_in_slot) {
     const int64_t lr = (int64_t)(q_t / (uint64_t)tiles_per_row);
-    const int j = (int)(q_t - (uint64_t)lr * tiles_per_row);
+    const int jpos = (int)(q_t - (uint64_t)lr * tiles_per_row);
     const int64_t row = slot + (int64_t)nslots * lr;
-    const int k = FWD ? j : tiles_per_row - 1 - j;
-    // lane space -> time: this wave's chunk, and the first step of segment row r
-    const int wbase = (k * NW + (FWD ? wave : NW - 1 - wave)) * WSTEPS;
-    const int lt = FWD ? lane : kWave - 1 - lane;
-    auto seg_t0 = [&](int r) { return wbase + ((FWD ? r : Q - 1 - r) * kWave + lt) * kSeg; };
+    const int k_own = FWD ? jpos : tiles_per_row - 1 - jpos;
+    // Tile k_own, or first a predecessor the look-back hands back (its map computed here,
+    // then this tile again from its loads).
+    for (int k = k_own, it = 0;; ++it) {
+      // lane space -> time: this wave's chunk, and the first step of segment row r
+      const int wbase = (k * NW + (FWD ? wave : NW - 1 - wave)) * WSTEPS;
+      const int lt = FWD ? lane : kWave - 1 - lane;
+      auto seg_t0 = [&](int r) { return wbase + ((FWD ? r : Q - 1 - r) * kWave + lt) * kSeg; };
 
-    // loads: Q segments, plus the neighbour step before the chunk in scan order
-    Regs R[Q];
+      // loads: Q segments, plus the neighbour step before the chunk in scan order
+      Regs R[Q];
 #pragma unroll
-    for (int r = 0; r < Q; ++r) op.template load<kSeg, VEC>(row, seg_t0(r), T, R[r]);
-    Halo edge{};
-    if constexpr (HAS_HALO) {
-      if (lane == 0 && (FWD ? wbase > 0 : wbase + WSTEPS < T))
-        edge = op.halo_load(row, clamp_step(FWD ? wbase - 1 : wbase + WSTEPS, T), T);
-    }
-    const bool first = FWD ? (k == 0) : (k == tiles_per_row - 1);
-    const State rc = (first && wave == 0) ? row_carry(op, row, T) : State{};
-
-#pragma unroll
-    for (int r = 0; r < Q; ++r) op.template prepare<kSeg, VEC>(R[r], row, seg_t0(r), T);
-
-    // neighbour step of each segment (the one before it in scan order): the previous lane,
-    // lane 63 of the previous segment row, or the edge load
-    Halo h[Q];
-#pragma unroll
-    for (int r = 0; r < Q; ++r) {
+      for (int r = 0; r < Q; ++r) op.template load<kSeg, VEC>(row, seg_t0(r), T, R[r]);
+      Halo edge{};
       if constexpr (HAS_HALO) {
-        const Halo prev = lane_prev(scan_export<Op, kSeg>(op, R[r]));
-        const Halo wrap = r > 0 ? lane_bcast(scan_export<Op, kSeg>(op, R[r > 0 ? r - 1 : 0]), kWave - 1) : edge;
-        h[r] = lane == 0 ? wrap : prev;
+        if (lane == 0 && (FWD ? wbase > 0 : wbase + WSTEPS < T))
+          edge = op.halo_load(row, clamp_step(FWD ? wbase - 1 : wbase + WSTEPS, T), T);
       }
-    }
+      const bool first = FWD ? (k == 0) : (k == tiles_per_row - 1);
+      const State rc = (first && wave == 0) ? row_carry(op, row, T) : State{};
+      if (it == 0 && tid == 0) {  // the epoch load was issued first: it is back by now
+        s_epoch = (uint32_t)e_raw & kEpochMask;
+        count_drawn();
+      }
 
-    Map steps[Q][kSeg];
-    Map m[Q];
-    Map rowagg[Q];  // map of each segment row (wave-uniform)
 #pragma unroll
-    for (int r = 0; r < Q; ++r) {
-      op.template coef<kSeg, VEC>(R[r], h[r], row, seg_t0(r), T, steps[r]);
-      m[r] = lane_scan(fold_segment<FWD, kSeg>(steps[r]), kWave);
-      rowagg[r] = lane_bcast(m[r], kWave - 1);
-    }
-    // the chunk's map: segment rows composed in scan order
-    Map wm = Map::identity();
+      for (int r = 0; r < Q; ++r) op.template prepare<kSeg, VEC>(R[r], row, seg_t0(r), T);
+
+      // neighbour step of each segment (the one before it in scan order): the previous lane,
+      // lane 63 of the previous segment row, or the edge load
+      Halo h[Q];
 #pragma unroll
-    for (int r = 0; r < Q; ++r) wm = compose(rowagg[r], wm);
-    if (lane == 0) s_map[wave] = wm;
-    __syncthreads();
-    if (wave == 0) {
-      Map tm = Map::identity();
-      for (int v = 0; v < NW; ++v) tm = compose(s_map[v], tm);
-      const State c = tile_carry<FWD>(tm, rc, row, k, tiles_per_row, epoch, ws, lane, spin_limit);
-      if (lane == 0) s_carry = c;
-    }
-    __syncthreads();
-    // state entering this wave's chunk, then each segment row, then each lane
-    State carry = s_carry;
-    for (int v = 0; v < wave; ++v) carry = s_map[v].apply(carry);
+      for (int r = 0; r < Q; ++r) {
+        if constexpr (HAS_HALO) {
+          const Halo prev = lane_prev(scan_export<Op, kSeg>(op, R[r]));
+          const Halo wrap = r > 0 ? lane_bcast(scan_export<Op, kSeg>(op, R[r > 0 ? r - 1 : 0]), kWave - 1) : edge;
+          h[r] = lane == 0 ? wrap : prev;
+        }
+      }
+
+      Map steps[Q][kSeg];
+      Map m[Q];
+      Map rowagg[Q];  // map of each segment row (wave-uniform)
 #pragma unroll
-    for (int r = 0; r < Q; ++r) {
-      State x_in = lane_prev(m[r].apply(carry));
-      if (lane == 0) x_in = carry;
-      carry = rowagg[r].apply(carry);
-      State xs[kSeg];
-      replay<FWD, kSeg>(steps[r], x_in, xs);
-      op.template emit<kSeg, VEC>(R[r], h[r], xs, x_in, row, seg_t0(r), T);
-      if constexpr (Op::kBlockStats) op.template stats<kSeg>(R[r], xs, seg_t0(r), T, st);
+      for (int r = 0; r < Q; ++r) {
+        op.template coef<kSeg, VEC>(R[r], h[r], row, seg_t0(r), T, steps[r]);
+        m[r] = lane_scan(fold_segment<FWD, kSeg>(steps[r]), kWave);
+        rowagg[r] = lane_bcast(m[r], kWave - 1);
+      }
+      // the chunk's map: segment rows composed in scan order
+      Map wm = Map::identity();
+#pragma unroll
+      for (int r = 0; r < Q; ++r) wm = compose(rowagg[r], wm);
+      if (lane == 0) s_map[wave] = wm;
+      __syncthreads();
+      const uint32_t epoch = s_epoch;
+      if (wave == 0) {
+        Map tm = Map::identity();
+        for (int v = 0; v < NW; ++v) tm = compose(s_map[v], tm);
+        if (k != k_own) {
+          publish_for<FWD>(tm, rc, row, k, tiles_per_row, epoch, fb, lane);
+          if (lane == 0) s_next = k_own;
+        } else {
+          int need;
+          const State c = tile_carry<FWD>(tm, rc, row, k, tiles_per_row, epoch, ws, fb, lane,
+                                          spin_limit, fallback_polls, need);
+          if (lane == 0) {
+            s_carry = c;
+            s_next = need;
+          }
+        }
+      }
+      __syncthreads();
+      const int next = s_next;
+      if (k != k_own || next >= 0) {
+        k = k != k_own ? k_own : next;
+        continue;
+      }
+      // state entering this wave's chunk, then each segment row, then each lane
+      State carry = s_carry;
+      for (int v = 0; v < wave; ++v) carry = s_map[v].apply(carry);
+#pragma unroll
+      for (int r = 0; r < Q; ++r) {
+        State x_in = lane_prev(m[r].apply(carry));
+        if (lane == 0) x_in = carry;
+        carry = rowagg[r].apply(carry);
+        State xs[kSeg];
+        replay<FWD, kSeg>(steps[r], x_in, xs);
+        op.template emit<kSeg, VEC>(R[r], h[r], xs, x_in, row, seg_t0(r), T);
+        if constexpr (Op::kBlockStats) op.template stats<kSeg>(R[r], xs, seg_t0(r), T, st);
+      }
+      break;
     }
+  } else if (tid == 0) {
+    s_epoch = (uint32_t)e_raw & kEpochMask;
+    count_drawn();
   }
   if constexpr (Op::kBlockStats) block_stats<NT>(st, op.partials);
   if (tid == 0 && drawn == wgs_per_slot - 1) {
-    atomic_st(sc + 0, 0);
     atomic_st(sc + 16, 0);
     const uint64_t slots_done =
         __hip_atomic_fetch_add(ws + 1, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (slots_done == (uint64_t)nslots - 1) {
       atomic_st(ws + 1, 0);
-      atomic_st(ws + 2, (uint64_t)((epoch + 1) & kEpochMask));
+      atomic_st(ws + 2, (uint64_t)((s_epoch + 1) & kEpochMask));
     }
   }
 }

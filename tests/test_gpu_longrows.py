@@ -123,7 +123,7 @@ def test_many_tiles_per_row(op, shape, device):
 
 def test_lookback_give_up_poisons_with_nan(device):
     """A look-back wait that gives up -- forced here from the host with a budget of zero
-    polls (rlk_debug_spin_limit), so that every tile whose predecessors are not all
+    polls (rlk_debug_lookback), so that every tile whose predecessors are not all
     published at its first poll gives up at once -- sets the workspace error flag and writes
     NaN for its tile and every tile chained through it, never plausible wrong values.  Every
     other element is still right, and nothing waits: the kernel ends normally."""
@@ -134,14 +134,13 @@ def test_lookback_give_up_poisons_with_nan(device):
     inp, params = _inputs(op, E, T, seed=13)
     exp = run_oracle(op, inp, params)[0]
     stream = torch.cuda.Stream(device)
-    prev = lib.rlk_debug_spin_limit(0)
+    assert lib.rlk_debug_lookback(0, -1) == 0
     try:
         with torch.cuda.stream(stream):
             got = run_api(op, inp, params, device)[0]
         torch.cuda.synchronize()
     finally:
-        lib.rlk_debug_spin_limit(-1)
-    assert prev == 1 << 20
+        lib.rlk_debug_lookback(-1, -1)
     key = (torch.device(device).index, stream.cuda_stream)
     ws = _native._workspaces.pop(key)  # this stream's workspace, made for this call
     flagged = int(ws[24:32].cpu().view(torch.int64).item()) != 0
@@ -150,3 +149,33 @@ def test_lookback_give_up_poisons_with_nan(device):
     print(f"gave up: {flagged}, NaN elements: {int(nan.sum())} of {g.size}")
     assert flagged == bool(nan.any())
     assert_close(g[~nan], exp[~nan], 1e-5, _atol(op, inp, exp), f"{op}[{E},{T}] outside the NaN tiles")
+
+
+@pytest.mark.parametrize("op,shape", [("prefix_sum", (1, 1 << 23)), ("vtrace", (1, 1 << 21)),
+                                      ("gae_masked", (2, 1 << 19)), ("retrace", (3, 70000)),
+                                      ("discounted_returns", (16, 131072)),
+                                      ("backward_scan", (1, 3 << 20))],
+                         ids=lambda v: v if isinstance(v, str) else f"{v[0]}x{v[1]}")
+def test_lookback_fallback_paths_give_the_same_bits(op, shape, device):
+    """With the fallback budget at zero polls (rlk_debug_lookback), a tile whose predecessor
+    has published nothing at its first poll computes that predecessor itself, and a window
+    of maps with no state sends the look-back further back at once -- the paths a call
+    only takes when some workgroup of it is not running.  The results equal the ordinary
+    run's bit for bit, and the oracle's."""
+    import torch
+    from rl_triton import _native
+    lib = _native.load()
+    inp, params = _inputs(op, *shape, seed=57)
+    plain = [t.clone() for t in run_api(op, inp, params, device)]
+    assert lib.rlk_debug_lookback(-1, 0) == 0
+    try:
+        forced = run_api(op, inp, params, device)
+        torch.cuda.synchronize()
+    finally:
+        lib.rlk_debug_lookback(-1, -1)
+    for name, a, b in zip(OUTPUTS[op], plain, forced):
+        assert torch.equal(a, b), f"{op}{shape}:{name} differs under the fallback paths"
+    exp = run_oracle(op, inp, params)
+    for name, g, e in zip(OUTPUTS[op], forced, exp):
+        assert_close(g.cpu().numpy(), e, 1e-5, _atol(op, inp, e), f"{op}{shape}:{name}")
+    assert not _native.workspace_error(device)
