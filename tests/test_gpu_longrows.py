@@ -1,7 +1,8 @@
 """The look-back path (rows longer than 2048 steps) in the layouts the BASELINE shapes do not
-reach: more rows than ticket slots (64), so that several rows share a slot's counter and
-its tickets run row after row; one workspace serving calls of changing shapes in stream
-order; and every op at those shapes.  Against the float64 oracle with the long-row
+reach: more rows than counter slots (64), so that several rows share a slot; rows of many
+tiles; one workspace serving calls of changing shapes in stream order; two streams at once;
+the rare paths (a predecessor computed in its workgroup's place, a walk back past 64 tiles,
+a wait that gives up) forced from the host; and every op at those shapes.  Against the float64 oracle with the long-row
 tolerance of test_gpu_parity.py (atol = 1e-5 * sqrt(L_eff / 128) * max(1, max|expected|)),
 and no look-back wait may give up (the workspace error flag stays clear).
 """
@@ -83,10 +84,10 @@ def test_one_workspace_across_changing_shapes(path, device, monkeypatch):
 
 def test_concurrent_streams(device):
     """Long-row calls queued on two streams at once, with no synchronisation between them:
-    each stream has its own workspace (ticket counters, epoch and status words), and the two
-    grids may share the GPU in any proportion, so a tile can wait on a predecessor whose
-    workgroup is not resident yet (tickets order each row's tiles by start).  Every result
-    matches the oracle and no wait gives up."""
+    each stream has its own workspace (counters, epoch and status words), and the two grids
+    may share the GPU in any proportion, so a tile can wait on a predecessor whose
+    workgroup is not resident yet (the look-back then computes that predecessor itself).
+    Every result matches the oracle and no wait gives up."""
     import torch
     from rl_triton import _native
     jobs = [[("prefix_sum", 4, 150000), ("discounted_returns", 3, 200001), ("vtrace", 2, 131072)],
