@@ -180,3 +180,15 @@ def test_lookback_fallback_paths_give_the_same_bits(op, shape, device):
     for name, g, e in zip(OUTPUTS[op], forced, exp):
         assert_close(g.cpu().numpy(), e, 1e-5, _atol(op, inp, e), f"{op}{shape}:{name}")
     assert not _native.workspace_error(device)
+
+
+@pytest.mark.parametrize("op,shape", [("vtrace", (2048, 16384)), ("prefix_sum", (1024, 1 << 16)),
+                                      ("gae_masked", (600, 12000))],
+                         ids=lambda v: v if isinstance(v, str) else f"{v[0]}x{v[1]}")
+def test_grids_larger_than_the_gpu(op, shape, device):
+    """Thousands of multi-tile rows: far more workgroups than the GPU holds at once, so tiles
+    wait on predecessors that may not have started; every result matches the oracle and no
+    wait gives up."""
+    from rl_triton import _native
+    _check(op, *shape, seed=73, device=device)
+    assert not _native.workspace_error(device)
