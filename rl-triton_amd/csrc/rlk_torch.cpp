@@ -115,8 +115,12 @@ struct Call {
 // call for the next.  Calls on one stream are ordered, so one buffer serves them all, and
 // the caching allocator keeps a replaced buffer until the stream's earlier work is done.
 // (The Python path keeps workspaces of its own; a workspace is only ever shared by calls
-// on one stream, whichever path they take.)  The GIL guards the map.
-std::map<std::pair<int, uintptr_t>, at::Tensor> g_workspaces;
+// on one stream, whichever path they take.)  The GIL guards the map.  It is never
+// destroyed: tensors must not be freed after the HIP allocator has gone at process exit.
+std::map<std::pair<int, uintptr_t>, at::Tensor>& workspaces() {
+  static auto* m = new std::map<std::pair<int, uintptr_t>, at::Tensor>();
+  return *m;
+}
 
 struct Workspace {
   void* ptr = nullptr;
@@ -135,7 +139,7 @@ Workspace workspace(const Call& c, const at::Tensor& like) {
     w.ok = false;
     return w;
   }
-  at::Tensor& buf = g_workspaces[{(int)c.dev, reinterpret_cast<uintptr_t>(s)}];
+  at::Tensor& buf = workspaces()[{(int)c.dev, reinterpret_cast<uintptr_t>(s)}];
   if (!buf.defined() || (size_t)buf.numel() < need) {
     size_t size = buf.defined() ? std::max(need, 2 * (size_t)buf.numel()) : need;
     size = (size + 255) / 256 * 256;
@@ -614,7 +618,7 @@ PyObject* workspace_error(PyObject*, PyObject* arg) {
   const long dev = PyLong_AsLong(arg);
   if (dev == -1 && PyErr_Occurred()) return nullptr;
   try {
-    for (auto& kv : g_workspaces) {
+    for (auto& kv : workspaces()) {
       if (kv.first.first != dev || !kv.second.defined()) continue;
       const at::Tensor flag = kv.second.narrow(0, 3 * 8, 8).to(at::kCPU);
       const uint8_t* b = flag.data_ptr<uint8_t>();
