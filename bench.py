@@ -581,7 +581,7 @@ def main(argv=None):
         return 0
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(rows are independent; sharding is described in DESIGN.md). Run with --gpus 1.",
+              "(rows are independent and would shard along num_envs with no exchange). Run with --gpus 1.",
               file=sys.stderr)
         return 2
 
