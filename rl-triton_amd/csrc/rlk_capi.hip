@@ -2,6 +2,8 @@
 // include/rl_triton_amd.h): argument checks, launch planning and kernel launches.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include "rl_triton_amd.h"
 #include "rlk_ops.hpp"
 
@@ -25,18 +27,19 @@ int ceil_log2(int64_t x) {
   return k;
 }
 
-// Compute units of the current device (cached; 256 on MI355X).
+// Compute units of the current device (cached per device; 256 on MI355X).  Threads that
+// race on the first call store the same value.
 int device_cus() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       n = 256;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 // Long rows: segments per thread.  Tiles are as large as the op's registers allow while
@@ -109,8 +112,8 @@ hipError_t launch_rows(const Op& op, int64_t E, int T, hipStream_t stream) {
 // Look-back poll budgets (rlk_debug_lookback): polls before a wait gives up (~1 s), and
 // polls before a wait on a predecessor that has published nothing computes it instead.
 constexpr int kFallbackPolls = 256;
-int g_spin_limit = kSpinLimit;
-int g_fallback_polls = kFallbackPolls;
+std::atomic<int> g_spin_limit{kSpinLimit};
+std::atomic<int> g_fallback_polls{kFallbackPolls};
 
 // Long rows: one tile of kLongThreads * 4 * Q steps per workgroup, grid = nslots * (tiles
 // of the fullest slot) (see chain_kernel in rlk_engine.hpp).
@@ -123,7 +126,8 @@ hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_
   const int64_t grid = chain_grid(E, T, NT, Q);
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   uint64_t* fb = ws + kStatusOffset + kStatusWords * status_tiles(E, T);
-  int spin_limit = g_spin_limit, fallback_polls = g_fallback_polls;
+  int spin_limit = g_spin_limit.load(std::memory_order_relaxed);
+  int fallback_polls = g_fallback_polls.load(std::memory_order_relaxed);
   void* args[] = {const_cast<Op*>(&op), &E, &T, &tpr, &ws, &fb, &spin_limit, &fallback_polls};
   return hipLaunchKernel(reinterpret_cast<const void*>(&chain_kernel<Op, NT, Q, VEC>),
                          dim3((unsigned)grid), dim3(NT), args, 0, stream);
@@ -475,8 +479,8 @@ size_t rlk_workspace_bytes(int64_t num_envs, int64_t seq_len) {
 }
 
 int rlk_debug_lookback(int give_up_polls, int fallback_polls) {
-  g_spin_limit = give_up_polls < 0 ? kSpinLimit : give_up_polls;
-  g_fallback_polls = fallback_polls < 0 ? kFallbackPolls : fallback_polls;
+  g_spin_limit.store(give_up_polls < 0 ? kSpinLimit : give_up_polls, std::memory_order_relaxed);
+  g_fallback_polls.store(fallback_polls < 0 ? kFallbackPolls : fallback_polls, std::memory_order_relaxed);
   return RLK_OK;
 }
 
