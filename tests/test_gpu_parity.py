@@ -445,8 +445,10 @@ def test_gae_normalized_full_size_and_repeatable(device):
     assert torch.equal(got[0], again[0]) and torch.equal(got[1], again[1])
 
 
+@pytest.mark.filterwarnings("ignore:std\\(\\):UserWarning")
 def test_gae_normalized_single_element_is_nan_like_torch(device):
-    """The unbiased std of one element is nan in torch; so are the normalised advantages."""
+    """The unbiased std of one element is nan in torch (which warns about it, as expected
+    here); so are the normalised advantages."""
     import rl_triton
     x = torch.ones(1, 1, device=device)
     adv, ret = rl_triton.compute_gae_normalized(x, x, torch.zeros_like(x))
