@@ -8,6 +8,11 @@ Every function takes float32 (int64 for Retrace actions) NumPy arrays shaped
 like the rl_triton API arguments and returns float64 arrays computed by a
 sequential double-precision loop that restates the reference's own PyTorch
 test loops (see the file:line citations in rlk_oracle.c).
+
+``loop32`` is the other kind: the reference's float32 torch
+loops restated in C with the same operation order and rounding
+(rlk_loops_f32.c), returning float32 arrays.  They measure the error level of
+"the reference's float32 sequential loop" at full size in milliseconds.
 """
 from __future__ import annotations
 
@@ -39,6 +44,16 @@ _SIGS = {
     "orc_discounted_returns": [_I64, _I64, _P, _P, _P, _P, _INT, _D, _P],
     "orc_eligibility_traces": [_I64, _I64, _P, _P, _D, _D, _P, _P],
     "orc_prefix_sum": [_I64, _I64, _P, _P, _P, _INT, _P],
+    # float32 loops (rlk_loops_f32.c)
+    "f32_gae": [_I64, _I64, _P, _P, _P, _P, _P, _INT, _D, _D, _P],
+    "f32_vtrace": [_I64, _I64, _P, _P, _P, _P, _P, _P, _D, _D, _D, _P, _P],
+    "f32_retrace": [_I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _D, _D, _D, _D, _P, _P],
+    "f32_lambda_returns": [_I64, _I64, _P, _P, _P, _P, _P, _INT, _D, _D, _P],
+    "f32_discounted_returns": [_I64, _I64, _P, _P, _P, _P, _INT, _D, _P],
+    "f32_eligibility_traces": [_I64, _I64, _P, _P, _D, _D, _P, _P],
+    "f32_prefix_sum": [_I64, _I64, _P, _P, _P, _INT, _P],
+    "f32_backward_scan": [_I64, _I64, _P, _P, _P, _P],
+    "f32_forward_scan": [_I64, _I64, _P, _P, _P, _P],
 }
 
 
@@ -193,3 +208,91 @@ def episodic_prefix_sum(inputs, dones, seed_values=None, boundary="ends_at"):
     _load().orc_prefix_sum(E, T, _ptr(x), _ptr(d), _ptr(s), int(boundary == "ends_at"),
                            _ptr(out))
     return out
+
+
+# ---------------------------------------------------------------------------------------
+# the reference's float32 sequential loops (rlk_loops_f32.c): float32 results
+# ---------------------------------------------------------------------------------------
+def loop32(op, inp, params):
+    """The float32 loop of `op` on a case dict (the keys of the rl_triton API arguments),
+    as a tuple of float32 arrays in the order of the API's outputs."""
+    g = inp.get
+    lib = _load()
+    if op == "gae":
+        r, v, te, tr = map(_f32, (g("rewards"), g("values"), g("terminateds"), g("truncateds")))
+        E, T = r.shape
+        b, mode = _boot(g("last_value") if g("last_value") is not None else g("bootstrap_values"), E, T)
+        out = np.empty((E, T), np.float32)
+        lib.f32_gae(E, T, _ptr(r), _ptr(v), _ptr(te), _ptr(tr), _ptr(b), mode,
+                    params["gamma"], params["lambda_"], _ptr(out))
+        return (out,)
+    if op == "vtrace":
+        if g("truncateds") is not None or g("bootstrap_values") is not None:
+            raise ValueError("the reference's float32 V-trace loop takes last_value only")
+        lpt, lpb, v, r, te, lv = map(_f32, (g("log_pi_target"), g("log_pi_behavior"), g("values"),
+                                            g("rewards"), g("terminateds"), g("last_value")))
+        E, T = r.shape
+        tg, adv = np.empty((E, T), np.float32), np.empty((E, T), np.float32)
+        lib.f32_vtrace(E, T, _ptr(lpt), _ptr(lpb), _ptr(v), _ptr(r), _ptr(te), _ptr(lv),
+                       params["gamma"], params.get("rho_bar", 1.0), params.get("c_bar", 1.0),
+                       _ptr(tg), _ptr(adv))
+        return tg, adv
+    if op == "retrace":
+        pi, mu, q, nq, r, te, tr = map(_f32, (g("action_probs_target"), g("action_probs_behavior"),
+                                              g("q_values"), g("next_q_values_all"), g("rewards"),
+                                              g("terminateds"), g("truncateds")))
+        act = np.ascontiguousarray(np.asarray(g("actions"), dtype=np.int64))
+        E, T, A = pi.shape
+        tg, adv = np.empty((E, T), np.float32), np.empty((E, T), np.float32)
+        lib.f32_retrace(E, T, A, _ptr(pi), _ptr(mu), _ptr(q), _ptr(nq), _ptr(act), _ptr(r),
+                        _ptr(te), _ptr(tr), params["gamma"], params.get("lambda_", 1.0),
+                        params.get("c_bar", 1.0), params.get("rho_bar", 1.0), _ptr(tg), _ptr(adv))
+        return tg, adv
+    if op == "lambda_returns":
+        r, nv, te, tr = map(_f32, (g("rewards"), g("next_values"), g("terminateds"), g("truncateds")))
+        E, T = r.shape
+        b, mode = _boot(g("bootstrap_values"), E, T)
+        out = np.empty((E, T), np.float32)
+        lib.f32_lambda_returns(E, T, _ptr(r), _ptr(nv), _ptr(te), _ptr(tr), _ptr(b), mode,
+                               params["gamma"], params["lambda_"], _ptr(out))
+        return (out,)
+    if op == "discounted_returns":
+        r, te, tr = map(_f32, (g("rewards"), g("terminateds"), g("truncateds")))
+        E, T = r.shape
+        b, mode = _boot(g("bootstrap_values"), E, T)
+        out = np.empty((E, T), np.float32)
+        lib.f32_discounted_returns(E, T, _ptr(r), _ptr(te), _ptr(tr), _ptr(b), mode,
+                                   params["gamma"], _ptr(out))
+        return (out,)
+    if op == "eligibility_traces":
+        x, d, s = map(_f32, (g("gradients"), g("dones"), g("seed_values")))
+        E, T = x.shape
+        out = np.empty((E, T), np.float32)
+        lib.f32_eligibility_traces(E, T, _ptr(x), _ptr(d), params["gamma"], params["lambda_"],
+                                   _ptr(s), _ptr(out))
+        return (out,)
+    if op == "prefix_sum":
+        x, d, s = map(_f32, (g("inputs"), g("dones"), g("seed_values")))
+        E, T = x.shape
+        out = np.empty((E, T), np.float32)
+        lib.f32_prefix_sum(E, T, _ptr(x), _ptr(d), _ptr(s),
+                           int(params.get("boundary", "ends_at") == "ends_at"), _ptr(out))
+        return (out,)
+    if op in ("backward_scan", "forward_scan"):
+        u, v = _f32(g("u")), _f32(g("v"))
+        c = _f32(g("bootstrap") if op == "backward_scan" else g("seed"))
+        E, T = u.shape
+        out = np.empty((E, T), np.float32)
+        fn = lib.f32_backward_scan if op == "backward_scan" else lib.f32_forward_scan
+        fn(E, T, _ptr(u), _ptr(v), _ptr(c), _ptr(out))
+        return (out,)
+    raise KeyError(op)
+
+
+def has_loop32(op, inp) -> bool:
+    """Whether the reference has a float32 loop for this call (its V-trace loop takes no
+    truncations and no per-step bootstrap)."""
+    if op == "vtrace":
+        return inp.get("truncateds") is None and inp.get("bootstrap_values") is None
+    return op in ("gae", "retrace", "lambda_returns", "discounted_returns", "eligibility_traces",
+                  "prefix_sum", "backward_scan", "forward_scan")

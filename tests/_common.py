@@ -263,6 +263,28 @@ def make_inputs(op, n_env, n_t, seed=0, p_term=0.05, p_trunc=0.0, boot="none", n
     return out, params
 
 
+def suite_atol(op, inp, expected, seq_len):
+    """The suite's absolute tolerance against the float64 oracle for one output: 1e-5 for
+    rows of up to 2048 steps; for longer rows (the look-back path)
+    1e-5 * sqrt(L_eff / 128) * max(1, max|expected|), with L_eff = 1 / (1 - decay) for
+    decaying scans (gamma = 0.99, lambda = 0.95) and the longest done-free run for the
+    prefix sum."""
+    import math
+    if seq_len <= 2048:
+        return 1e-5
+    scale = max(1.0, float(np.max(np.abs(expected))))
+    if op == "prefix_sum":
+        l_eff = 1
+        for row in np.asarray(inp["dones"]) > 0:
+            idx = np.flatnonzero(np.concatenate(([True], row, [True])))
+            l_eff = max(l_eff, int(np.max(np.diff(idx))))
+    elif op in ("discounted_returns", "backward_scan", "forward_scan"):
+        l_eff = 1.0 / (1.0 - 0.99)
+    else:
+        l_eff = 1.0 / (1.0 - 0.99 * 0.95)
+    return 1e-5 * math.sqrt(max(l_eff, 128) / 128.0) * scale
+
+
 def max_abs_err(actual, expected):
     a = np.asarray(actual, dtype=np.float64)
     e = np.asarray(expected, dtype=np.float64)

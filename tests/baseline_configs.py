@@ -104,6 +104,47 @@ def make(name: str, seed: int = 0, device="cpu", shape=None):
     raise KeyError(name)
 
 
+def make_exact(name: str, seed: int = 0, device="cpu"):
+    """Configuration `name` at its full shape and done/truncation distributions, with inputs
+    on which float32 arithmetic is exact in any order: integer rewards, values and
+    bootstraps in [-3, 3], unit discounts (gamma = lambda = 1), V-trace log-ratios >= 0 with
+    rho_bar = 0.5 and c_bar = 1 (so rho = 0.5 and c = 1 at every step: the two clips
+    differ), Retrace with pi = [0.25, 0.75], mu = 0.125 (ratios 2 and 6, clipped to
+    c = 1, rho = 0.5).  Every partial result is then a multiple of 1/8 below 2^21 in
+    magnitude, so a correct kernel equals the float64 oracle bit for bit whatever its
+    association order, and any error in indexing, done gating or carry passing shows as a
+    difference."""
+    op, E, T, _ = CONFIGS[name]
+    inp, params = make(name, seed=seed, device=device)
+    g = torch.Generator(device=device).manual_seed(seed + 7)
+    ri = lambda *s: torch.randint(-3, 4, s, generator=g, device=device).float()  # noqa: E731
+    for k in ("rewards", "values", "gradients", "inputs", "q_values"):
+        if k in inp:
+            inp[k] = ri(E, T)
+    if "last_value" in inp:
+        inp["last_value"] = ri(E)
+    if "bootstrap_values" in inp:
+        inp["bootstrap_values"] = torch.where(inp["bootstrap_values"] != 0, ri(E, T),
+                                              torch.zeros(E, T, device=device))
+        inp["bootstrap_values"][:, -1] = ri(E)
+    if "next_values" in inp:
+        inp["next_values"] = ri(E, T)
+    params = {k: (1.0 if k in ("gamma", "lambda_") else v) for k, v in params.items()}
+    if op == "vtrace":
+        lpb = torch.randn(E, T, generator=g, device=device)
+        inp["log_pi_behavior"] = lpb
+        inp["log_pi_target"] = lpb + torch.rand(E, T, generator=g, device=device)
+        params.update(rho_bar=0.5, c_bar=1.0)
+    if op == "retrace":
+        p = torch.tensor([0.25, 0.75], device=device)
+        inp["action_probs_target"] = p.expand(E, T, 2).contiguous()
+        inp["action_probs_behavior"] = torch.full((E, T), 0.125, device=device)
+        inp["next_q_values_all"] = torch.stack((ri(E, T), ri(E, T)), dim=-1).contiguous()
+        inp["actions"] = torch.randint(0, 2, (E, T), generator=g, device=device)
+        params.update(c_bar=1.0, rho_bar=0.5)
+    return inp, params
+
+
 def as_dtype(inp: dict, dtype) -> dict:
     """The float inputs of a configuration as `dtype` (int64 actions unchanged)."""
     return {k: (v.to(dtype) if v is not None and v.is_floating_point() else v)

@@ -243,6 +243,36 @@ def brute_vtrace(lpt, lpb, v, r, term, trunc, boot, gamma, rho_bar, c_bar):
     return tg, adv
 
 
+def brute_retrace(pi, mu, q, nq, act, r, term, trunc, gamma, lam, c_bar, rho_bar):
+    """Retrace(lambda) from its definition (tests/test_retrace.py:19-60 states the same):
+    E_pi[Q'] = sum over actions of pi * Q';  pi(a_t) = the target probability of the action
+    taken;  c = lambda * min(c_bar, pi(a_t)/mu),  rho = min(rho_bar, pi(a_t)/mu);
+    Q_ret[t] = q + (r + gamma*E_pi[Q']*(1-term) - q) + gamma*c[t+1]*(1-done)*(Q_ret[t+1] - q[t+1]),
+    with c[T] = 0, and adv = rho*(r + gamma*Q_ret[t+1]*(1-term) - q), Q_ret[T] = 0."""
+    A = len(pi[0][0])
+    tg = [[0.0] * T for _ in range(N)]
+    adv = [[0.0] * T for _ in range(N)]
+    for n in range(N):
+        c = [0.0] * (T + 1)
+        rho = [0.0] * T
+        enq = [0.0] * T
+        for t in range(T):
+            enq[t] = sum(pi[n][t][a] * nq[n][t][a] for a in range(A))
+            ratio = pi[n][t][act[n][t]] / mu[n][t]
+            c[t] = lam * min(c_bar, ratio)
+            rho[t] = min(rho_bar, ratio)
+        acc = 0.0
+        for t in reversed(range(T)):
+            cut = min(term[n][t] + trunc[n][t], 1.0)
+            acc = (r[n][t] + gamma * enq[t] * (1.0 - term[n][t]) - q[n][t]
+                   + gamma * c[t + 1] * (1.0 - cut) * acc)
+            tg[n][t] = acc + q[n][t]
+        for t in range(T):
+            nxt = tg[n][t + 1] if t + 1 < T else 0.0
+            adv[n][t] = rho[t] * (r[n][t] + gamma * nxt * (1.0 - term[n][t]) - q[n][t])
+    return tg, adv
+
+
 def brute_lambda(r, nv, term, trunc, boot, gamma, lam):
     out = [[0.0] * T for _ in range(N)]
     for n in range(N):
@@ -315,6 +345,57 @@ def truncation_fixtures():
                   {"rewards": r, "values": v, "terminateds": zeros, "truncateds": tr1,
                    "bootstrap_values": b1},
                   {"gamma": 0.95, "lambda_": 1.0}, {"advantages": mc}))
+    c.extend(clip_split_fixtures(rng))
+    return c
+
+
+def clip_split_fixtures(rng):
+    """V-trace with rho_bar != c_bar, and Retrace with several actions: the clips the
+    reference applies separately (kernels/vtrace_fused.py:104-106, ops/retrace.py:178-182)
+    and the action reduction and gather over the [E, T, A] layout.  Ratios are spread over
+    [e^-1, e] so that many fall between, and beyond, the two clip levels."""
+    trunc, boot = _layout()
+    zeros = [[0.0] * T for _ in range(N)]
+    term = [[0.0] * T for _ in range(N)]
+    term[0][9] = term[1][2] = 1.0
+    g = 0.99
+    c = []
+    for rho_bar, c_bar in ((0.8, 0.9), (1.3, 0.6)):
+        lpt, lpb = _rand(rng, -1.0, 0.0), _rand(rng, -1.0, 0.0)
+        v, r = _rand(rng), _rand(rng, -1.0, 1.0)
+        tg, adv = brute_vtrace(lpt, lpb, v, r, term, trunc, boot, g, rho_bar, c_bar)
+        c.append(case(f"vtrace_rho{rho_bar}_c{c_bar}_interior_truncations", "vtrace",
+                      "kernels/vtrace_fused.py:104-106 (separate clips), tests/test_vtrace.py:487-570 (layout)",
+                      {"log_pi_target": lpt, "log_pi_behavior": lpb, "values": v, "rewards": r,
+                       "terminateds": term, "truncateds": trunc, "bootstrap_values": boot},
+                      {"gamma": g, "rho_bar": rho_bar, "c_bar": c_bar},
+                      {"targets": tg, "advantages": adv}))
+        # no truncations, last_value only (the window boundary value alone)
+        lv = [_f32(x) for x in rng.normal(size=N)]
+        boot_last = [[0.0] * (T - 1) + [lv[n]] for n in range(N)]
+        tg, adv = brute_vtrace(lpt, lpb, v, r, term, zeros, boot_last, g, rho_bar, c_bar)
+        c.append(case(f"vtrace_rho{rho_bar}_c{c_bar}_last_value", "vtrace",
+                      "kernels/vtrace_fused.py:104-106 (separate clips)",
+                      {"log_pi_target": lpt, "log_pi_behavior": lpb, "values": v, "rewards": r,
+                       "terminateds": term, "last_value": lv},
+                      {"gamma": g, "rho_bar": rho_bar, "c_bar": c_bar},
+                      {"targets": tg, "advantages": adv}))
+    for A in (3, 5):
+        logits = rng.normal(size=(N, T, A))
+        p = np.exp(logits) / np.exp(logits).sum(-1, keepdims=True)
+        pi = [[[_f32(x) for x in p[n, t]] for t in range(T)] for n in range(N)]
+        nq = [[[_f32(x) for x in rng.normal(size=A)] for _ in range(T)] for _ in range(N)]
+        mu = _rand(rng, 0.1, 0.9)
+        q, r = _rand(rng, -1.0, 1.0), _rand(rng, -1.0, 1.0)
+        act = [[int(a) for a in rng.integers(0, A, size=T)] for _ in range(N)]
+        tg, adv = brute_retrace(pi, mu, q, nq, act, r, term, trunc, g, 0.9, 0.9, 0.8)
+        c.append(case(f"retrace_A{A}_clipped", "retrace",
+                      "ops/retrace.py:178-182 (action reduction, gather), tests/test_retrace.py:19-60",
+                      {"action_probs_target": pi, "action_probs_behavior": mu, "q_values": q,
+                       "next_q_values_all": nq, "actions": act, "rewards": r, "terminateds": term,
+                       "truncateds": trunc},
+                      {"gamma": g, "lambda_": 0.9, "c_bar": 0.9, "rho_bar": 0.8},
+                      {"targets": tg, "advantages": adv}))
     return c
 
 

@@ -4,14 +4,18 @@ support for small-batch workloads"; torch.cuda.graph over the same public calls)
 A captured call is replayed several times.  Between replays the static inputs are
 overwritten with new data and other eager work (uncaptured calls of the same op, torch ops)
 runs on the default stream; every replay's outputs must equal, bit for bit, an eager call on
-the same inputs.  Rows longer than 2048 steps use the look-back workspace: both the
+the same inputs, and match the float64 oracle on those inputs at the suite's tolerances
+(rtol = atol = 1e-5 up to 2048 steps, the horizon-scaled atol beyond; normalised advantages
+with that tolerance divided by the batch std).  Rows longer than 2048 steps use the look-back workspace: both the
 documented order (a warm-up call on the capture stream creates it before capture) and a
 first call inside the capture are covered.
 """
 import pytest
 import torch
 
-from _common import make_inputs, run_api, to_device
+import numpy as np
+
+from _common import OUTPUTS, assert_close, make_inputs, run_api, run_oracle, suite_atol, to_device
 
 pytestmark = pytest.mark.gpu
 
@@ -79,6 +83,24 @@ def _same(a, b):
     return torch.equal(a.view(torch.int32), b.view(torch.int32))  # bitwise, nan included
 
 
+def _against_oracle(op, inp, params, outs, T, what):
+    exp = run_oracle(op, inp, params)
+    if op.startswith("gae_normalized"):
+        adv_exp, ret_exp = exp
+        raw = ret_exp - np.asarray(inp["values"], np.float64)
+        kept = raw if inp.get("mask") is None else raw[np.asarray(inp["mask"]) != 0]
+        std = float(np.std(kept, ddof=1))
+        base = suite_atol("gae", inp, raw, T)
+        scale = max(1.0, float(np.max(np.abs(ret_exp))))
+        assert_close(outs[1].cpu().numpy(), ret_exp, 1e-5, base + 1e-6 * scale, f"{what}:returns")
+        assert_close(outs[0].cpu().numpy(), adv_exp, 1e-5, base / min(std, 1.0) + 1e-6,
+                     f"{what}:advantages")
+        return
+    base_op = "gae" if op == "gae_masked" else op
+    for name, o, e in zip(OUTPUTS[op], outs, exp):
+        assert_close(o.cpu().numpy(), e, 1e-5, suite_atol(base_op, inp, e, T), f"{what}:{name}")
+
+
 @pytest.mark.parametrize("warm", [True, False], ids=["warmed", "first-call-in-capture"])
 @pytest.mark.parametrize("op", OPS)
 @pytest.mark.parametrize("shape", [(64, 512), (16, 2048), (3, 5000)], ids=lambda s: f"{s[0]}x{s[1]}")
@@ -112,4 +134,5 @@ def test_graph_replays_match_eager(op, shape, warm, device, monkeypatch):
         want = run_api(op, new, params, device)
         for o, w in zip(outs, want):
             assert _same(o, w), f"{op}{shape} replay {rep}: differs from the eager call"
+        _against_oracle(op, new, params, outs, shape[1], f"{op}{shape} replay {rep}")
     del graph

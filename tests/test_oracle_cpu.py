@@ -5,9 +5,13 @@
 2. identities the mathematics fixes, independent of any implementation;
 3. library routines the recurrences reduce to (cumsum, geometric convolution);
 4. brute force of the affine recurrence through its explicit product formula;
-5. the float32 torch-loop restatement of the reference loops (oracle/torch_loops.py).
-A planted mistake (sign, shift of done by one step, dropped bootstrap) fails at least one
-of these -- see test_checks_catch_planted_mistakes.
+5. the float32 torch-loop restatement of the reference loops (oracle/torch_loops.py);
+6. for V-trace's separate rho/c clips and Retrace's action reduction and gather: IMPALA's
+   explicit sum, the uniform on-policy and greedy-target cases of Retrace, and NumPy's
+   einsum / take_along_axis over the [E, T, A] layout.
+A planted mistake (sign, shift of done by one step, dropped bootstrap; rho/c clips swapped,
+a wrong action stride or gather) fails at least one of these -- see
+test_checks_catch_planted_mistakes and test_clip_and_action_pins_catch_planted_mistakes.
 """
 import numpy as np
 import pytest
@@ -323,3 +327,393 @@ def test_masked_gae_hand_worked():
     # the unmasked row, then masked) -- misses the hand-worked answer
     plain = orc.gae(r, v, np.zeros_like(r), None, 0.5, 0.5)
     assert not np.allclose(plain[0, 0], 1.0625)
+
+
+# ---------------------------------------------------------------------------------------
+# V-trace with rho_bar != c_bar and Retrace with several actions.  The reference clips rho
+# and c separately (kernels/vtrace_fused.py:104-106) and reduces Retrace's [E, T, A] inputs
+# by an expectation over actions and a gather of the taken action (ops/retrace.py:178-182).
+# Besides the golden fixtures (independent brute-force loops, tests/golden), each is pinned
+# by a closed form evaluated term by term, with no recurrence:
+#   * V-trace: the explicit sum of Espeholt et al. 2018 (IMPALA), eq. (1):
+#       v_s = V(x_s) + sum_{t>=s} (prod_{i=s}^{t-1} gamma_i c_i) rho_t delta_t
+#     with gamma_i = gamma*(1 - done_i); c_bar = 0 leaves the one-step target
+#     V + rho*delta, rho_bar = 0 leaves V and zero advantages;
+#   * Retrace: the on-policy uniform case of tests/test_retrace.py:343-361 (pi = mu = 1/A,
+#     lambda = 1: n-step expected-SARSA TD, E_pi[Q'] = the mean over actions), and a greedy
+#     (one-hot) target, Watkins' case: pi(a_t) = [a_t == greedy_t], so an off-greedy action
+#     cuts the trace and has a zero advantage, and E_pi[Q'] = Q'[t, greedy_t].
+# A planted mistake -- rho and c clips swapped, a wrong action stride, a gather of the
+# wrong step's action, c[t] in place of c[t+1], SARSA in place of expected SARSA, ... --
+# fails at least one of them (test_clip_and_action_pins_catch_planted_mistakes).
+# ---------------------------------------------------------------------------------------
+def _vtrace_case(seed, rho_bar, c_bar, E=6, T=40):
+    r = _rng(seed)
+    lpt = r.uniform(-1.0, 0.0, size=(E, T)).astype(np.float32)
+    lpb = r.uniform(-1.0, 0.0, size=(E, T)).astype(np.float32)
+    val = r.normal(size=(E, T)).astype(np.float32)
+    rew = r.normal(size=(E, T)).astype(np.float32)
+    term = (r.random((E, T)) < 0.08).astype(np.float32)
+    lv = r.normal(size=E).astype(np.float32)
+    inp = {"log_pi_target": lpt, "log_pi_behavior": lpb, "values": val, "rewards": rew,
+           "terminateds": term, "last_value": lv}
+    return inp, {"gamma": 0.97, "rho_bar": rho_bar, "c_bar": c_bar}
+
+
+def _impala_closed_form(inp, p):
+    """V-trace targets and policy-gradient advantages by IMPALA's eq. (1), term by term."""
+    lpt, lpb, v, r, te = (inp[k].astype(np.float64) for k in
+                          ("log_pi_target", "log_pi_behavior", "values", "rewards", "terminateds"))
+    lv = inp["last_value"].astype(np.float64)
+    E, T = r.shape
+    g = p["gamma"]
+    ratio = np.exp(lpt - lpb)
+    rho, c = np.minimum(p["rho_bar"], ratio), np.minimum(p["c_bar"], ratio)
+    v_next = np.concatenate([v[:, 1:], lv[:, None]], axis=1)
+    gam = g * (1.0 - te)
+    delta = rho * (r + gam * v_next - v)
+    vs = np.zeros((E, T))
+    for s in range(T):
+        acc, prod = 0.0, np.ones(E)
+        for t in range(s, T):
+            acc = acc + prod * delta[:, t]
+            prod = prod * gam[:, t] * c[:, t]
+        vs[:, s] = v[:, s] + acc
+    vs_next = np.concatenate([vs[:, 1:], lv[:, None]], axis=1)
+    adv = rho * (r + gam * vs_next - v)
+    return vs, adv
+
+
+@pytest.mark.parametrize("rho_bar,c_bar", [(0.8, 0.9), (1.3, 0.6), (2.0, 2.0)])
+def test_vtrace_separate_clips_explicit_sum(rho_bar, c_bar):
+    inp, p = _vtrace_case(20, rho_bar, c_bar)
+    tg, adv = run_oracle("vtrace", inp, p)
+    etg, eadv = _impala_closed_form(inp, p)
+    assert_close(tg, etg, 1e-12, 1e-12, "vs")
+    assert_close(adv, eadv, 1e-12, 1e-12, "adv")
+
+
+def test_vtrace_zero_clips():
+    """c_bar = 0: no trace, vs = V + rho*delta; rho_bar = 0: vs = V, advantages 0."""
+    inp, p = _vtrace_case(21, 0.8, 0.0)
+    tg, adv = run_oracle("vtrace", inp, p)
+    lpt, lpb, v, r, te = (inp[k].astype(np.float64) for k in
+                          ("log_pi_target", "log_pi_behavior", "values", "rewards", "terminateds"))
+    v_next = np.concatenate([v[:, 1:], inp["last_value"].astype(np.float64)[:, None]], axis=1)
+    rho = np.minimum(0.8, np.exp(lpt - lpb))
+    assert_close(tg, v + rho * (r + 0.97 * (1 - te) * v_next - v), 1e-12, 1e-12, "c_bar=0")
+    tg, adv = run_oracle("vtrace", inp, dict(p, rho_bar=0.0, c_bar=1.0))
+    assert_close(tg, v, 0, 0, "rho_bar=0 targets")
+    assert np.array_equal(adv, np.zeros_like(adv))
+
+
+def _retrace_uniform_case(seed, A=4, E=5, T=33):
+    """tests/test_retrace.py:343-361: pi = mu = 1/A, lambda = 1, clips far above 1."""
+    r = _rng(seed)
+    inp = {"action_probs_target": np.full((E, T, A), 1.0 / A, np.float32),
+           "action_probs_behavior": np.full((E, T), 1.0 / A, np.float32),
+           "q_values": r.normal(size=(E, T)).astype(np.float32),
+           "next_q_values_all": r.normal(size=(E, T, A)).astype(np.float32),
+           "actions": r.integers(0, A, size=(E, T)).astype(np.int64),
+           "rewards": r.normal(size=(E, T)).astype(np.float32),
+           "terminateds": np.zeros((E, T), np.float32),
+           "truncateds": np.zeros((E, T), np.float32)}
+    return inp, {"gamma": 0.99, "lambda_": 1.0, "c_bar": 1e6, "rho_bar": 1e6}
+
+
+def _retrace_uniform_expected(inp, p):
+    q, r = inp["q_values"].astype(np.float64), inp["rewards"].astype(np.float64)
+    mean_q = inp["next_q_values_all"].astype(np.float64).mean(axis=-1)
+    g = p["gamma"]
+    delta = r + g * mean_q - q
+    E, T = q.shape
+    tg = np.zeros((E, T))
+    for t in range(T):
+        tg[:, t] = q[:, t] + sum(g ** (k - t) * delta[:, k] for k in range(t, T))
+    nxt = np.concatenate([tg[:, 1:], np.zeros((E, 1))], axis=1)
+    return tg, r + g * nxt - q
+
+
+def _retrace_greedy_case(seed, A=3, E=5, T=37):
+    r = _rng(seed)
+    greedy = r.integers(0, A, size=(E, T))
+    pi = np.zeros((E, T, A), np.float32)
+    np.put_along_axis(pi, greedy[..., None], 1.0, axis=-1)
+    term = (r.random((E, T)) < 0.06).astype(np.float32)
+    trunc = ((r.random((E, T)) < 0.06) * (1 - term)).astype(np.float32)
+    inp = {"action_probs_target": pi,
+           "action_probs_behavior": r.uniform(0.2, 1.0, size=(E, T)).astype(np.float32),
+           "q_values": r.normal(size=(E, T)).astype(np.float32),
+           "next_q_values_all": r.normal(size=(E, T, A)).astype(np.float32),
+           # the behaviour picks the greedy action about two times in three
+           "actions": np.where(r.random((E, T)) < 0.67, greedy,
+                               r.integers(0, A, size=(E, T))).astype(np.int64),
+           "rewards": r.normal(size=(E, T)).astype(np.float32),
+           "terminateds": term, "truncateds": trunc}
+    return inp, {"gamma": 0.95, "lambda_": 0.9, "c_bar": 2.0, "rho_bar": 1.2}, greedy
+
+
+def _retrace_greedy_expected(inp, p, greedy):
+    """Watkins' case: D[t] = sum_{k>=t} (prod_{i=t}^{k-1} gamma*c[i+1]*(1-done_i)) delta_k,
+    delta_k = r + gamma*Q'[k, greedy_k]*(1-term) - q, c = lambda*min(c_bar, [a == greedy]/mu)."""
+    q, r, mu, te, tr = (inp[k].astype(np.float64) for k in
+                        ("q_values", "rewards", "action_probs_behavior", "terminateds", "truncateds"))
+    nq = inp["next_q_values_all"].astype(np.float64)
+    on = (inp["actions"] == greedy).astype(np.float64)
+    g, lam = p["gamma"], p["lambda_"]
+    E, T = q.shape
+    qg = np.take_along_axis(nq, greedy[..., None], axis=-1)[..., 0]
+    delta = r + g * qg * (1.0 - te) - q
+    c = lam * np.minimum(p["c_bar"], on / mu)
+    keep = 1.0 - np.minimum(te + tr, 1.0)
+    tg = np.zeros((E, T))
+    for t in range(T):
+        acc, prod = 0.0, np.ones(E)
+        for k in range(t, T):
+            acc = acc + prod * delta[:, k]
+            prod = prod * (g * c[:, k + 1] * keep[:, k] if k + 1 < T else 0.0)
+        tg[:, t] = q[:, t] + acc
+    nxt = np.concatenate([tg[:, 1:], np.zeros((E, 1))], axis=1)
+    adv = on * np.minimum(p["rho_bar"], 1.0 / mu) * (r + g * nxt * (1.0 - te) - q)
+    return tg, adv
+
+
+def test_retrace_uniform_on_policy_is_expected_sarsa_td():
+    inp, p = _retrace_uniform_case(30)
+    tg, adv = run_oracle("retrace", inp, p)
+    etg, eadv = _retrace_uniform_expected(inp, p)
+    assert_close(tg, etg, 1e-11, 1e-11, "targets")
+    assert_close(adv, eadv, 1e-11, 1e-11, "advantages")
+
+
+def test_retrace_greedy_target_cuts_traces():
+    inp, p, greedy = _retrace_greedy_case(31)
+    tg, adv = run_oracle("retrace", inp, p)
+    etg, eadv = _retrace_greedy_expected(inp, p, greedy)
+    assert_close(tg, etg, 1e-12, 1e-12, "targets")
+    assert_close(adv, eadv, 1e-12, 1e-12, "advantages")
+    off = inp["actions"] != greedy
+    assert off.any() and np.array_equal(adv[off], np.zeros(int(off.sum())))
+
+
+@pytest.mark.parametrize("A", [2, 4, 7])
+def test_retrace_matches_numpy_reduction_and_gather(A):
+    """E_pi[Q'] by einsum and pi(a_t) by take_along_axis -- NumPy's own reduction and gather
+    over the [E, T, A] layout -- fed through a float64 backward scan, at clipped ratios."""
+    inp, p = make_inputs("retrace", 7, 45, seed=32, n_act=A, p_trunc=0.05)
+    p = dict(p, c_bar=0.9, rho_bar=0.8)
+    tg, adv = run_oracle("retrace", inp, p)
+    pi, nq = inp["action_probs_target"].astype(np.float64), inp["next_q_values_all"].astype(np.float64)
+    mu, q, r, te, tr = (inp[k].astype(np.float64) for k in
+                        ("action_probs_behavior", "q_values", "rewards", "terminateds", "truncateds"))
+    enq = np.einsum("eta,eta->et", pi, nq)
+    pa = np.take_along_axis(pi, inp["actions"][..., None], axis=-1)[..., 0]
+    c = p["lambda_"] * np.minimum(p["c_bar"], pa / mu)
+    rho = np.minimum(p["rho_bar"], pa / mu)
+    u = r + p["gamma"] * enq * (1.0 - te) - q
+    c_next = np.concatenate([c[:, 1:], np.zeros((c.shape[0], 1))], axis=1)
+    v = p["gamma"] * c_next * (1.0 - np.minimum(te + tr, 1.0))
+    d = np.zeros_like(u)
+    acc = np.zeros(u.shape[0])
+    for t in range(u.shape[1] - 1, -1, -1):
+        acc = u[:, t] + v[:, t] * acc
+        d[:, t] = acc
+    etg = d + q
+    nxt = np.concatenate([etg[:, 1:], np.zeros((q.shape[0], 1))], axis=1)
+    assert_close(tg, etg, 1e-12, 1e-12, "targets")
+    assert_close(adv, rho * (r + p["gamma"] * nxt * (1.0 - te) - q), 1e-12, 1e-12, "advantages")
+
+
+def _vtrace_variant(inp, p, mistake=None):
+    """A float64 copy of the V-trace recurrence in which a mistake can be planted."""
+    lpt, lpb, v, r, te = (np.asarray(inp[k], np.float64) for k in
+                          ("log_pi_target", "log_pi_behavior", "values", "rewards", "terminateds"))
+    E, T = r.shape
+    tr = np.asarray(inp["truncateds"], np.float64) if inp.get("truncateds") is not None else np.zeros((E, T))
+    if inp.get("bootstrap_values") is not None:
+        boot = np.asarray(inp["bootstrap_values"], np.float64)
+    else:
+        boot = np.zeros((E, T))
+        if inp.get("last_value") is not None:
+            boot[:, -1] = np.asarray(inp["last_value"], np.float64)
+    g = p["gamma"]
+    ratio = np.exp(lpt - lpb)
+    rb, cb = (p["c_bar"], p["rho_bar"]) if mistake == "clip_swap" else (p["rho_bar"], p["c_bar"])
+    rho, c = np.minimum(rb, ratio), np.minimum(cb, ratio)
+    if mistake == "c_shifted":
+        c = np.concatenate([c[:, 1:], np.zeros((E, 1))], axis=1)
+    if mistake == "rho_missing":
+        rho_d = np.ones_like(rho)
+    else:
+        rho_d = rho
+    done = np.minimum(te + tr, 1.0)
+
+    def nxt_of(x):
+        raw = np.concatenate([x[:, 1:], np.zeros((E, 1))], axis=1)
+        return np.where(tr == 0.0, raw, 0.0) + boot
+
+    delta = rho_d * (r + g * nxt_of(v) * (1.0 - te) - v)
+    d = np.zeros((E, T))
+    acc = np.zeros(E)
+    for t in range(T - 1, -1, -1):
+        acc = delta[:, t] + g * c[:, t] * (1.0 - done[:, t]) * acc
+        d[:, t] = acc
+    vs = d + v
+    nv = nxt_of(v) if mistake == "adv_uses_values" else nxt_of(vs)
+    return vs, rho * (r + g * nv * (1.0 - te) - v)
+
+
+def _retrace_variant(inp, p, mistake=None):
+    """A float64 copy of the Retrace recurrence in which a mistake can be planted."""
+    pi, nq = (np.asarray(inp[k], np.float64) for k in ("action_probs_target", "next_q_values_all"))
+    mu, q, r, te, tr = (np.asarray(inp[k], np.float64) for k in
+                        ("action_probs_behavior", "q_values", "rewards", "terminateds", "truncateds"))
+    act = np.asarray(inp["actions"], np.int64)
+    E, T, A = pi.shape
+    g, lam = p["gamma"], p.get("lambda_", 1.0)
+    c_bar, rho_bar = p.get("c_bar", 1.0), p.get("rho_bar", 1.0)
+    if mistake == "action_stride":  # the flat buffer read as [E, A, T]
+        pi = pi.reshape(E, A, T).transpose(0, 2, 1)
+        nq = nq.reshape(E, A, T).transpose(0, 2, 1)
+    if mistake == "next_step_action":
+        act = np.concatenate([act[:, 1:], act[:, -1:]], axis=1)
+    enq = (pi * nq).sum(-1)
+    if mistake == "sarsa":
+        enq = np.take_along_axis(nq, act[..., None], axis=-1)[..., 0]
+    pa = np.take_along_axis(pi, act[..., None], axis=-1)[..., 0]
+    if mistake == "clip_swap":
+        c_bar, rho_bar = rho_bar, c_bar
+    c = lam * np.minimum(c_bar, pa / mu)
+    rho = np.minimum(rho_bar, pa / mu) * (lam if mistake == "lambda_on_rho" else 1.0)
+    c_next = c if mistake == "c_unshifted" else np.concatenate([c[:, 1:], np.zeros((E, 1))], axis=1)
+    done = np.minimum(te + tr, 1.0)
+    u = r + g * enq * (1.0 - te) - q
+    d = np.zeros((E, T))
+    acc = np.zeros(E)
+    for t in range(T - 1, -1, -1):
+        acc = u[:, t] + g * c_next[:, t] * (1.0 - done[:, t]) * acc
+        d[:, t] = acc
+    tg = d + q
+    nxt = np.concatenate([tg[:, 1:], np.zeros((E, 1))], axis=1)
+    return tg, rho * (r + g * nxt * (1.0 - te) - q)
+
+
+def _clip_and_action_pins():
+    """(op, inputs, params, expected outputs) of every pin above, golden fixtures included."""
+    pins = []
+    for c in golden_cases("vtrace") + golden_cases("retrace"):
+        exp = tuple(np.asarray(c["expected"].get(n), np.float64) if n in c["expected"] else None
+                    for n in OUTPUTS[c["op"]])
+        inp = {k: (np.asarray(v, np.int64) if k == "actions" else np.asarray(v, np.float32))
+               for k, v in c["inputs"].items()}
+        pins.append((c["op"], inp, c["params"], exp))
+    for rb, cb in [(0.8, 0.9), (1.3, 0.6)]:
+        inp, p = _vtrace_case(20, rb, cb)
+        pins.append(("vtrace", inp, p, _impala_closed_form(inp, p)))
+    inp, p = _retrace_uniform_case(30)
+    pins.append(("retrace", inp, p, _retrace_uniform_expected(inp, p)))
+    inp, p, greedy = _retrace_greedy_case(31)
+    pins.append(("retrace", inp, p, _retrace_greedy_expected(inp, p, greedy)))
+    return pins
+
+
+def _fails_a_pin(op, impl, pins):
+    for pop, inp, p, exp in pins:
+        if pop != op:
+            continue
+        for got, want in zip(impl(inp, p), exp):
+            if want is not None and not np.allclose(got, want, rtol=1e-6, atol=1e-6):
+                return True
+    return False
+
+
+def test_clip_and_action_pins_catch_planted_mistakes():
+    pins = _clip_and_action_pins()
+    assert not _fails_a_pin("vtrace", _vtrace_variant, pins)   # the unplanted copies pass
+    assert not _fails_a_pin("retrace", _retrace_variant, pins)
+    for mistake in ("clip_swap", "c_shifted", "rho_missing", "adv_uses_values"):
+        assert _fails_a_pin("vtrace", lambda i, p, m=mistake: _vtrace_variant(i, p, m), pins), mistake
+    for mistake in ("action_stride", "next_step_action", "sarsa", "clip_swap", "lambda_on_rho",
+                    "c_unshifted"):
+        assert _fails_a_pin("retrace", lambda i, p, m=mistake: _retrace_variant(i, p, m), pins), mistake
+    # and the clip swap is caught by the rho_bar != c_bar pins alone, the action stride by
+    # the multi-action ones alone: the single-action, equal-clip pins would miss both
+    is_split = lambda x: x[0] == "vtrace" and x[2]["rho_bar"] != x[2]["c_bar"]  # noqa: E731
+    is_multi = lambda x: x[0] == "retrace" and x[1]["action_probs_target"].shape[-1] > 1  # noqa: E731
+    split = [x for x in pins if is_split(x)]
+    multi = [x for x in pins if is_multi(x)]
+    same = [x for x in pins if not is_split(x) and not is_multi(x)]
+    assert _fails_a_pin("vtrace", lambda i, p: _vtrace_variant(i, p, "clip_swap"), split)
+    assert not _fails_a_pin("vtrace", lambda i, p: _vtrace_variant(i, p, "clip_swap"), same)
+    assert _fails_a_pin("retrace", lambda i, p: _retrace_variant(i, p, "action_stride"), multi)
+    assert not _fails_a_pin("retrace", lambda i, p: _retrace_variant(i, p, "action_stride"), same)
+
+
+# ---------------------------------------------------------------------------------------
+# the reference's float32 loops: the C restatement (oracle.loop32, fast enough for the
+# full-size configurations) equals the torch restatement (oracle/torch_loops.py) bit for
+# bit -- same operations, same order, same float32 roundings -- except through exp
+# (V-trace: the C library's expf against torch's, which may differ in the last place)
+# ---------------------------------------------------------------------------------------
+def _torch_loop(op, inp, params):
+    t = {k: torch.from_numpy(np.asarray(v)) for k, v in inp.items() if v is not None}
+    g = t.get
+    if op == "gae":
+        return (torch_loops.gae_loop(g("rewards"), g("values"), g("terminateds"), g("truncateds"),
+                                     params["gamma"], params["lambda_"],
+                                     bootstrap_values=g("bootstrap_values"),
+                                     last_value=g("last_value")),)
+    if op == "vtrace":
+        return torch_loops.vtrace_loop(g("log_pi_target"), g("log_pi_behavior"), g("values"),
+                                       g("rewards"), g("terminateds"), params["gamma"],
+                                       params["rho_bar"], params["c_bar"], last_value=g("last_value"))
+    if op == "retrace":
+        return torch_loops.retrace_loop(g("action_probs_target"), g("action_probs_behavior"),
+                                        g("q_values"), g("next_q_values_all"), g("actions"),
+                                        g("rewards"), g("terminateds"), g("truncateds"), **params)
+    if op == "lambda_returns":
+        return (torch_loops.lambda_returns_loop(g("rewards"), g("next_values"), g("terminateds"),
+                                                g("truncateds"), params["gamma"], params["lambda_"],
+                                                bootstrap_values=g("bootstrap_values")),)
+    if op == "discounted_returns":
+        return (torch_loops.discounted_returns_loop(g("rewards"), g("terminateds"), g("truncateds"),
+                                                    params["gamma"],
+                                                    bootstrap_values=g("bootstrap_values")),)
+    if op == "eligibility_traces":
+        return (torch_loops.eligibility_traces_loop(g("gradients"), g("dones"), params["gamma"],
+                                                    params["lambda_"], g("seed_values")),)
+    if op == "prefix_sum":
+        return (torch_loops.prefix_sum_loop(g("inputs"), g("dones"), g("seed_values"),
+                                            params.get("boundary", "ends_at")),)
+    raise KeyError(op)
+
+
+LOOP_CASES = [
+    ("gae", dict(p_term=0.05, boot="row")), ("gae", dict(p_term=0.05, p_trunc=0.05, boot="full")),
+    ("vtrace", dict(p_term=0.05, boot="row")), ("retrace", dict(n_act=2)),
+    ("retrace", dict(n_act=3, p_trunc=0.05)),
+    ("lambda_returns", dict(boot="full")), ("lambda_returns", dict(p_trunc=0.05, boot="full")),
+    ("discounted_returns", dict()), ("discounted_returns", dict(p_trunc=0.05, boot="full")),
+    ("eligibility_traces", dict(boot="row")), ("prefix_sum", dict(boot="row")),
+]
+
+
+@pytest.mark.parametrize("op,kw", LOOP_CASES, ids=lambda v: v if isinstance(v, str) else
+                         "-".join(f"{k}{w}" for k, w in v.items()))
+def test_float32_loops_c_equals_torch(op, kw):
+    inp, params = make_inputs(op, 16, 300, seed=60, **kw)
+    if op == "vtrace":
+        params = dict(params, rho_bar=0.8, c_bar=0.9)
+    if op == "retrace":
+        params = dict(params, c_bar=0.9, rho_bar=0.8)
+    want = _torch_loop(op, inp, params)
+    got = orc.loop32(op, inp, params)
+    for g, w in zip(got, want):
+        assert g.dtype == np.float32
+        if op == "vtrace":
+            np.testing.assert_allclose(g, w.numpy(), rtol=2e-6, atol=2e-6)
+        else:
+            assert np.array_equal(g, w.numpy()), f"{op}: {np.max(np.abs(g - w.numpy()))}"
+    if op == "prefix_sum":
+        p2 = {"boundary": "starts_at"}
+        assert np.array_equal(orc.loop32(op, inp, p2)[0], _torch_loop(op, inp, p2)[0].numpy())
