@@ -28,7 +28,10 @@
  *     rlk_workspace_bytes(num_envs, seq_len) bytes, ZERO-FILLED BEFORE ITS FIRST USE.
  *     Each call leaves the workspace ready for the next one, so zero it once and reuse
  *     it, across calls of any shape; calls that share a workspace must be ordered on one
- *     stream (concurrent use races).  Calls that need no workspace ignore the argument
+ *     stream (concurrent use races).  Zero it again after at most
+ *     RLK_WORKSPACE_MAX_CALLS long-row calls: the status words carry a 30-bit count of
+ *     the calls made on the workspace, which wraps after 2^30 calls, and a word left by
+ *     a call 2^30 calls earlier would then read as current (a silently wrong carry).  Calls that need no workspace ignore the argument
  *     (NULL is fine).  Layout (uint64 words): [0..7] header, word [3] the error flag --
  *     nonzero if a look-back wait gave up or the counters were not at rest (results of
  *     that call are invalid); [8..2055] 64 counter slots; then two places of up to five
@@ -64,6 +67,9 @@ extern "C" {
 
 #define RLK_BACKWARD 0
 #define RLK_FORWARD 1
+
+/* Long-row calls a workspace may serve between two zero-fills (see Workspace above). */
+#define RLK_WORKSPACE_MAX_CALLS (1 << 29)
 
 /* A bfloat16 value as its raw bits (the upper half of an IEEE float32). */
 typedef uint16_t rlk_bf16;

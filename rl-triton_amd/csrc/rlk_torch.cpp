@@ -122,6 +122,18 @@ std::map<std::pair<int, uintptr_t>, at::Tensor>& workspaces() {
   return *m;
 }
 
+// Long-row calls served by each cached workspace since it was last zero-filled.  Its status
+// words carry a 30-bit count of the calls made on it, which wraps after 2^30 calls; a word
+// left 2^30 calls earlier would then read as current.  So a workspace is zero-filled again
+// (on its stream, before the call) once it has served g_ws_max_calls calls: the C ABI's
+// RLK_WORKSPACE_MAX_CALLS, lowered only by tests (set_workspace_max_calls).
+std::map<std::pair<int, uintptr_t>, uint64_t>& workspace_calls() {
+  static auto* m = new std::map<std::pair<int, uintptr_t>, uint64_t>();
+  return *m;
+}
+uint64_t g_ws_max_calls = RLK_WORKSPACE_MAX_CALLS;
+uint64_t g_ws_clears = 0;
+
 struct Workspace {
   void* ptr = nullptr;
   size_t bytes = 0;
@@ -139,12 +151,21 @@ Workspace workspace(const Call& c, const at::Tensor& like) {
     w.ok = false;
     return w;
   }
-  at::Tensor& buf = workspaces()[{(int)c.dev, reinterpret_cast<uintptr_t>(s)}];
+  const std::pair<int, uintptr_t> key{(int)c.dev, reinterpret_cast<uintptr_t>(s)};
+  at::Tensor& buf = workspaces()[key];
+  uint64_t& calls = workspace_calls()[key];
   if (!buf.defined() || (size_t)buf.numel() < need) {
     size_t size = buf.defined() ? std::max(need, 2 * (size_t)buf.numel()) : need;
     size = (size + 255) / 256 * 256;
     buf = at::zeros({(int64_t)size}, like.options().dtype(at::kByte));
+    calls = 0;
   }
+  if (calls >= g_ws_max_calls) {
+    buf.zero_();  // a fill kernel on the current stream, before this call's launch
+    ++g_ws_clears;
+    calls = 0;
+  }
+  ++calls;
   w.ptr = buf.data_ptr();
   w.bytes = (size_t)buf.numel();
   return w;
@@ -632,8 +653,25 @@ PyObject* workspace_error(PyObject*, PyObject* arg) {
   Py_RETURN_FALSE;
 }
 
+// set_workspace_max_calls(n) -> the previous limit; n <= 0 restores
+// RLK_WORKSPACE_MAX_CALLS.  For tests of the re-zeroing of cached workspaces.
+PyObject* set_workspace_max_calls(PyObject*, PyObject* arg) {
+  const long long n = PyLong_AsLongLong(arg);
+  if (n == -1 && PyErr_Occurred()) return nullptr;
+  const uint64_t prev = g_ws_max_calls;
+  g_ws_max_calls = n <= 0 ? (uint64_t)RLK_WORKSPACE_MAX_CALLS : (uint64_t)n;
+  return PyLong_FromUnsignedLongLong(prev);
+}
+
+PyObject* workspace_clears(PyObject*, PyObject*) { return PyLong_FromUnsignedLongLong(g_ws_clears); }
+
 PyMethodDef kMethods[] = {
     {"entry", make_entry, METH_VARARGS, "entry(op, names, npos, defaults, required, fallback)"},
+    {"set_workspace_max_calls", set_workspace_max_calls, METH_O,
+     "set_workspace_max_calls(n) -> previous limit of long-row calls between zero-fills of a "
+     "cached workspace (n <= 0: the default, RLK_WORKSPACE_MAX_CALLS)"},
+    {"workspace_clears", workspace_clears, METH_NOARGS,
+     "workspace_clears() -> cached workspaces zero-filled again at the call limit so far"},
     {"launched", launched, METH_NOARGS, "launched() -> calls the fast path has launched so far"},
     {"workspace_error", workspace_error, METH_O,
      "workspace_error(device) -> True if a look-back wait of this module's calls gave up"},

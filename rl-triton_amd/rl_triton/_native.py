@@ -180,6 +180,26 @@ def _check(status: int, what: str) -> None:
 # ---------------------------------------------------------------------------------------
 _workspaces: dict = {}
 _ws_need: dict = {}
+# Status words carry a 30-bit count of the calls made on their workspace, which wraps after
+# 2^30 long-row calls; a word left 2^30 calls earlier would then read as current.  A cached
+# workspace is therefore zero-filled again (a fill kernel on its own stream, ordered before
+# the call) once it has served WORKSPACE_MAX_CALLS long-row calls -- the C ABI's
+# RLK_WORKSPACE_MAX_CALLS, which tests may lower.
+WORKSPACE_MAX_CALLS = 1 << 29
+_ws_calls: dict = {}
+_ws_clears = 0
+
+
+def _count_call(key, ws) -> None:
+    """Count one long-row call on workspace `ws` (cache key `key`), zero-filling it first
+    when it has already served WORKSPACE_MAX_CALLS calls since it was last zeroed."""
+    global _ws_clears
+    n = _ws_calls.get(key, 0)
+    if n >= WORKSPACE_MAX_CALLS:
+        ws.zero_()
+        _ws_clears += 1
+        n = 0
+    _ws_calls[key] = n + 1
 # Buffers of calls captured into a HIP graph.  A captured call gets its own, allocated (and
 # zero-filled, by a kernel the graph records) inside the capture, so every replay starts
 # from a clean buffer and no replay shares one with eager calls, whatever streams they run
@@ -211,6 +231,8 @@ def _workspace(dev: int, stream: int, n_env: int, n_t: int):
             raise RuntimeError("workspace stream mismatch")
         ws = torch.zeros(size, dtype=torch.uint8, device=torch.device("cuda", dev))
         _workspaces[(dev, stream)] = ws
+        _ws_calls[(dev, stream)] = 0
+    _count_call((dev, stream), ws)
     return ws.data_ptr(), ws.numel()
 
 

@@ -226,3 +226,31 @@ def test_gae_normalized_checks_match_compute_gae():
         _check_gae_args(t, t, t, None, t, _Gpu(4))
     with pytest.raises(AssertionError, match="cannot be combined with truncateds"):
         _check_gae_args(t, t, t, t, None, _Gpu(4))
+
+
+def test_workspace_call_limit_is_below_the_epoch_wrap():
+    """The call limit between zero-fills of a workspace (RLK_WORKSPACE_MAX_CALLS, mirrored by
+    the Python binding) is below the 2^30 calls after which the status words' call count
+    (kEpochMask in the engine) wraps."""
+    text = open(HEADER).read()
+    limit = int(eval(re.search(r"#define RLK_WORKSPACE_MAX_CALLS \(([^)]*)\)", text).group(1)))
+    engine = open(os.path.join(ROOT, "rl-triton_amd", "csrc", "rlk_engine.hpp")).read()
+    mask = int(re.search(r"kEpochMask = (0x[0-9a-fA-F]+)u", engine).group(1), 16)
+    assert limit == _native.WORKSPACE_MAX_CALLS == 1 << 29
+    assert limit < mask + 1
+
+
+def test_workspace_rezeroed_at_call_limit(monkeypatch):
+    """A cached workspace that has served WORKSPACE_MAX_CALLS long-row calls is zero-filled
+    before the next one (here on a CPU stand-in with the limit lowered to 3)."""
+    monkeypatch.setattr(_native, "WORKSPACE_MAX_CALLS", 3)
+    key = ("cpu-test", 0)
+    monkeypatch.setitem(_native._ws_calls, key, 0)
+    ws = torch.full((64,), 7, dtype=torch.uint8)
+    zeroed_before = []
+    for call in range(1, 11):
+        _native._count_call(key, ws)
+        zeroed_before.append(bool((ws == 0).all()))
+        ws.fill_(7)
+    assert [c for c, z in zip(range(1, 11), zeroed_before) if z] == [4, 7, 10]
+    del _native._ws_calls[key]

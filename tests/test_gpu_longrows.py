@@ -124,16 +124,22 @@ def test_many_tiles_per_row(op, shape, device):
 
 def test_lookback_give_up_poisons_with_nan(device):
     """A look-back wait that gives up -- forced here from the host with a budget of zero
-    polls (rlk_debug_lookback), so that every tile whose predecessors are not all
-    published at its first poll gives up at once -- sets the workspace error flag and writes
-    NaN for its tile and every tile chained through it, never plausible wrong values.  Every
-    other element is still right, and nothing waits: the kernel ends normally."""
+    polls (rlk_debug_lookback), so that every tile whose 64 nearest predecessors do not
+    already lead to a published state at its first poll gives up at once -- sets the
+    workspace error flag and writes NaN for its tile and every tile chained through it,
+    never plausible wrong values.  The row has no dones, so no tile's map ignores its carry
+    and every tile needs a state from up to 255 tiles before it: the far tiles cannot have
+    one at their first poll, so some wait does give up.  NaN then covers whole tiles only,
+    the row's first tile (which takes the row's own carry) is never NaN, every other
+    element is right, and nothing waits: the kernel ends normally."""
     import torch
     from rl_triton import _native
     lib = _native.load()
-    op, E, T = "prefix_sum", 1, 1 << 23  # 256 tiles: most cannot see a state at their first poll
-    inp, params = _inputs(op, E, T, seed=13)
+    op, E, T = "prefix_sum", 1, 1 << 23
+    inp, params = make_inputs(op, E, T, seed=13, p_done=0.0)
     exp = run_oracle(op, inp, params)[0]
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    tile = next(1024 * 4 * q for q in (8, 4, 2) if E * -(-T // (1024 * 4 * q)) >= cus or q == 2)
     stream = torch.cuda.Stream(device)
     assert lib.rlk_debug_lookback(0, -1) == 0
     try:
@@ -143,12 +149,15 @@ def test_lookback_give_up_poisons_with_nan(device):
     finally:
         lib.rlk_debug_lookback(-1, -1)
     key = (torch.device(device).index, stream.cuda_stream)
-    ws = _native._workspaces.pop(key)  # this stream's workspace, made for this call
+    ws = _native._workspaces.pop(key)  # this stream's workspace: do not reuse its flag
     flagged = int(ws[24:32].cpu().view(torch.int64).item()) != 0
     g = got.cpu().numpy()
     nan = np.isnan(g)
-    print(f"gave up: {flagged}, NaN elements: {int(nan.sum())} of {g.size}")
-    assert flagged == bool(nan.any())
+    per_tile = nan.reshape(E, -1, tile)
+    print(f"gave up: {flagged}, NaN tiles: {int(per_tile.all(axis=2).sum())} of {per_tile.shape[1]}")
+    assert flagged and nan.any()
+    assert np.array_equal(per_tile.any(axis=2), per_tile.all(axis=2)), "NaN covers part of a tile"
+    assert not per_tile[:, 0].any(), "the row's first tile takes the row carry, never NaN"
     assert_close(g[~nan], exp[~nan], 1e-5, _atol(op, inp, exp), f"{op}[{E},{T}] outside the NaN tiles")
 
 
@@ -196,4 +205,44 @@ def test_grids_larger_than_the_gpu(op, shape, device):
     wait gives up."""
     from rl_triton import _native
     _check(op, *shape, seed=73, device=device)
+    assert not _native.workspace_error(device)
+
+
+@pytest.mark.parametrize("path", ["python", "fast"])
+def test_workspace_rezeroed_at_call_limit(path, device, monkeypatch):
+    """Each binding zero-fills its cached workspace again after RLK_WORKSPACE_MAX_CALLS
+    long-row calls (the status words' 30-bit call count would wrap after 2^30).  With the
+    limit lowered to 3: once the stream's workspace has been re-zeroed (within the first
+    few calls, however many calls it served before), nine more calls of changing shapes
+    re-zero it exactly three more times; every call matches the oracle and no wait gives
+    up.  The largest workspace comes first, so the cache never grows (which also resets
+    the count) during the test."""
+    import torch
+    from rl_triton import _native
+    seq = [("gae", 130, 2100), ("prefix_sum", 3, 70000), ("vtrace", 2, 131073),
+           ("discounted_returns", 64, 4096), ("forward_scan", 9, 33333)]
+    if path == "fast":
+        monkeypatch.delenv("RL_TRITON_CORRECTNESS_WARNINGS")
+        clears = _native.fast.workspace_clears
+        prev = _native.fast.set_workspace_max_calls(3)
+    else:
+        clears = lambda: _native._ws_clears  # noqa: E731
+        monkeypatch.setattr(_native, "WORKSPACE_MAX_CALLS", 3)
+    try:
+        stream = torch.cuda.Stream(device)
+        with torch.cuda.stream(stream):
+            _check(*seq[0], seed=499, device=device)  # the workspace exists, large enough
+            start, i = clears(), 0
+            while clears() == start:
+                assert i < 4, "no re-zeroing within the call limit"
+                _check(*seq[i % len(seq)], seed=500 + i, device=device)
+                i += 1
+            first = clears()
+            for j in range(9):
+                _check(*seq[(i + j) % len(seq)], seed=600 + j, device=device)
+            torch.cuda.synchronize()
+            assert clears() - first == 3
+    finally:
+        if path == "fast":
+            _native.fast.set_workspace_max_calls(prev)
     assert not _native.workspace_error(device)
