@@ -60,6 +60,8 @@ extern "C" {
 #define RLK_ERR_INVALID_ARGUMENT (-1)
 #define RLK_ERR_WORKSPACE (-2)
 #define RLK_ERR_LAUNCH (-3)
+#define RLK_ERR_SCRATCH_LIMIT (-4) /* rlk_gae_noalloc: the call needs more than its static buffer */
+#define RLK_ERR_DEVICE (-5)        /* a HIP device query or set-up call failed */
 
 #define RLK_BOOT_NONE 0
 #define RLK_BOOT_ROW 1
@@ -101,6 +103,26 @@ int rlk_gae(const float *rewards, const float *values, const float *terminateds,
             const float *truncateds, const float *bootstrap, int boot_mode, float *advantages,
             int64_t num_envs, int64_t seq_len, float gamma, float lambda_, void *workspace,
             size_t workspace_bytes, void *stream);
+
+/* GAE that allocates nothing and takes no workspace.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory -- code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  Arguments, results and error codes are
+ * rlk_gae's without `workspace`/`workspace_bytes`.  Rows longer than 2048 steps keep their
+ * look-back status words in a static device buffer of the library, RLK_NOALLOC_SCRATCH_BYTES
+ * (1 MiB) on each GPU it runs on, held until the process ends; a call whose
+ * rlk_workspace_bytes(num_envs, seq_len) exceeds it (more than 12900 row tiles of 4096
+ * steps, e.g. [4096, 16384]) returns RLK_ERR_SCRATCH_LIMIT and launches nothing.  All calls
+ * on one GPU share that GPU's buffer, which keeps the last call's contents: calls that
+ * overlap on one GPU (other streams, other host threads) race.  The first call on a device
+ * that needs the buffer also enqueues a small kernel on `stream` that clears it, as does
+ * every RLK_WORKSPACE_MAX_CALLS-th such call after that, and every such call made while
+ * `stream` captures a graph (so each replay starts from a clear buffer).  No memset and
+ * no allocating routine is called. */
+#define RLK_NOALLOC_SCRATCH_BYTES (1 << 20)
+int rlk_gae_noalloc(const float *rewards, const float *values, const float *terminateds,
+                    const float *truncateds, const float *bootstrap, int boot_mode,
+                    float *advantages, int64_t num_envs, int64_t seq_len, float gamma,
+                    float lambda_, void *stream);
 
 /* GAE with skipped steps ("verl-style" masking, listed in the reference's
  * ROADMAP.md:131-140; no counterpart in the reference).  mask [num_envs, seq_len]: a step

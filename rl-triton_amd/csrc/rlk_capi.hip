@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "rl_triton_amd.h"
 #include "rlk_ops.hpp"
@@ -451,6 +452,68 @@ int affine_scan_impl(const E* u, const E* v, const E* carry, E* out, int64_t num
   return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
 }
 
+// ---------------------------------------------------------------------------------------
+// rlk_gae_noalloc: the look-back workspace of long rows in a static device array instead of
+// a caller's buffer, for callers that cannot allocate.  Each GPU holds its own copy of
+// `scratch`; host code never uses the array's name as an address (on the host it is only a
+// stand-in) but the address hipGetSymbolAddress returns for the current device, kept per
+// device.  The array must start from zero (the look-back's counters at rest, no status
+// word tagged with the current call count): clear_scratch zeroes it on the first eager call
+// on a device, every RLK_WORKSPACE_MAX_CALLS calls after that (before the status words'
+// 30-bit call count can wrap), and in every captured call, so that each graph replay starts
+// from zero.  The whole array is cleared, not just the call's share: a clear also resets the
+// call count, and words of an earlier, larger call must not outlive it.
+// ---------------------------------------------------------------------------------------
+constexpr int64_t kNoAllocWords = RLK_NOALLOC_SCRATCH_BYTES / (int64_t)sizeof(uint64_t);
+static __device__ __align__(256) uint64_t scratch[kNoAllocWords];
+
+__global__ __launch_bounds__(256) void clear_scratch(uint64_t* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    p[i] = 0;
+}
+
+constexpr int kMaxDevices = 64;
+struct NoAllocDevice {
+  std::mutex mu;
+  uint64_t* ptr = nullptr;  // this device's copy of `scratch`
+  bool cleared = false;     // an eager clear has been enqueued since set-up
+  uint64_t calls = 0;       // long-row eager calls since that clear
+};
+NoAllocDevice g_noalloc[kMaxDevices];
+
+// The current device's scratch, cleared first when due (on `stream`).
+int noalloc_scratch(void* stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return RLK_ERR_DEVICE;
+  NoAllocDevice& d = g_noalloc[dev];
+  std::lock_guard<std::mutex> lock(d.mu);
+  if (d.ptr == nullptr) {  // set-up, once per device, with that device current
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr)
+      return RLK_ERR_DEVICE;
+    d.ptr = static_cast<uint64_t*>(p);
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess) return RLK_ERR_DEVICE;
+  const bool capturing = cs != hipStreamCaptureStatusNone;
+  if (capturing || !d.cleared || d.calls >= (uint64_t)RLK_WORKSPACE_MAX_CALLS) {
+    uint64_t* p = d.ptr;
+    int64_t n = kNoAllocWords;
+    void* args[] = {&p, &n};
+    if (hipLaunchKernel(reinterpret_cast<const void*>(&clear_scratch), dim3(128), dim3(256), args,
+                        0, s) != hipSuccess)
+      return RLK_ERR_LAUNCH;
+    if (!capturing) {
+      d.cleared = true;
+      d.calls = 0;
+    }
+  }
+  if (!capturing) ++d.calls;
+  *out = d.ptr;
+  return RLK_OK;
+}
+
 // rlk_bf16 (raw bits) <-> the kernels' bf16 storage type
 const bf16* B(const rlk_bf16* p) { return reinterpret_cast<const bf16*>(p); }
 bf16* B(rlk_bf16* p) { return reinterpret_cast<bf16*>(p); }
@@ -470,6 +533,10 @@ const char* rlk_status_string(int status) {
     case RLK_ERR_INVALID_ARGUMENT: return "invalid argument";
     case RLK_ERR_WORKSPACE: return "workspace missing, too small or misaligned";
     case RLK_ERR_LAUNCH: return "kernel launch failed";
+    case RLK_ERR_SCRATCH_LIMIT:
+      return "the call needs more look-back scratch than rlk_gae_noalloc's static buffer "
+             "(RLK_NOALLOC_SCRATCH_BYTES) holds";
+    case RLK_ERR_DEVICE: return "HIP device query or set-up failed";
     default: return "unknown status";
   }
 }
@@ -490,6 +557,25 @@ int rlk_gae(const float* rewards, const float* values, const float* terminateds,
             size_t workspace_bytes, void* stream) {
   return gae_impl(rewards, values, terminateds, truncateds, bootstrap, boot_mode, advantages,
                   num_envs, seq_len, gamma, lambda_, workspace, workspace_bytes, stream);
+}
+
+int rlk_gae_noalloc(const float* rewards, const float* values, const float* terminateds,
+                    const float* truncateds, const float* bootstrap, int boot_mode,
+                    float* advantages, int64_t num_envs, int64_t seq_len, float gamma,
+                    float lambda_, void* stream) {
+  if (is_empty(num_envs, seq_len)) return RLK_OK;
+  if (num_envs < 0 || seq_len < 0 || seq_len > (int64_t{1} << 30)) return RLK_ERR_INVALID_ARGUMENT;
+  void* ws = nullptr;
+  const size_t need = workspace_bytes(num_envs, seq_len);
+  if (need > 0) {
+    if (num_envs > kNoAllocWords || need > (size_t)RLK_NOALLOC_SCRATCH_BYTES)
+      return RLK_ERR_SCRATCH_LIMIT;
+    const int st = noalloc_scratch(stream, &ws);
+    if (st != RLK_OK) return st;
+  }
+  return gae_impl(rewards, values, terminateds, truncateds, bootstrap, boot_mode, advantages,
+                  num_envs, seq_len, gamma, lambda_, ws, ws ? (size_t)RLK_NOALLOC_SCRATCH_BYTES : 0,
+                  stream);
 }
 
 int rlk_gae_bf16(const rlk_bf16* rewards, const rlk_bf16* values, const rlk_bf16* terminateds,

@@ -33,6 +33,7 @@ _SZ = ctypes.c_size_t
 # name -> argtypes (must match include/rl_triton_amd.h)
 SIGNATURES = {
     "rlk_gae": [_P, _P, _P, _P, _P, _INT, _P, _I64, _I64, _F, _F, _P, _SZ, _P],
+    "rlk_gae_noalloc": [_P, _P, _P, _P, _P, _INT, _P, _I64, _I64, _F, _F, _P],
     "rlk_gae_masked": [_P, _P, _P, _P, _P, _INT, _P, _P, _I64, _I64, _F, _F, _P, _SZ, _P],
     "rlk_gae_normalized": [_P, _P, _P, _P, _P, _INT, _P, _P, _I64, _I64, _F, _F, _F, _P, _SZ, _P,
                            _SZ, _P],

@@ -254,3 +254,16 @@ def test_workspace_rezeroed_at_call_limit(monkeypatch):
         ws.fill_(7)
     assert [c for c, z in zip(range(1, 11), zeroed_before) if z] == [4, 7, 10]
     del _native._ws_calls[key]
+
+
+def test_noalloc_entry_refuses_before_any_device_call():
+    """rlk_gae_noalloc checks sizes on the host: a call whose look-back status words exceed
+    its static buffer, or with negative sizes, is refused without a HIP call (so also here,
+    without a GPU); an empty call is a no-op."""
+    lib = _native.load()
+    p = 4096  # never dereferenced
+    assert lib.rlk_gae_noalloc(p, p, p, None, None, 0, p, 4096, 16384, 0.99, 0.95, None) == -4
+    assert lib.rlk_gae_noalloc(p, p, p, None, None, 0, p, -1, 5000, 0.99, 0.95, None) == -1
+    assert lib.rlk_gae_noalloc(None, None, None, None, None, 0, None, 0, 5000, 0.99, 0.95, None) == 0
+    assert b"static buffer" in lib.rlk_status_string(-4)
+    assert b"device" in lib.rlk_status_string(-5)
