@@ -34,11 +34,19 @@ Printed JSON (one line, stdout):
   element_aligned_rows
                  C2, C3 and the C5 prefix sum one step short of a multiple of four
                  ([4096,127], [8,2^20-1]): quads that are only element-aligned
+  independent_ceilings
+                 the same bytes moved by torch copy_ (hipMemcpyAsync device to device: a
+                 copy of half the bytes reads and writes them all) on rotating buffers, and
+                 the dispatch floor: back-to-back launches of a kernel that moves 32 KB
   cpu_baseline   the reference's sequential torch loops (restated in
-                 oracle/torch_loops.py) on the host CPU, 1 thread, bounded sample; this
-                 CPU leg also checks the headline outputs against the float64 oracle
-                 (parity_max_abs_err) and against those float32 loops
-                 (parity_vs_reference_loops_max_abs_err)
+                 oracle/torch_loops.py) on the host CPU, bounded sample: the headline step
+                 (GAE C2 + V-trace C3) with the host's thread share and with 1 thread, and
+                 C1's reference_gae at [64, 512] by the reference's _bench_cpu method; CPU
+                 model and thread counts recorded.  This CPU leg also checks the headline
+                 outputs against the float64 oracle (parity_max_abs_err) and against those
+                 float32 loops (parity_vs_reference_loops_max_abs_err), and every
+                 configuration's set-0 outputs against both (configs[*].max_abs_err,
+                 max_abs_err_f32_loop: the reference's float32 loop's own error)
 """
 from __future__ import annotations
 
@@ -144,6 +152,27 @@ def parity_vs_loops(torch, cpu_sets, outs):
             "vtrace_advantages": d(outs[1][1], ad)}
 
 
+def config_errors(np, kept):
+    """Max abs error of each configuration's set-0 outputs against the float64 oracle, and
+    the error of the reference's float32 sequential loop (oracle.loop32) on the same inputs:
+    the north star's bar is the former no larger than (twice) the latter."""
+    from _common import OUTPUTS, run_oracle
+    from oracle import oracle as orc
+    import baseline_configs as bc
+    res = {}
+    for name, (inp, params, outs) in kept.items():
+        op = bc.CONFIGS[name][0]
+        n = {k: v.numpy() for k, v in inp.items()}
+        exp = run_oracle(op, n, params)
+        loop = orc.loop32(op, n, params)
+        err = max(float(np.max(np.abs(o.numpy().astype(np.float64) - e))) for o, e in zip(outs, exp))
+        err_loop = max(float(np.max(np.abs(lp.astype(np.float64) - e))) for lp, e in zip(loop, exp))
+        res[name] = {"max_abs_err": err, "max_abs_err_f32_loop": err_loop,
+                     "outputs": list(OUTPUTS[op])}
+        log(f"[bench] {name}: max abs err {err:.3e} vs float64 (the float32 loop: {err_loop:.3e})")
+    return res
+
+
 def time_ops(torch, rl, sets, iters, batch=100):
     """Average device duration of each op's kernel, from HIP events on the launch stream.
     Each batch of `batch` calls is queued behind a GPU spin, so the GPU runs the kernels
@@ -166,11 +195,12 @@ def time_ops(torch, rl, sets, iters, batch=100):
     return res
 
 
-def time_configs(torch, names, min_launches=200, batch=50, dtype=None):
+def time_configs(torch, names, min_launches=200, batch=50, dtype=None, keep=None):
     """Average kernel duration of every BASELINE configuration's public-API call (one
     kernel launch per call), from HIP events around batches of back-to-back launches queued
     behind a GPU spin, over rotating input sets of more than 3 x 256 MB.  dtype=bfloat16:
-    the same calls with bfloat16 I/O (float32 arithmetic)."""
+    the same calls with bfloat16 I/O (float32 arithmetic).  keep: a dict that receives each
+    configuration's first input set and outputs, on the host."""
     import baseline_configs as bc
     dtype = dtype or torch.float32
     dev = torch.device("cuda:0")
@@ -184,7 +214,10 @@ def time_configs(torch, names, min_launches=200, batch=50, dtype=None):
         sets = [bc.make(name, seed=100 + i, device=dev) for i in range(n_sets)]
         sets = [(bc.as_dtype(inp, dtype), params) for inp, params in sets]
         for i in range(min(n_sets, 8)):
-            bc.call(name, *sets[i])
+            outs = bc.call(name, *sets[i])
+            if i == 0 and keep is not None:  # set 0, its outputs, for the CPU leg's parity check
+                keep[name] = ({k: v.cpu() for k, v in sets[0][0].items()}, sets[0][1],
+                              [o.cpu() for o in outs])
         torch.cuda.synchronize()
         total_ms, n = 0.0, 0
         while n < min_launches:
@@ -320,6 +353,51 @@ def time_stream_ceiling(torch, sets):
     sweep["asymptotic_gb_s"] = round(1e-3 / slope, 1)
     log(f"[bench] stream ceiling sweep (V-trace pattern): {sweep}")
     res["vtrace_pattern_sweep"] = sweep
+    return res
+
+
+def time_independent_ceilings(torch, ops):
+    """Ceilings measured without this project's kernels, timed like the kernels (batches of
+    back-to-back calls queued behind a GPU spin, rotating over more than 3 x 256 MB):
+      copy_  torch's device-to-device copy (hipMemcpyAsync) of half the headline kernel's
+             bytes, so that its reads plus writes equal the kernel's algorithmic bytes;
+      dispatch_floor  a launch of the streaming kernel over 8192 floats (2 workgroups,
+             32 KB read and written): what any kernel launch costs back to back."""
+    import ctypes
+    dev = torch.device("cuda:0")
+    res = {}
+    for name in ("gae", "vtrace"):
+        nbytes = ops[name]["bytes_per_launch"]
+        n = nbytes // 2 // 4
+        n_sets = max(2, -(-3 * MALL_BYTES // nbytes) + 1)
+        bufs = [(torch.empty(n, device=dev), torch.empty(n, device=dev)) for _ in range(n_sets)]
+        for src, _ in bufs:
+            src.normal_()
+        us = _device_us(torch, lambda src, dst: dst.copy_(src), bufs)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[f"copy_{name}_bytes"] = {"device_us": round(us, 3), "bytes_moved": nbytes,
+                                     "gb_s": round(gbs, 1), "pct_peak": round(100 * gbs / PEAK_GBS, 2),
+                                     "kernel_frac_of_copy": round(us / ops[name]["device_us"], 3)}
+        log(f"[bench] copy_ of {nbytes / 2 / 1e6:.2f} MB (moves {nbytes / 1e6:.2f} MB, like {name}): "
+            f"{us:.2f} us/call, {gbs:.0f} GB/s")
+        del bufs
+    lib = ctypes.CDLL(os.path.join(ROOT, "rl-triton_amd", "rl_triton", "librlk_stream_ceiling.so"))
+    fn = lib.rlk_stream_ceiling
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.POINTER(ctypes.c_void_p),
+                   ctypes.c_int, ctypes.c_int64, ctypes.c_void_p]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    small = [(torch.empty(8192, device=dev), torch.empty(8192, device=dev)) for _ in range(4)]
+    calls = [((ctypes.c_void_p * 1)(a.data_ptr()), (ctypes.c_void_p * 1)(b.data_ptr())) for a, b in small]
+
+    def tiny(pin, pout):
+        if fn(pin, 1, pout, 1, 8192, stream) != 0:
+            raise RuntimeError("rlk_stream_ceiling failed")
+
+    us = _device_us(torch, tiny, calls, min_launches=400, batch=100)
+    res["dispatch_floor"] = {"device_us": round(us, 3), "workgroups": 2, "bytes_moved": 2 * 8192 * 4}
+    log(f"[bench] dispatch floor (2-workgroup kernel back to back): {us:.2f} us/launch")
+    torch.cuda.empty_cache()
     return res
 
 
@@ -529,30 +607,93 @@ def time_launch_paths(torch, calls=2000):
     return res
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def _host_threads():
+    """The host's thread share: os.cpu_count(), as BASELINE.md prescribes, capped at this
+    job's CPU share (OMP_NUM_THREADS, which the GPU box sets to 16 for one GPU)."""
+    n = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS")
+    return min(n, int(cap)) if cap and cap.isdigit() and int(cap) > 0 else n
+
+
 def cpu_baseline(torch, cpu_sets, budget_s):
+    """The reference's sequential torch loops on the host, as oracle/torch_loops.py restates
+    them.  The headline step (GAE C2 + V-trace C3 at [4096, 128]) is timed for `budget_s`
+    seconds with the host's thread share (the reported value) and again with one thread;
+    C1's reference_gae at [64, 512] is timed by the reference's _bench_cpu method
+    (tests/bench_utils.py:184-195: 3 warm-ups, then at least 0.5 s and 5 calls, mean).
+    Per-step vectors of 64-4096 floats are below ATen's 32768-element grain for intra-op
+    threads, so these loops run on one core whatever the thread count."""
     from oracle import torch_loops
+    import baseline_configs as bc
     gae, vt = cpu_sets
     prev = torch.get_num_threads()
-    torch.set_num_threads(1)
-    try:
+
+    def step():
+        torch_loops.gae_loop(gae["rewards"], gae["values"], gae["terminateds"], gae["truncateds"],
+                             0.99, 0.95, bootstrap_values=gae["bootstrap_values"])
+        torch_loops.vtrace_loop(vt["log_pi_target"], vt["log_pi_behavior"], vt["values"],
+                                vt["rewards"], vt["terminateds"], 0.99, 1.0, 1.0,
+                                last_value=vt["last_value"])
+
+    def timed_steps(seconds):
         n, t0 = 0, time.perf_counter()
         while True:
-            torch_loops.gae_loop(gae["rewards"], gae["values"], gae["terminateds"], gae["truncateds"],
-                                 0.99, 0.95, bootstrap_values=gae["bootstrap_values"])
-            torch_loops.vtrace_loop(vt["log_pi_target"], vt["log_pi_behavior"], vt["values"],
-                                    vt["rewards"], vt["terminateds"], 0.99, 1.0, 1.0,
-                                    last_value=vt["last_value"])
+            step()
             n += 1
             el = time.perf_counter() - t0
-            if el >= budget_s:
-                break
+            if el >= seconds:
+                return n, el
+
+    threads = _host_threads()
+    try:
+        torch.set_num_threads(threads)
+        used = torch.get_num_threads()
+        n, el = timed_steps(budget_s)
+        torch.set_num_threads(1)
+        n1, el1 = timed_steps(budget_s / 2)
+        # C1: reference_gae at [64, 512], terminateds 0, last_value (tests/test_gae.py:34-60)
+        c1, c1p = bc.make("C1_gae_64x512", seed=0)
+        torch.set_num_threads(threads)
+
+        def c1_call():
+            torch_loops.gae_loop(c1["rewards"], c1["values"], c1["terminateds"], None,
+                                 c1p["gamma"], c1p["lambda_"], last_value=c1["last_value"])
+
+        for _ in range(3):
+            c1_call()
+        k, t0 = 0, time.perf_counter()
+        while k < 5 or time.perf_counter() - t0 < 0.5:
+            c1_call()
+            k += 1
+        c1_ms = 1e3 * (time.perf_counter() - t0) / k
     finally:
         torch.set_num_threads(prev)
-    return {"value": 2 * E * T * n / el / 1e9, "unit": "Gelem/s", "cores": 1, "kind": "port",
-            "sample": f"{n} full steps (GAE C2 + V-trace C3 at [{E},{T}]) in {el:.1f} s, "
-                      f"torch CPU loops of oracle/torch_loops.py, 1 thread, "
-                      f"host {platform.processor() or platform.machine()} ({os.cpu_count()} cpus)",
-            "ms_per_step": 1e3 * el / n}
+    model = _cpu_model()
+    return {"value": 2 * E * T * n / el / 1e9, "unit": "Gelem/s", "cores": used, "kind": "port",
+            "sample": f"{n} full steps (GAE C2 + V-trace C3 at [{E},{T}]) in {el:.1f} s, torch CPU "
+                      f"loops of oracle/torch_loops.py, torch.set_num_threads({threads}) "
+                      f"(os.cpu_count() = {os.cpu_count()}, capped at the job's CPU share), "
+                      f"{model}; per-step vectors are below ATen's intra-op grain, so one core works",
+            "ms_per_step": 1e3 * el / n, "cpu_model": model, "os_cpu_count": os.cpu_count(),
+            "torch_threads": used,
+            "one_thread": {"value": 2 * E * T * n1 / el1 / 1e9, "ms_per_step": 1e3 * el1 / n1,
+                           "sample": f"{n1} steps in {el1:.1f} s, torch.set_num_threads(1)"},
+            "c1_reference_gae_64x512": {
+                "ms_per_call": round(c1_ms, 3), "gelem_s": round(64 * 512 / (c1_ms * 1e-3) / 1e9, 5),
+                "calls": k, "method": "tests/bench_utils.py:184-195 (_bench_cpu): 3 warm-ups, "
+                                      ">= 0.5 s and >= 5 calls, mean",
+                "reference_published_ms": {"RTX 2000 Ada box host": 14.205, "H100 box host": 16.514}}}
 
 
 def main(argv=None):
@@ -610,8 +751,8 @@ def main(argv=None):
     torch.cuda.synchronize()
     start.record()
     t0 = time.perf_counter()
-    for i in range(a.steps):
-        s = sets[i % n_sets]
+    for i in range(a.steps):  # from the set after the warm-up's last: the least recently used
+        s = sets[(a.warmup + i) % n_sets]
         run_gae(rl_triton, s[0])
         run_vtrace(rl_triton, s[1])
     end.record()
@@ -638,6 +779,7 @@ def main(argv=None):
     ceiling = time_stream_ceiling(torch, sets)
     for name in ("gae", "vtrace"):
         ceiling[name]["kernel_frac_of_ceiling"] = round(ceiling[name]["device_us"] / ops[name]["device_us"], 3)
+    independent = time_independent_ceilings(torch, ops)
 
     graph_ms = time_graph_steps(torch, rl_triton, sets, a.steps)
     log(f"[bench] graph-replayed step: {graph_ms * 1e3:.2f} us "
@@ -652,7 +794,8 @@ def main(argv=None):
         cfg_names = list(baseline_configs.CONFIGS)
     elif a.configs != "none":
         cfg_names = a.configs.split(",")
-    configs = time_configs(torch, cfg_names) if cfg_names else None
+    kept = {} if not a.no_cpu_baseline else None
+    configs = time_configs(torch, cfg_names, keep=kept) if cfg_names else None
     configs_bf16 = time_configs(torch, cfg_names, dtype=torch.bfloat16) if cfg_names else None
     extensions = time_extensions(torch) if a.configs != "none" else None
     element_aligned = time_element_aligned(torch, configs) if a.configs != "none" else None
@@ -677,6 +820,11 @@ def main(argv=None):
         log(f"[bench] parity vs the reference's float32 loops (max abs err): {errs_loops}")
         if max(errs_loops.values()) > 1e-4:
             raise SystemExit(f"parity check failed: {errs_loops}")
+        if configs and kept:
+            for name, r in config_errors(np, kept).items():
+                configs[name].update(max_abs_err=r["max_abs_err"],
+                                     max_abs_err_f32_loop=r["max_abs_err_f32_loop"])
+            del kept
         log(f"[bench] CPU baseline ({a.cpu_seconds:.0f} s sample) ...")
         cpu = cpu_baseline(torch, cpu_sets, a.cpu_seconds)
         log(f"[bench] CPU baseline: {cpu['value']:.4f} Gelem/s ({cpu['ms_per_step']:.1f} ms/step)")
@@ -691,7 +839,8 @@ def main(argv=None):
                                f"{n_sets} HBM-resident sets",
                    "num_envs": E, "seq_len": T, "gamma": 0.99, "lambda": 0.95,
                    "rho_bar": 1.0, "c_bar": 1.0, "timing": "value: eager public-API calls, HIP events around the timed region"},
-        "roofline": roofline, "ops": ops, "stream_ceiling": ceiling, "configs": configs, "configs_bf16_io": configs_bf16,
+        "roofline": roofline, "ops": ops, "stream_ceiling": ceiling,
+        "independent_ceilings": independent, "configs": configs, "configs_bf16_io": configs_bf16,
         "extensions": extensions, "element_aligned_rows": element_aligned,
         "graph_replay": {"ms_per_step": round(graph_ms, 6),
                          "gelem_s": round(2 * E * T / (graph_ms * 1e-3) / 1e9, 3)},

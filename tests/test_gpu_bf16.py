@@ -152,3 +152,47 @@ def test_bf16_mixed_dtypes_are_rejected(device, monkeypatch):
             rl_triton.compute_discounted_returns(x, b)
         with pytest.raises(AssertionError, match="expected float32"):
             rl_triton.compute_gae(x.double(), x.double(), x.double())
+
+
+# ---------------------------------------------------------------------------------------
+# Precision drift (the study the reference's ROADMAP.md:82-99 names as the prerequisite of
+# bfloat16 support).  Per (op, seq_len), on seeded float32 inputs of 2^20 elements (2^23 at
+# a million steps), each error is max |x - exact| / max |exact|, exact = the float64 oracle
+# on the float32 inputs:
+#   f32 I/O        the float32 kernels;
+#   bf16 I/O       the bfloat16 kernels (inputs rounded to bfloat16, outputs bfloat16);
+#   quantisation   the float64 oracle on the bfloat16-rounded inputs, its result rounded
+#                  to bfloat16: what any bfloat16-I/O implementation loses.
+# The bfloat16 kernels must sit at the quantisation floor (float32 accumulation adds
+# nothing visible), whatever the length; each case prints its row of the table.
+# ---------------------------------------------------------------------------------------
+DRIFT_OPS = ["gae", "vtrace", "retrace", "lambda_returns", "discounted_returns",
+             "eligibility_traces", "prefix_sum"]
+DRIFT_CASES = [(op, T) for op in DRIFT_OPS for T in (128, 2048, 131072)] + \
+              [("eligibility_traces", 1 << 20), ("prefix_sum", 1 << 20)]
+
+
+def _rel(x, exact):
+    scale = float(np.max(np.abs(exact))) or 1.0
+    return float(np.max(np.abs(np.asarray(x, dtype=np.float64) - exact))) / scale
+
+
+@pytest.mark.parametrize("op,T", DRIFT_CASES, ids=lambda v: str(v))
+def test_bf16_drift_at_the_quantisation_floor(op, T, device):
+    E = max(1, (1 << (23 if T == 1 << 20 else 20)) // T)
+    kw = {"p_done": 1e-4} if op in ("prefix_sum", "eligibility_traces") else {}
+    boot = "full" if op in ("gae", "vtrace", "lambda_returns", "discounted_returns") else "none"
+    inp, params = make_inputs(op, E, T, seed=3, p_term=0.01,
+                              p_trunc=0.005 if op != "retrace" else 0.0, boot=boot, **kw)
+    print(f"[case] bf16 drift {op} [{E},{T}]", flush=True)
+    exact = run_oracle(op, inp, params)
+    f32 = run_api(op, inp, params, device)
+    b16 = run_api(op, inp, params, device, dtype=BF16)
+    quant = run_oracle(op, _bf16_values(inp), params)
+    for name, e, a, b, q in zip(OUTPUTS[op], exact, f32, b16, quant):
+        floor = _rel(torch.as_tensor(np.asarray(q, np.float32)).to(BF16).float().numpy(), e)
+        err_b, err_f = _rel(b.float().cpu().numpy(), e), _rel(a.cpu().numpy(), e)
+        print(f"| {op} | {name} | {E} x {T} | {err_f:.1e} | {err_b:.1e} | {floor:.1e} | "
+              f"{err_b / floor:.2f} | {float(np.max(np.abs(e))):.3g} |")
+        assert err_b <= 1.25 * floor + 1e-6, f"{op} T={T} {name}: bf16 {err_b:.2e}, floor {floor:.2e}"
+        assert err_f < 1e-5

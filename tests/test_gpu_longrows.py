@@ -246,3 +246,48 @@ def test_workspace_rezeroed_at_call_limit(path, device, monkeypatch):
         if path == "fast":
             _native.fast.set_workspace_max_calls(prev)
     assert not _native.workspace_error(device)
+
+
+@pytest.mark.parametrize("op,shape", [("discounted_returns", (2, 65536)), ("prefix_sum", (2, 65536)),
+                                      ("discounted_returns", (2, 2000)), ("prefix_sum", (2, 2000))],
+                         ids=lambda v: v if isinstance(v, str) else f"{v[0]}x{v[1]}")
+def test_non_finite_input_after_a_reset(op, shape, device):
+    """An inf reward/input in a row with resets (dones every 300 steps).  The reference's
+    sequential loop makes every later step in scan order non-finite, across resets too
+    (0 * inf and 0 * nan are nan).  Rows of up to 2048 steps do exactly that.  A long row
+    does it up to the end of the first tile, in scan order after the one holding the inf,
+    whose map ignores its carry (a reset inside it): that tile publishes its outgoing value
+    before it knows its carry, computed from a zero carry, so the tiles after it see a
+    finite value.  There each step holds what the row gives with the inf replaced by 0 --
+    a value the inf's episode cannot reach -- and never any other value.  So on every
+    element: the oracle's finite values are matched; where the oracle is not finite the
+    result is either not finite or the zeroed row's value; the non-finite elements form
+    one run in scan order, starting at the inf."""
+    import torch
+    E, T = shape
+    inp, params = make_inputs(op, E, T, seed=31, p_term=0.0, p_done=0.0)
+    key = "rewards" if op == "discounted_returns" else "inputs"
+    dkey = "terminateds" if op == "discounted_returns" else "dones"
+    inp[dkey][:, 150::300] = 1.0
+    at = (T * 3) // 4 if op == "discounted_returns" else T // 4  # backward / forward scans
+    zeroed = {k: (v.copy() if v is not None else None) for k, v in inp.items()}
+    inp[key][:, at] = np.inf
+    zeroed[key][:, at] = 0.0
+    exp = run_oracle(op, inp, params)[0]
+    exp0 = run_oracle(op, zeroed, params)[0]
+    got = run_api(op, inp, params, device)[0].cpu().numpy().astype(np.float64)
+    torch.cuda.synchronize()
+    fin_e, fin_g = np.isfinite(exp), np.isfinite(got)
+    tol = 1e-4 * max(1.0, float(np.max(np.abs(exp0))))
+    assert np.all(np.abs(got[fin_e] - exp[fin_e]) <= tol), "finite oracle values not matched"
+    other = ~fin_e & fin_g
+    assert np.all(np.abs(got[other] - exp0[other]) <= tol), "a finite value that is not the zeroed row's"
+    for n in range(E):  # the non-finite run, in scan order, starts at the inf and is contiguous
+        idx = np.flatnonzero(~fin_g[n])
+        order = idx if op == "prefix_sum" else idx[::-1]
+        assert order[0] == at, "the inf itself is not where the non-finite run starts"
+        assert np.all(np.abs(np.diff(order)) == 1), "the non-finite elements are not one run"
+    if T <= 2048:  # whole rows in one workgroup: the sequential loop's pattern exactly
+        assert np.array_equal(fin_g, fin_e)
+    else:
+        assert np.any(other), "the long row was expected to stop the nan at a tile boundary"
