@@ -31,11 +31,12 @@
  *     stream (concurrent use races).  Zero it again after at most
  *     RLK_WORKSPACE_MAX_CALLS long-row calls: the status words carry a 30-bit count of
  *     the calls made on the workspace, which wraps after 2^30 calls, and a word left by
- *     a call 2^30 calls earlier would then read as current (a silently wrong carry).  Calls that need no workspace ignore the argument
- *     (NULL is fine).  Layout (uint64 words): [0..7] header, word [3] the error flag --
- *     nonzero if a look-back wait gave up or the counters were not at rest (results of
- *     that call are invalid); [8..2055] 64 counter slots; then two places of up to five
- *     status words per tile.
+ *     a call 2^30 calls earlier would then read as current (a silently wrong carry).
+ *     Calls that need no workspace ignore the argument (NULL is fine).
+ *     Layout (uint64 words): [0..7] header, word [3] the error flag -- nonzero if a
+ *     look-back wait gave up or the counters were not at rest (results of that call are
+ *     invalid); [8..2055] 64 slots (start counter and epoch of a slot of rows); then two
+ *     places of up to five status words per tile.
  *   - Return value: RLK_OK or a negative RLK_ERR_* code; rlk_status_string() names it.
  *     Empty inputs (num_envs == 0 or seq_len == 0) return RLK_OK without a launch.
  *   - bfloat16 I/O: every estimator has an `_bf16` twin whose float arrays (inputs,

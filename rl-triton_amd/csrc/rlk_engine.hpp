@@ -371,19 +371,22 @@ struct Halo2 {
 //
 // Workspace (uint64 words), the same layout for every shape so that one buffer serves
 // calls of any shape in stream order:
-//   header   [0..7]               [1] finished-slot counter, [2] epoch of the call,
-//                                 [3] error flag (a bounded wait gave up, or counters were
+//   header   [0..7]               [3] error flag (a bounded wait gave up, or counters were
 //                                 not at rest); others reserved
-//   slots    [8 + 32*s], s < 64   slot s (256 bytes each): +16 counter of the workgroups
-//                                 of rows r = s mod 64 that have started (its own line)
+//   slots    [8 + 32*s], s < 64   slot s (256 bytes each), rows r = s mod 64:
+//                                 +16 counter of the slot's workgroups that have started,
+//                                 +24 epoch of the slot's calls
 //   status   [8 + 32*64 ...]      kStatusWords words per tile, tiles of row r at
 //                                 r*tiles_per_row: what the tile's own workgroup publishes
 //   second   [status + kStatusWords*tiles ...]  the same layout: what other workgroups
 //                                 publish for a tile they computed in its place
 // (tiles counted at the smallest tile; see rlk_workspace_bytes).  Device-scope atomics on
 // one address serialise (~12 ns each on MI355X), so the start counters are spread over 64
-// slots.  The epoch is global and advances once per call, after every workgroup has read
-// it, so a status word left by any earlier call never matches the current one.
+// slots.  Each slot holds a copy of the epoch, and all 64 copies advance once per call
+// (each as soon as every workgroup that reads it has done so: the one that completes a
+// slot's start count advances the copies of its residue class), so they stay equal, a
+// status word left by any earlier call never matches the current epoch, and no workgroup
+// issues an atomic on its way out of the kernel.
 // ---------------------------------------------------------------------------------------
 constexpr int kHeaderWords = 8;
 constexpr int kSlots = 64;
@@ -705,6 +708,13 @@ __host__ __device__ inline int lookback_slots(int64_t E) { return E < kSlots ? (
 // the other waves', so nothing it issued looks pending to the compiler afterwards.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Lane 0's value of a 64-bit register, in every lane.
+__device__ __forceinline__ uint64_t lane0_u64(uint64_t x) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, 0);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), 0);
+  return ((uint64_t)hi << 32) | lo;
+}
+
 // What one look-back read finds for a tile: lane l examines tile k -/+ (1 + base + l) of
 // the row, in its own status words (st) and in those another workgroup published for it
 // (sf, see chain_kernel).  kind: 0 (nothing usable yet), kAgg or kInc; absent: nothing of
@@ -1014,16 +1024,28 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
   // before it; the look-back does not rely on that).
   const uint64_t q_t = blockIdx.x / (unsigned)nslots;
 
-  // The epoch is read first and used once the tile's loads are in flight.  Every workgroup
-  // counts itself in the slot's counter once it has the epoch; the one that completes the
-  // count resets it (and, last of all slots, advances the epoch) when it finishes, after
-  // every workgroup of the call has read the epoch.  The count's result is only read at the
-  // end, so no workgroup waits on an atomic on its way out.
+  // The slot's epoch is read first and used once the tile's loads are in flight.  Every
+  // workgroup counts itself in the slot's counter once it has the epoch (the count is issued
+  // after the epoch load has returned).  The one that completes the count has then seen
+  // every workgroup of the slot read the epoch: once its tile is scanned (the count's result
+  // is back by then) it resets the count and advances the slot's epoch for the next call.
   uint64_t e_raw = 0, drawn = 0;
-  if (tid == 0) e_raw = atomic_ld(ws + 2);
+  if (tid == 0) e_raw = atomic_ld(sc + 24);
   auto count_drawn = [&]() {
     drawn = __hip_atomic_fetch_add(sc + 16, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (drawn >= wgs_per_slot) atomic_st(ws + 3, (uint64_t)1);  // counters were not at rest
+  };
+  // It advances the epoch of every slot this call leaves unused whose index falls on its
+  // slot modulo nslots as well, so that every call advances all 64 epochs once and they stay
+  // equal: a call of another row count maps rows to other slots and other status words, and
+  // a word some earlier call left there must not carry a slot's current epoch.
+  // Called by all of wave 0 (the count is thread 0's): one copy per lane, one store.
+  auto advance_slot = [&](uint32_t epoch) {
+    if (lane0_u64(drawn) == wgs_per_slot - 1) {
+      if (lane == 0) atomic_st(sc + 16, 0);
+      const int s2 = slot + lane * nslots;
+      if (s2 < kSlots) atomic_st(ws + kHeaderWords + kSlotWords * s2 + 24, (uint64_t)((epoch + 1) & kEpochMask));
+    }
   };
 
   Stats st;  // output statistics (ops with kBlockStats)
@@ -1087,6 +1109,7 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
       if (lane == 0) s_map[wave] = wm;
       __syncthreads();
       const uint32_t epoch = s_epoch;
+      if (it == 0 && wave == 0) advance_slot(epoch);
       if (wave == 0) {
         Map tm = Map::identity();
         for (int v = 0; v < NW; ++v) tm = compose(s_map[v], tm);
@@ -1124,20 +1147,11 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
       }
       break;
     }
-  } else if (tid == 0) {
-    s_epoch = (uint32_t)e_raw & kEpochMask;
-    count_drawn();
+  } else if (wave == 0) {  // a slot with fewer rows than the fullest: no tile, only the count
+    if (tid == 0) count_drawn();
+    advance_slot((uint32_t)lane0_u64(e_raw) & kEpochMask);
   }
   if constexpr (Op::kBlockStats) block_stats<NT>(st, op.partials);
-  if (tid == 0 && drawn == wgs_per_slot - 1) {
-    atomic_st(sc + 16, 0);
-    const uint64_t slots_done =
-        __hip_atomic_fetch_add(ws + 1, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (slots_done == (uint64_t)nslots - 1) {
-      atomic_st(ws + 1, 0);
-      atomic_st(ws + 2, (uint64_t)((s_epoch + 1) & kEpochMask));
-    }
-  }
 }
 
 }  // namespace rlk

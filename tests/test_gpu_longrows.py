@@ -109,6 +109,36 @@ def test_concurrent_streams(device):
     assert not _native.workspace_error(device)
 
 
+@pytest.mark.parametrize("path", ["python", "fast"])
+def test_row_counts_change_on_a_new_workspace(path, device, monkeypatch):
+    """A new stream (so a new, zeroed workspace) and long-row calls whose row counts change
+    from call to call, growing and shrinking past the 64 slots: rows then fall in other
+    slots and use other status words, so the words an earlier call published lie where a
+    later call's rows now look.  One row first (the 19 tiles of row 0), then two rows of 10
+    tiles (row 1's words are row 0's last nine): a word an earlier call left must never
+    carry the current epoch of the slot that reads it.  Every result matches the oracle
+    and no wait gives up."""
+    import torch
+    from rl_triton import _native
+    if path == "fast":
+        monkeypatch.delenv("RL_TRITON_CORRECTNESS_WARNINGS")
+    shapes = [("prefix_sum", 1, 600000), ("prefix_sum", 2, 300000), ("discounted_returns", 3, 200001),
+              ("prefix_sum", 70, 9000), ("discounted_returns", 5, 100000), ("prefix_sum", 64, 12000),
+              ("discounted_returns", 1, 400000), ("prefix_sum", 9, 65537)]
+    stream = torch.cuda.Stream(device)
+    pending = []
+    with torch.cuda.stream(stream):
+        for i, (op, E, T) in enumerate(shapes):
+            inp, params = _inputs(op, E, T, seed=500 + i)
+            pending.append((op, E, T, inp, params, run_api(op, inp, params, device)))
+    torch.cuda.synchronize()
+    for op, E, T, inp, params, got in pending:
+        exp = run_oracle(op, inp, params)
+        for name, g, e in zip(OUTPUTS[op], got, exp):
+            assert_close(g.cpu().numpy(), e, 1e-5, _atol(op, inp, e), f"{op}[{E},{T}] in sequence:{name}")
+    assert not _native.workspace_error(device)
+
+
 @pytest.mark.parametrize("op,shape", [("prefix_sum", (1, 1 << 23)), ("vtrace", (1, 1 << 21)),
                                       ("gae_masked", (1, 1 << 20)), ("backward_scan", (1, 3 << 20)),
                                       ("discounted_returns", (2, 1 << 21)),
