@@ -1039,7 +1039,8 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
   // slot modulo nslots as well, so that every call advances all 64 epochs once and they stay
   // equal: a call of another row count maps rows to other slots and other status words, and
   // a word some earlier call left there must not carry a slot's current epoch.
-  // Called by all of wave 0 (the count is thread 0's): one copy per lane, one store.
+  // Called by all of wave 0 (the count is thread 0's) once its look-back is done: one copy
+  // per lane, one store.
   auto advance_slot = [&](uint32_t epoch) {
     if (lane0_u64(drawn) == wgs_per_slot - 1) {
       if (lane == 0) atomic_st(sc + 16, 0);
@@ -1109,7 +1110,6 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
       if (lane == 0) s_map[wave] = wm;
       __syncthreads();
       const uint32_t epoch = s_epoch;
-      if (it == 0 && wave == 0) advance_slot(epoch);
       if (wave == 0) {
         Map tm = Map::identity();
         for (int v = 0; v < NW; ++v) tm = compose(s_map[v], tm);
@@ -1125,6 +1125,7 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
             s_next = need;
           }
         }
+        if (it == 0) advance_slot(epoch);  // after the look-back: off its path
       }
       __syncthreads();
       const int next = s_next;
