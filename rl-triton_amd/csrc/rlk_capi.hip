@@ -106,9 +106,9 @@ hipError_t launch_rows(const Op& op, int64_t E, int T, hipStream_t stream) {
   const int64_t grid = rows_grid(E, T, S, NT);
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   void* args[] = {const_cast<Op*>(&op), &E, &T, &log2L};
-  // aligned 4-step rows of 33..2048 steps: the instance whose scan width is fixed
+  // 4-step rows of 33..2048 steps: the instance whose scan width is fixed
   const void* k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC>);
-  if constexpr (S == 4 && VEC) {
+  if constexpr (S == 4) {
     if (log2L == 4) k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC, 16>);
     else if (log2L == 5) k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC, 32>);
     else if (log2L >= 6) k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC, kWave>);

@@ -642,7 +642,8 @@ __device__ __forceinline__ M lane_scan(M m, int W) {
 // log2L at run time.  With W = 16 or 32, L = W is fixed too.  A fixed width leaves the lane
 // scan and the index arithmetic straight-line code the compiler schedules across: V-trace
 // [4096,128] 4.12 -> 3.99 us, GAE 3.99 -> 3.80 us, GAE [8192,64] 3.97 -> 3.78 us, TD(lambda)
-// [256,2048] 3.61 -> 3.48 us on MI355X (bit-identical results).
+// [256,2048] 3.61 -> 3.48 us, element-aligned V-trace [4096,127] 4.80 -> 4.66 us on MI355X
+// (bit-identical results).
 template <class Op, int NT, int S, bool VEC, int WT = 0>
 __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T, int log2L_arg) {
   constexpr bool FWD = Op::kForward;
