@@ -28,8 +28,8 @@ pytestmark = pytest.mark.gpu
 BF16 = torch.bfloat16
 OPS = ["gae", "gae_masked", "vtrace", "retrace", "lambda_returns", "discounted_returns",
        "eligibility_traces", "prefix_sum", "backward_scan", "forward_scan"]
-SHAPES = [(1, 1), (1, 7), (33, 257), (4096, 128), (16, 2048), (3, 1100), (2, 5001), (3, 5000),
-          (2, 40000)]
+SHAPES = [(1, 1), (1, 7), (5, 64), (9, 61), (6, 127), (33, 257), (4096, 128), (16, 2048), (3, 1100),
+          (2, 5001), (3, 5000), (2, 40000)]
 
 
 def _inputs(op, shape, seed):

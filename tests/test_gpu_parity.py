@@ -82,6 +82,20 @@ def test_parity_shapes(op, shape, device):
     _check(op, inp, params, device, 1e-5, 1e-5, f"{op}{shape}")
 
 
+@pytest.mark.parametrize("op", OPS)
+@pytest.mark.parametrize("shape", [(3, 32), (5, 33), (7, 61), (9, 64), (6, 65), (3, 127), (2, 128),
+                                   (4, 129), (3, 256), (2, 257), (8200, 64), (4100, 128),
+                                   (2050, 256)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_parity_scan_width_instances(op, shape, device):
+    """Row lengths on both sides of each change of short-row kernel instance: up to 32 steps
+    the scan width comes from the launch; 33-64, 65-128 and 129-2048 steps run instances
+    with the width fixed at compile time (16, 32, 64), aligned (T % 4 == 0) or not, in
+    256-thread workgroups (few rows) and 512-thread ones (the larger E, ragged last
+    workgroup)."""
+    inp, params = make_inputs(op, *shape, seed=77)
+    _check(op, inp, params, device, 1e-5, 1e-5, f"{op}{shape}")
+
+
 @pytest.mark.parametrize("op", ["gae", "vtrace", "lambda_returns", "discounted_returns"])
 @pytest.mark.parametrize("boot", ["none", "row", "full"])
 @pytest.mark.parametrize("trunc", [0.0, 0.05])
