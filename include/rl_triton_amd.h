@@ -43,7 +43,7 @@
  *     bootstrap, seed and outputs alike) are bfloat16, passed as rlk_bf16 (the raw 16
  *     bits).  The arithmetic stays float32: a bfloat16 result is the float32 entry
  *     point's result on the same (widened) inputs, rounded to nearest even as torch's
- *     float -> bfloat16 conversion rounds it (NaN -> 0x7fc0).  The reference accepts
+ *     float -> bfloat16 conversion on the GPU rounds it (NaN -> 0x7fc0).  The reference accepts
  *     float32 only (its ROADMAP.md:82-99 lists this as planned); the twins have no
  *     counterpart there.
  */

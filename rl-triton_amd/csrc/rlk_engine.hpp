@@ -122,11 +122,22 @@ template <class E>
 __device__ __forceinline__ E from_f32(float x);
 template <>
 __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+// gfx950's v_cvt_pk_bf16_f32 (what the compiler emits for a float -> __bf16 conversion)
+// rounds to nearest even exactly as the integer form (u + 0x7fff + lsb) >> 16 does, for
+// every non-NaN float, denormals and infinities included: the two agree on all 2^32 bit
+// patterns on MI355X.  It keeps a NaN's sign and payload, so NaN is mapped to 0x7fc0
+// after it.  Two values convert in one instruction.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+  if (lo != lo) w = (w & 0xffff0000u) | 0x7fc0u;
+  if (hi != hi) w = (w & 0x0000ffffu) | 0x7fc00000u;
+  return w;
+}
 template <>
 __device__ __forceinline__ bf16 from_f32<bf16>(float x) {
-  const uint32_t u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return bf16{0x7fc0};
-  return bf16{(uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16)};
+  return bf16{(uint16_t)pack_bf16x2(x, 0.f)};
 }
 
 // ---------------------------------------------------------------------------------------
@@ -170,9 +181,7 @@ __device__ __forceinline__ void store_quad(float* p, float4 v) {
 }
 template <bool NT = false>
 __device__ __forceinline__ void store_quad(bf16* p, float4 v) {
-  const uint32_t a = from_f32<bf16>(v.x).bits, b = from_f32<bf16>(v.y).bits;
-  const uint32_t c = from_f32<bf16>(v.z).bits, d = from_f32<bf16>(v.w).bits;
-  const nt_u2 w = {a | (b << 16), c | (d << 16)};
+  const nt_u2 w = {pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
   if constexpr (NT) __builtin_nontemporal_store(w, reinterpret_cast<nt_u2*>(p));
   else *reinterpret_cast<nt_u2*>(p) = w;
 }
@@ -196,9 +205,7 @@ __device__ __forceinline__ void store_quad_ua(float* p, float4 v) {
   *reinterpret_cast<ua_f4*>(p) = ua_f4{v.x, v.y, v.z, v.w};
 }
 __device__ __forceinline__ void store_quad_ua(bf16* p, float4 v) {
-  const uint32_t a = from_f32<bf16>(v.x).bits, b = from_f32<bf16>(v.y).bits;
-  const uint32_t c = from_f32<bf16>(v.z).bits, d = from_f32<bf16>(v.w).bits;
-  *reinterpret_cast<ua_u2*>(p) = ua_u2{a | (b << 16), c | (d << 16)};
+  *reinterpret_cast<ua_u2*>(p) = ua_u2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
 }
 // Element k of a quad, k >= 3 giving the last one.
 __device__ __forceinline__ float quad_elem(float4 f, int k) {

@@ -76,6 +76,43 @@ def test_bf16_is_float32_result_rounded(op, shape, path, device, monkeypatch):
                                  f"float32 result {r.flatten()[i].item()!r}")
 
 
+@pytest.mark.parametrize("op", ["discounted_returns", "prefix_sum", "vtrace", "gae"])
+@pytest.mark.parametrize("shape", [(6, 128), (3, 61), (2, 5000)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_bf16_rounding_of_non_finite_and_tiny_results(op, shape, device):
+    """bfloat16 outputs round as torch's conversion on the GPU does (`Tensor.to`), for
+    results that are NaN of either sign (0x7fc0), infinite, float32 denormals or halfway
+    cases: NaN, infinities, denormal and halfway-valued inputs are planted in the rows (the
+    bfloat16 twins convert on gfx950's v_cvt_pk_bf16_f32 and map NaN to 0x7fc0 afterwards).
+    torch's vectorised CPU conversion writes NaN as 0xffff instead, so the CPU is not the
+    reference here."""
+    inp, params = _inputs(op, shape, seed=5)
+    inp = _bf16_values(inp)
+    key = {"discounted_returns": "rewards", "prefix_sum": "inputs", "vtrace": "rewards",
+           "gae": "rewards"}[op]
+    x = np.array(inp[key], dtype=np.float32)
+    E, T = x.shape
+    rng = np.random.default_rng(9)
+    specials = np.array([np.nan, -np.nan, np.inf, -np.inf, 1e-39, -3e-40, 1e-45,
+                         np.float32(1.0 + 2.0 ** -8), -np.float32(3.0 * 2.0 ** -9)], dtype=np.float32)
+    neg_nan = np.frombuffer(np.uint32(0xFFC00001).tobytes(), dtype=np.float32)[0]
+    specials = np.concatenate([specials, [neg_nan]]).astype(np.float32)
+    for e in range(E):
+        cols = rng.choice(T, size=min(T, len(specials)), replace=False)
+        x[e, cols] = specials[:len(cols)]
+    inp[key] = torch.as_tensor(x).to(BF16).float().numpy()
+    got = run_api(op, inp, params, device, dtype=BF16)
+    ref = run_api(op, inp, params, device, dtype=torch.float32)
+    for name, g, r in zip(OUTPUTS[op], got, ref):
+        want = r.to(BF16)
+        same = _bits(g) == _bits(want)
+        assert bool(same.all()), (f"{op}{shape}:{name}: {int((~same).sum())} elements differ; first "
+                                  f"got {hex(int(_bits(g).flatten()[(~same).flatten()][0]) & 0xffff)} "
+                                  f"want {hex(int(_bits(want).flatten()[(~same).flatten()][0]) & 0xffff)}")
+        nan_bits = (_bits(g)[torch.isnan(g)].int() & 0xffff).unique().tolist()
+        assert nan_bits in ([], [0x7fc0]), f"{op}:{name}: NaN written as {[hex(b) for b in nan_bits]}"
+    assert any(bool(torch.isnan(g).any()) for g in got), "no NaN result: the NaN path was not exercised"
+
+
 def _longest_run(d):
     best = 0
     for row in np.asarray(d) > 0:
