@@ -1042,8 +1042,9 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
   // The slot's epoch is read first and used once the tile's loads are in flight.  Every
   // workgroup counts itself in the slot's counter once it has the epoch (the count is issued
   // after the epoch load has returned).  The one that completes the count has then seen
-  // every workgroup of the slot read the epoch: once its tile is scanned (the count's result
-  // is back by then) it resets the count and advances the slot's epoch for the next call.
+  // every workgroup of the slot read the epoch: once its tile's look-back is done (the
+  // count's result is back long before) it resets the count and advances the slot's epoch
+  // for the next call.
   uint64_t e_raw = 0, drawn = 0;
   if (tid == 0) e_raw = atomic_ld(sc + 24);
   auto count_drawn = [&]() {
