@@ -96,6 +96,40 @@ def test_parity_scan_width_instances(op, shape, device):
     _check(op, inp, params, device, 1e-5, 1e-5, f"{op}{shape}")
 
 
+def _sweep_cases(n=40, seed=2024):
+    """Seeded random (op, E, T, bootstrap, truncation) cases, T up to 2300 so that every
+    short-row instance and the first long-row tiles are reached."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        op = OPS[i % len(OPS)]
+        T = int(rng.choice([rng.integers(1, 70), rng.integers(70, 600), rng.integers(600, 2300)]))
+        E = int(rng.integers(1, 300 if T < 600 else 40))
+        boot = str(rng.choice(["none", "row", "full"])) if op in (
+            "gae", "vtrace", "lambda_returns", "discounted_returns") else "row"
+        if op in ("lambda_returns", "discounted_returns") and boot == "row":
+            boot = "full"
+        trunc = float(rng.choice([0.0, 0.05])) if op in (
+            "gae", "vtrace", "lambda_returns", "discounted_returns") else 0.0
+        if op == "gae" and boot == "row":
+            trunc = 0.0
+        cases.append((op, E, T, boot, trunc, 1000 + i))
+    return cases
+
+
+@pytest.mark.parametrize("case", _sweep_cases(), ids=lambda c: f"{c[0]}-{c[1]}x{c[2]}-{c[3]}-{c[4]}")
+def test_parity_random_shapes(case, device):
+    """A seeded sweep of random shapes, bootstrap modes and truncation rates for every op."""
+    op, E, T, boot, trunc, seed = case
+    inp, params = make_inputs(op, E, T, seed=seed, p_trunc=trunc, boot=boot)
+    rtol, atol = 1e-5, 1e-5
+    if T > 2048:
+        atol = 1e-5 * math.sqrt(max(1.0 / (1.0 - 0.99), 128) / 128.0)
+        if op == "prefix_sum":
+            atol = 1e-5 * math.sqrt(max(float(T), 128) / 128.0)
+    _check(op, inp, params, device, rtol, atol, f"{op}[{E},{T}] boot={boot} trunc={trunc}")
+
+
 @pytest.mark.parametrize("op", ["gae", "vtrace", "lambda_returns", "discounted_returns"])
 @pytest.mark.parametrize("boot", ["none", "row", "full"])
 @pytest.mark.parametrize("trunc", [0.0, 0.05])
