@@ -100,6 +100,19 @@ int64_t launch_grid(int64_t E, int64_t T) {
   return rows_grid(E, T, 4, rows_threads(E, T));
 }
 
+// Ops whose aligned short rows of 65..128 steps run two row groups per thread
+// (rows_pair_kernel): in place of a 512-thread workgroup, a 256-thread one whose threads
+// each hold a row of the first and of the second half (same grid, half the waves, twice the
+// loads in flight per wave).  float32 Retrace (nine arrays per step) gains from it: C4
+// [4096,128] 6.55 -> 6.41 us on MI355X.  Elsewhere the second row's scan lengthens each
+// wave's path after its loads: GAE [4096,128] 3.81 -> 3.98 us, V-trace 3.99 -> 4.22 us,
+// TD(lambda) 3.11 -> 3.18 us, bfloat16 Retrace 4.77 -> 5.20 us; Retrace [8192,64] is
+// unchanged (6.39-6.58 us either way).
+template <class Op>
+struct paired_rows : std::false_type {};
+template <int NA, bool TRUNC>
+struct paired_rows<RetraceOp<NA, TRUNC, float>> : std::true_type {};
+
 template <class Op, int NT, int S, bool VEC>
 hipError_t launch_rows(const Op& op, int64_t E, int T, hipStream_t stream) {
   int log2L = ceil_log2((T + S - 1) / S);
@@ -108,6 +121,12 @@ hipError_t launch_rows(const Op& op, int64_t E, int T, hipStream_t stream) {
   void* args[] = {const_cast<Op*>(&op), &E, &T, &log2L};
   // 4-step rows of 33..2048 steps: the instance whose scan width is fixed
   const void* k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC>);
+  if constexpr (S == 4 && VEC && NT == kNTWide && paired_rows<Op>::value) {
+    if (log2L == 5) {
+      k = reinterpret_cast<const void*>(&rows_pair_kernel<Op, NT / 2, 32>);
+      return hipLaunchKernel(k, dim3((unsigned)grid), dim3(NT / 2), args, 0, stream);
+    }
+  }
   if constexpr (S == 4) {
     if (log2L == 4) k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC, 16>);
     else if (log2L == 5) k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC, 32>);

@@ -151,6 +151,18 @@ def test_retrace_action_counts(n_act, shape, device):
     _check("retrace", inp, params, device, 1e-5, 1e-5, f"retrace A={n_act}{shape}")
 
 
+@pytest.mark.parametrize("n_act", [1, 2, 3, 4])
+@pytest.mark.parametrize("trunc", [0.0, 0.02])
+@pytest.mark.parametrize("shape", [(4100, 128), (4097, 100), (8192, 68)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_retrace_paired_rows(n_act, trunc, shape, device):
+    """float32 Retrace on aligned rows of 65..128 steps in a grid of at least one 512-thread
+    workgroup per compute unit runs two row groups per thread (256-thread workgroups); the
+    last workgroup's second group is partly or wholly past the last row."""
+    inp, params = make_inputs("retrace", *shape, seed=5, n_act=n_act, p_trunc=trunc)
+    params = dict(params, c_bar=0.9, rho_bar=0.8)
+    _check("retrace", inp, params, device, 1e-5, 1e-5, f"retrace A={n_act}{shape} trunc={trunc}")
+
+
 @pytest.mark.parametrize("boundary", ["ends_at", "starts_at"])
 @pytest.mark.parametrize("seed_row", [False, True])
 @pytest.mark.parametrize("shape", [(64, 512), (5, 3001), (2, 20000)], ids=lambda s: f"{s[0]}x{s[1]}")
