@@ -15,6 +15,7 @@ namespace {
 constexpr int kNT = 256;          // short rows: threads per workgroup of small calls (4 wavefronts)
 constexpr int kNTWide = 512;      // short rows otherwise (8 wavefronts; one row of 1025..2048 steps)
 constexpr int kShortMaxT = 2048;  // rows up to this length are kept whole in one workgroup
+constexpr int kStridedThreads = 256, kStridedSegments = 2;  // rows of 1025..2048 steps
 static_assert(kNTWide >= kShortMaxT / 4, "a short row (up to 512 threads of 4 steps) fits one workgroup");
 // Long rows: each op fixes its threads per workgroup (kLongThreads) and the most 4-step
 // segments per thread its registers hold without spilling (kLongMaxSegments, 2..8).  The
@@ -135,6 +136,32 @@ hipError_t launch_rows(const Op& op, int64_t E, int T, hipStream_t stream) {
   return hipLaunchKernel(k, dim3((unsigned)grid), dim3(NT), args, 0, stream);
 }
 
+// Aligned rows of 1025..2048 steps: one row per 256-thread workgroup, two wave-strided
+// segments per thread (rows_strided_kernel), grid = E, for every op but V-trace and
+// Retrace, in both storage types (so that a bfloat16 result stays the float32 kernels'
+// result rounded).  Against rows_kernel's 512 threads of one segment, on MI355X:
+// TD(lambda) [256,2048] 3.47 -> 3.35 us, prefix sum [256,2048] 3.28 -> 3.09 us (bfloat16
+// 3.12 -> 3.06), GAE [256,2048] 4.33 -> 4.27 us, TD(lambda) [512,1100] 4.14 -> 4.00 us,
+// the other bfloat16 calls unchanged.  V-trace (4.42 -> 4.44 us, bfloat16 3.88 -> 3.99)
+// and Retrace (6.66 -> 6.64 us, bfloat16 5.47 -> 5.74) keep rows_kernel, as do
+// element-aligned rows ([256,2047] 3.76 -> 3.78 us).
+template <class Op>
+struct strided_rows : std::true_type {};
+template <bool TRUNC, class E>
+struct strided_rows<VtraceOp<TRUNC, E>> : std::false_type {};
+template <int NA, bool TRUNC, class E>
+struct strided_rows<RetraceOp<NA, TRUNC, E>> : std::false_type {};
+
+template <class Op>
+hipError_t launch_strided(const Op& op, int64_t E, int T, hipStream_t stream) {
+  static_assert(kStridedThreads * kSeg * kStridedSegments == kShortMaxT, "one row per workgroup");
+  if (E > 0x7fffffffLL) return hipErrorInvalidValue;
+  int unused = 0;
+  void* args[] = {const_cast<Op*>(&op), &E, &T, &unused};
+  return hipLaunchKernel(reinterpret_cast<const void*>(&rows_strided_kernel<Op, kStridedThreads, kStridedSegments, true>),
+                         dim3((unsigned)E), dim3(kStridedThreads), args, 0, stream);
+}
+
 // Look-back poll budgets (rlk_debug_lookback): polls before a wait gives up (~1 s), and
 // polls before a wait on a predecessor that has published nothing computes it instead.
 constexpr int kFallbackPolls = 256;
@@ -182,6 +209,8 @@ int launch(const Op& op, int64_t E, int64_t T, bool vec, void* workspace, size_t
     if (ws == nullptr || workspace_bytes_given < workspace_bytes(E, T) || !aligned16(ws))
       return RLK_ERR_WORKSPACE;
     e = vec ? launch_long<Op, true>(op, E, Ti, ws, s) : launch_long<Op, false>(op, E, Ti, ws, s);
+  } else if (strided_rows<Op>::value && vec && T > kShortMaxT / 2) {
+    e = launch_strided(op, E, Ti, s);
   } else if (rows_seg(T) == 1) {
     e = launch_rows<Op, kNT, 1, false>(op, E, Ti, s);
   } else if (rows_threads(E, T) == kNT) {

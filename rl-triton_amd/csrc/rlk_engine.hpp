@@ -1078,6 +1078,88 @@ __device__ __forceinline__ SkipAffine lane_bcast(SkipAffine m, int l) {
 
 constexpr int kSeg = 4;  // steps per segment of the long-row path
 
+// Rows of 1025..2048 steps, one per workgroup, with the long-row tile layout: NT threads
+// hold Q segments of 4 steps each, strided by the wave (segment q of lane l at step
+// (q*64 + l)*4 of the wave's chunk), so every vector access of a wave covers 1 KB.  Against
+// one segment per thread (rows_kernel with NT = 512) a row has half the waves, so its wave
+// maps chain through LDS in at most NW - 1 = 3 applies instead of 7.  Launch: grid = E.
+template <class Op, int NT, int Q, bool VEC>
+__global__ __launch_bounds__(NT) void rows_strided_kernel(const Op op, int64_t E, int T, int) {
+  constexpr bool FWD = Op::kForward;
+  constexpr int NW = NT / kWave;
+  constexpr int S = 4;
+  constexpr int WSTEPS = Q * kWave * S;  // steps per wave chunk
+  using Regs = typename Op::template Regs<S>;
+  using Halo = typename Op::Halo;
+  using Map = typename Op::Map;
+  using State = typename Map::State;
+  constexpr bool HAS_HALO = !std::is_same<Halo, NoHalo>::value;
+  __shared__ Map s_map[NW];
+
+  const int tid = threadIdx.x;
+  const int lane = __lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int64_t row = blockIdx.x;
+  // lane space -> time: this wave's chunk, and the first step of segment row r
+  const int wbase = (FWD ? wave : NW - 1 - wave) * WSTEPS;
+  const int lt = FWD ? lane : kWave - 1 - lane;
+  auto seg_t0 = [&](int r) { return wbase + ((FWD ? r : Q - 1 - r) * kWave + lt) * S; };
+
+  Regs R[Q];
+#pragma unroll
+  for (int r = 0; r < Q; ++r) op.template load<S, VEC>(row, seg_t0(r), T, R[r]);
+  Halo edge{};
+  if constexpr (HAS_HALO) {
+    if (lane == 0 && (FWD ? wbase > 0 : wbase + WSTEPS < T))
+      edge = op.halo_load(row, clamp_step(FWD ? wbase - 1 : wbase + WSTEPS, T), T);
+  }
+  State carry = row_carry(op, row, T);
+#pragma unroll
+  for (int r = 0; r < Q; ++r) op.template prepare<S, VEC>(R[r], row, seg_t0(r), T);
+
+  // neighbour step of each segment (the one before it in scan order): the previous lane,
+  // lane 63 of the previous segment row, or the edge load
+  Halo h[Q];
+#pragma unroll
+  for (int r = 0; r < Q; ++r) {
+    if constexpr (HAS_HALO) {
+      const Halo prev = lane_prev(scan_export<Op, S>(op, R[r]));
+      const Halo wrap = r > 0 ? lane_bcast(scan_export<Op, S>(op, R[r > 0 ? r - 1 : 0]), kWave - 1) : edge;
+      h[r] = lane == 0 ? wrap : prev;
+    }
+  }
+  Map steps[Q][S];
+  Map m[Q];
+  Map rowagg[Q];  // map of each segment row (wave-uniform)
+#pragma unroll
+  for (int r = 0; r < Q; ++r) {
+    op.template coef<S, VEC>(R[r], h[r], row, seg_t0(r), T, steps[r]);
+    m[r] = lane_scan(fold_segment<FWD, S>(steps[r]), kWave);
+    rowagg[r] = lane_bcast(m[r], kWave - 1);
+  }
+  // the chunk's map: segment rows composed in scan order
+  Map wm = rowagg[0];
+#pragma unroll
+  for (int r = 1; r < Q; ++r) wm = compose(rowagg[r], wm);
+  if (lane == 0) s_map[wave] = wm;
+  __syncthreads();
+  // state entering this wave's chunk, then each segment row, then each lane
+  for (int v = 0; v < wave; ++v) carry = s_map[v].apply(carry);
+  Stats st;
+#pragma unroll
+  for (int r = 0; r < Q; ++r) {
+    State x_in = lane_prev(m[r].apply(carry));
+    if (lane == 0) x_in = carry;
+    carry = rowagg[r].apply(carry);
+    State xs[S];
+    replay<FWD, S>(steps[r], x_in, xs);
+    op.template emit<S, VEC>(R[r], h[r], xs, x_in, row, seg_t0(r), T);
+    if constexpr (Op::kBlockStats) op.template stats<S>(R[r], xs, seg_t0(r), T, st);
+  }
+  if constexpr (Op::kBlockStats) block_stats<NT>(st, op.partials);
+}
+
+
 template <class Op, int NT, int Q, bool VEC>
 __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T, int tiles_per_row,
                                                    uint64_t* __restrict__ ws, uint64_t* __restrict__ fb,

@@ -96,6 +96,17 @@ def test_parity_scan_width_instances(op, shape, device):
     _check(op, inp, params, device, 1e-5, 1e-5, f"{op}{shape}")
 
 
+@pytest.mark.parametrize("op", OPS)
+@pytest.mark.parametrize("shape", [(5, 1028), (3, 1500), (40, 2044), (300, 2048), (2, 1027)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_parity_rows_of_1025_to_2048_steps(op, shape, device):
+    """Aligned rows of 1025..2048 steps run one row per 256-thread workgroup with two
+    wave-strided segments per thread (all ops but V-trace and Retrace), padding segments and
+    padding waves included; element-aligned rows (1027 steps) keep one segment per thread."""
+    inp, params = make_inputs(op, *shape, seed=91)
+    _check(op, inp, params, device, 1e-5, 1e-5, f"{op}{shape}")
+
+
 def _sweep_cases(n=40, seed=2024):
     """Seeded random (op, E, T, bootstrap, truncation) cases, T up to 2300 so that every
     short-row instance and the first long-row tiles are reached."""
