@@ -619,8 +619,9 @@ def _cpu_model():
 
 
 def _host_threads():
-    """The host's thread share: os.cpu_count(), as BASELINE.md prescribes, capped at this
-    job's CPU share (OMP_NUM_THREADS, which the GPU box sets to 16 for one GPU)."""
+    """The host's thread share: os.cpu_count() (the thread count the CPU baseline is
+    specified at), capped at this job's CPU share (OMP_NUM_THREADS, which the GPU box sets to
+    16 for one GPU)."""
     n = os.cpu_count() or 1
     cap = os.environ.get("OMP_NUM_THREADS")
     return min(n, int(cap)) if cap and cap.isdigit() and int(cap) > 0 else n
