@@ -13,9 +13,10 @@ namespace {
 
 // Launch geometry.
 constexpr int kNT = 256;          // short rows: threads per workgroup of small calls (4 wavefronts)
-constexpr int kNTWide = 512;      // short rows otherwise (8 wavefronts; one row of 1025..2048 steps)
+constexpr int kNTWide = 512;      // short rows otherwise (8 wavefronts; one row of 1025..2048
+                                  // steps where rows_strided_kernel is not used)
 constexpr int kShortMaxT = 2048;  // rows up to this length are kept whole in one workgroup
-constexpr int kStridedThreads = 256, kStridedSegments = 2;  // rows of 1025..2048 steps
+constexpr int kStridedThreads = 256, kStridedSegments = 2;  // rows_strided_kernel's tile
 static_assert(kNTWide >= kShortMaxT / 4, "a short row (up to 512 threads of 4 steps) fits one workgroup");
 // Long rows: each op fixes its threads per workgroup (kLongThreads) and the most 4-step
 // segments per thread its registers hold without spilling (kLongMaxSegments, 2..8).  The
