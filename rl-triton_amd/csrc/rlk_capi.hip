@@ -94,9 +94,26 @@ int64_t chain_grid(int64_t E, int64_t T, int NT, int Q) {
 // up; rows of 1-3 steps take one step per thread, element by element.
 int rows_seg(int64_t T) { return T < 4 ? 1 : 4; }
 
+// Discounted returns without truncations (512-thread tiles of up to 8 segments per thread):
+// a call that gives every CU a tile of 16384 steps runs them as 1024 threads x 4 segments
+// instead of 512 x 8, the same tiles.  On MI355X: [64,65536] 11.58 -> 10.37 us; four
+// segments per thread were the fastest shape wherever they gave every CU a tile (C5
+// [16,131072] keeps 512 x 4, 8.12 us, against 8.41 at 1024 x 2).
+template <class Op>
+struct wide_long_tiles : std::false_type {};
+template <class E>
+struct wide_long_tiles<ReturnsOp<false, false, E>> : std::true_type {};
+constexpr int kWideLongThreads = 1024, kWideLongSegments = 4;
+bool wide_long_call(int64_t E, int64_t T) {
+  const int64_t tile = (int64_t)kWideLongThreads * kSeg * kWideLongSegments;
+  return E * ((T + tile - 1) / tile) >= device_cus();
+}
+
 // Workgroups of the launch that launch() makes for Op at [E, T] (E, T > 0).
 template <class Op>
 int64_t launch_grid(int64_t E, int64_t T) {
+  if (T > kShortMaxT && wide_long_tiles<Op>::value && wide_long_call(E, T))
+    return chain_grid(E, T, kWideLongThreads, kWideLongSegments);
   if (T > kShortMaxT) return chain_grid(E, T, Op::kLongThreads, long_segments<Op>(E, T));
   if (rows_seg(T) == 1) return rows_grid(E, T, 1, kNT);
   return rows_grid(E, T, 4, rows_threads(E, T));
@@ -171,9 +188,8 @@ std::atomic<int> g_fallback_polls{kFallbackPolls};
 
 // Long rows: one tile of kLongThreads * 4 * Q steps per workgroup, grid = nslots * (tiles
 // of the fullest slot) (see chain_kernel in rlk_engine.hpp).
-template <class Op, int Q, bool VEC>
+template <class Op, int Q, bool VEC, int NT = Op::kLongThreads>
 hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_t stream) {
-  constexpr int NT = Op::kLongThreads;
   static_assert(NT * kSeg * Q >= kMinTile, "the workspace is sized for the smallest tile");
   constexpr int64_t tile = (int64_t)NT * kSeg * Q;
   int tpr = (int)((T + tile - 1) / tile);
@@ -189,6 +205,8 @@ hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_
 
 template <class Op, bool VEC>
 hipError_t launch_long(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_t stream) {
+  if constexpr (wide_long_tiles<Op>::value)
+    if (wide_long_call(E, T)) return launch_chain<Op, kWideLongSegments, VEC, kWideLongThreads>(op, E, T, ws, stream);
   const int q = long_segments<Op>(E, T);
   if constexpr (Op::kLongMaxSegments >= 8)
     if (q == 8) return launch_chain<Op, 8, VEC>(op, E, T, ws, stream);

@@ -226,6 +226,31 @@ def test_lookback_fallback_paths_give_the_same_bits(op, shape, dtype, device):
     assert not _native.workspace_error(device)
 
 
+@pytest.mark.parametrize("boot", ["none", "full"])
+@pytest.mark.parametrize("shape", [(64, 65536), (300, 16385), (256, 16383)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
+def test_discounted_returns_wide_tiles(shape, boot, device):
+    """Discounted returns without truncations, on calls that give every compute unit a tile of
+    16384 steps, run 1024-thread tiles of four segments per thread (aligned rows, a ragged
+    last tile, element-aligned rows): float32 against the oracle, and bfloat16 bit-identical
+    to the float32 kernels' result rounded."""
+    import torch
+    from rl_triton import _native
+    inp, params = make_inputs("discounted_returns", *shape, seed=88, boot=boot)
+    got = run_api("discounted_returns", inp, params, device)
+    exp = run_oracle("discounted_returns", inp, params)
+    for name, g, e in zip(OUTPUTS["discounted_returns"], got, exp):
+        assert_close(g.cpu().numpy(), e, 1e-5, _atol("discounted_returns", inp, e),
+                     f"discounted{shape}:{name}")
+    assert not _native.workspace_error(device)
+    rounded = {k: (None if v is None else torch.as_tensor(v).to(torch.bfloat16).float().numpy())
+               for k, v in inp.items()}
+    got_b = run_api("discounted_returns", rounded, params, device, dtype=torch.bfloat16)
+    ref = run_api("discounted_returns", rounded, params, device, dtype=torch.float32)
+    for g, r in zip(got_b, ref):
+        assert torch.equal(g.view(torch.int16), r.to(torch.bfloat16).view(torch.int16))
+
+
 @pytest.mark.parametrize("op,shape", [("vtrace", (2048, 16384)), ("prefix_sum", (1024, 1 << 16)),
                                       ("gae_masked", (600, 12000))],
                          ids=lambda v: v if isinstance(v, str) else f"{v[0]}x{v[1]}")
