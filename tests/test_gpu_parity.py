@@ -3,8 +3,8 @@ float64 CPU oracle and the reference's known answers.
 
 Tolerances (stated per test):
   * known answers: rtol = atol = 1e-5 (the reference's own bar for them);
-  * seq_len <= 2048: rtol = 1e-5, atol = 1e-5 * max(1, max|expected|) against the float64
-    oracle (plain 1e-5 at the BASELINE configurations), and no further from it than 2x the
+  * seq_len <= 2048: rtol = atol = 1e-5 against the float64 oracle (discounted returns:
+    atol = 1e-5 * max(1, max|expected|), see _check), and no further from it than 2x the
     reference's float32 sequential loop on the same inputs (oracle.loop32, the reference's
     torch loops restated in C) plus 1e-6;
   * long rows (look-back path): atol = 1e-5 * sqrt(L_eff / 128) * max(1, max|ref|), rtol = 1e-5,
@@ -50,16 +50,21 @@ def loop_gate(op, inp, params, got, exp, what, floor=1e-6):
 
 
 def _check(op, inp, params, device, rtol, atol, what):
-    """atol is scaled by max(1, max|expected|) here: an element near zero in a row of large
-    values (discounted returns over 2048 steps reach ~30) is a difference of large terms,
-    so its float32 rounding error is relative to them (e.g. 1.9e-5 at an element of 0.0095
-    in discounted returns [256, 2048]); the float32-loop gate bounds the error tightly."""
+    """rtol and atol as given (1e-5 at rows of up to 2048 steps), except for discounted
+    returns and rows longer than 2048 steps, where atol is scaled by max(1, max|expected|):
+    an element near zero in a row of large values (undamped discounted returns over 2048
+    steps reach ~25) is a difference of large terms, so its float32 rounding error is
+    relative to them (e.g. 1.9e-5 at an element of 0.0095 in discounted returns
+    [256, 2048]; the reference's own float32 loop reaches 0.75 of the plain tolerance
+    there).  The float32-loop gate bounds every result tightly."""
     got = run_api(op, inp, params, device)
     exp = run_oracle(op, inp, params)
     torch.cuda.synchronize()
     got = [g.cpu().numpy() for g in got]
+    T = int(np.asarray(got[0]).shape[-1]) if got and np.asarray(got[0]).ndim else 0
     for name, g, e in zip(OUTPUTS[op], got, exp):
-        scale = max(1.0, float(np.max(np.abs(e)))) if e.size else 1.0
+        scaled = op == "discounted_returns" or T > 2048
+        scale = max(1.0, float(np.max(np.abs(e)))) if (e.size and scaled) else 1.0
         assert_close(g, e, rtol, atol * scale, f"{what}:{name}")
     loop_gate(op, inp, params, got, exp, what)
     return got, exp
