@@ -227,13 +227,14 @@ def test_lookback_fallback_paths_give_the_same_bits(op, shape, dtype, device):
 
 
 @pytest.mark.parametrize("boot", ["none", "full"])
-@pytest.mark.parametrize("shape", [(64, 65536), (300, 16385), (256, 16383)],
+@pytest.mark.parametrize("shape", [(64, 65536), (300, 16385), (256, 16383), (1024, 1 << 16)],
                          ids=lambda s: f"{s[0]}x{s[1]}")
 def test_discounted_returns_wide_tiles(shape, boot, device):
     """Discounted returns without truncations, on calls that give every compute unit a tile of
     16384 steps, run 1024-thread tiles of four segments per thread (aligned rows, a ragged
-    last tile, element-aligned rows): float32 against the oracle, and bfloat16 bit-identical
-    to the float32 kernels' result rounded."""
+    last tile, element-aligned rows, and 4096 tiles, far more than the GPU holds at once):
+    float32 against the oracle, and bfloat16 bit-identical to the float32 kernels' result
+    rounded."""
     import torch
     from rl_triton import _native
     inp, params = make_inputs("discounted_returns", *shape, seed=88, boot=boot)
