@@ -94,26 +94,42 @@ int64_t chain_grid(int64_t E, int64_t T, int NT, int Q) {
 // up; rows of 1-3 steps take one step per thread, element by element.
 int rows_seg(int64_t T) { return T < 4 ? 1 : 4; }
 
-// Discounted returns without truncations (512-thread tiles of up to 8 segments per thread):
-// a call that gives every CU a tile of 16384 steps runs them as 1024 threads x 4 segments
-// instead of 512 x 8, the same tiles.  On MI355X: [64,65536] 11.58 -> 10.37 us; four
-// segments per thread were the fastest shape wherever they gave every CU a tile (C5
-// [16,131072] keeps 512 x 4, 8.12 us, against 8.41 at 1024 x 2).
+// Discounted returns without truncations (512-thread tiles of up to 8 segments per thread)
+// take 1024-thread tiles on two kinds of calls, where measured faster on MI355X (A/B twice,
+// same box, both storage types; four segments per thread were the fastest shape wherever
+// they gave every CU a tile):
+//   * a call that gives every CU a 16384-step tile runs 1024 x 4 instead of 512 x 8, the same
+//     tiles: [64,65536] 11.2 -> 10.3 us, [8,2^20] 23.1 -> 22.0 us;
+//   * a call of a few rows of at least eight 8192-step tiles, whose 8192-step tiles reach
+//     half the CUs but not all of them, runs 1024 x 2 (those tiles) instead of 512 x 2
+//     (4096-step tiles, enough for every CU): [2,10^6] 10.3 -> 8.9 us, [3,500000]
+//     8.20 -> 7.62 us, [5,300000] 7.98 -> 7.44 us, [8,200000] 9.15 -> 8.12 us; bfloat16
+//     [3,500000] 7.60 -> 7.00 us, [5,300000] 7.28 -> 6.88 us.  Shorter rows lose to the
+//     last tile's padding ([100,10000] 6.19 -> 6.44 us).
+// C5 [16,131072] keeps 512 x 4 (8.12 us, against 8.41 at 1024 x 2).
 template <class Op>
 struct wide_long_tiles : std::false_type {};
 template <class E>
 struct wide_long_tiles<ReturnsOp<false, false, E>> : std::true_type {};
-constexpr int kWideLongThreads = 1024, kWideLongSegments = 4;
-bool wide_long_call(int64_t E, int64_t T) {
-  const int64_t tile = (int64_t)kWideLongThreads * kSeg * kWideLongSegments;
-  return E * ((T + tile - 1) / tile) >= device_cus();
+struct LongShape {
+  int threads, segments;  // 0, 0: the op's own (kLongThreads, long_segments)
+};
+LongShape wide_long_shape(int64_t E, int64_t T) {
+  const int64_t cus = device_cus();
+  auto tiles = [&](int64_t tile) { return E * ((T + tile - 1) / tile); };
+  if (tiles(1024 * kSeg * 4) >= cus) return {1024, 4};
+  const int64_t t8 = tiles(1024 * kSeg * 2);
+  if (T >= 8 * 8192 && t8 < cus && 2 * t8 >= cus) return {1024, 2};
+  return {0, 0};
 }
 
 // Workgroups of the launch that launch() makes for Op at [E, T] (E, T > 0).
 template <class Op>
 int64_t launch_grid(int64_t E, int64_t T) {
-  if (T > kShortMaxT && wide_long_tiles<Op>::value && wide_long_call(E, T))
-    return chain_grid(E, T, kWideLongThreads, kWideLongSegments);
+  if (T > kShortMaxT && wide_long_tiles<Op>::value) {
+    const LongShape sh = wide_long_shape(E, T);
+    if (sh.threads) return chain_grid(E, T, sh.threads, sh.segments);
+  }
   if (T > kShortMaxT) return chain_grid(E, T, Op::kLongThreads, long_segments<Op>(E, T));
   if (rows_seg(T) == 1) return rows_grid(E, T, 1, kNT);
   return rows_grid(E, T, 4, rows_threads(E, T));
@@ -205,8 +221,11 @@ hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_
 
 template <class Op, bool VEC>
 hipError_t launch_long(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_t stream) {
-  if constexpr (wide_long_tiles<Op>::value)
-    if (wide_long_call(E, T)) return launch_chain<Op, kWideLongSegments, VEC, kWideLongThreads>(op, E, T, ws, stream);
+  if constexpr (wide_long_tiles<Op>::value) {
+    const LongShape sh = wide_long_shape(E, T);
+    if (sh.threads == 1024 && sh.segments == 4) return launch_chain<Op, 4, VEC, 1024>(op, E, T, ws, stream);
+    if (sh.threads == 1024 && sh.segments == 2) return launch_chain<Op, 2, VEC, 1024>(op, E, T, ws, stream);
+  }
   const int q = long_segments<Op>(E, T);
   if constexpr (Op::kLongMaxSegments >= 8)
     if (q == 8) return launch_chain<Op, 8, VEC>(op, E, T, ws, stream);

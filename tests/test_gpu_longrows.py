@@ -227,14 +227,16 @@ def test_lookback_fallback_paths_give_the_same_bits(op, shape, dtype, device):
 
 
 @pytest.mark.parametrize("boot", ["none", "full"])
-@pytest.mark.parametrize("shape", [(64, 65536), (300, 16385), (256, 16383), (1024, 1 << 16)],
+@pytest.mark.parametrize("shape", [(64, 65536), (300, 16385), (256, 16383), (1024, 1 << 16),
+                                   (3, 500000), (8, 200001)],
                          ids=lambda s: f"{s[0]}x{s[1]}")
 def test_discounted_returns_wide_tiles(shape, boot, device):
-    """Discounted returns without truncations, on calls that give every compute unit a tile of
-    16384 steps, run 1024-thread tiles of four segments per thread (aligned rows, a ragged
-    last tile, element-aligned rows, and 4096 tiles, far more than the GPU holds at once):
-    float32 against the oracle, and bfloat16 bit-identical to the float32 kernels' result
-    rounded."""
+    """Discounted returns without truncations take 1024-thread tiles on two kinds of calls:
+    four segments per thread where every compute unit gets a 16384-step tile (aligned rows,
+    a ragged last tile, element-aligned rows, and 4096 tiles, far more than the GPU holds at
+    once), two segments on a few long rows whose 8192-step tiles reach half the compute
+    units ([3,500000], [8,200001]).  float32 against the oracle, and bfloat16 bit-identical
+    to the float32 kernels' result rounded."""
     import torch
     from rl_triton import _native
     inp, params = make_inputs("discounted_returns", *shape, seed=88, boot=boot)
