@@ -94,43 +94,72 @@ int64_t chain_grid(int64_t E, int64_t T, int NT, int Q) {
 // up; rows of 1-3 steps take one step per thread, element by element.
 int rows_seg(int64_t T) { return T < 4 ? 1 : 4; }
 
-// Discounted returns without truncations (512-thread tiles of up to 8 segments per thread)
-// take 1024-thread tiles on two kinds of calls, where measured faster on MI355X (A/B twice,
-// same box, both storage types; four segments per thread were the fastest shape wherever
-// they gave every CU a tile):
-//   * a call that gives every CU a 16384-step tile runs 1024 x 4 instead of 512 x 8, the same
-//     tiles: [64,65536] 11.2 -> 10.3 us, [8,2^20] 23.1 -> 22.0 us;
-//   * a call of a few rows of at least eight 8192-step tiles, whose 8192-step tiles reach
-//     half the CUs but not all of them, runs 1024 x 2 (those tiles) instead of 512 x 2
+// Long-row tile shapes (threads x 4-step segments per thread).  Each op has its own thread
+// count and largest segment count (kLongThreads, kLongMaxSegments), and long_segments picks
+// the largest tile that still gives every CU one.  Three kinds of call change the shape,
+// where measured faster on MI355X (A/B twice, same box, both storage types alike so that a
+// bfloat16 result stays the float32 result rounded):
+//   * discounted returns without truncations (512-thread tiles of up to 8 segments), a call
+//     that gives every CU a 16384-step tile: 1024 x 4 instead of 512 x 8, the same tiles
+//     ([64,65536] 11.2 -> 10.3 us, [8,2^20] 23.1 -> 22.0 us; C5 [16,131072] keeps 512 x 4,
+//     8.12 us, against 8.41 at 1024 x 2);
+//   * discounted returns on rows of at least eight 8192-step tiles, whose 8192-step tiles
+//     reach half the CUs but not all of them: 1024 x 2 (those tiles) instead of 512 x 2
 //     (4096-step tiles, enough for every CU): [2,10^6] 10.3 -> 8.9 us, [3,500000]
-//     8.20 -> 7.62 us, [5,300000] 7.98 -> 7.44 us, [8,200000] 9.15 -> 8.12 us; bfloat16
-//     [3,500000] 7.60 -> 7.00 us, [5,300000] 7.28 -> 6.88 us.  Shorter rows lose to the
-//     last tile's padding ([100,10000] 6.19 -> 6.44 us).
-// C5 [16,131072] keeps 512 x 4 (8.12 us, against 8.41 at 1024 x 2).
+//     8.20 -> 7.62 us, [8,200000] 9.15 -> 8.12 us; bfloat16 [3,500000] 7.60 -> 7.00 us.
+//     Shorter rows lose to the last tile's padding ([100,10000] 6.19 -> 6.44 us);
+//   * 1024-thread ops whose 8192-step tiles (1024 x 2) outnumber the CUs but not twice
+//     over: a CU holds one 1024-thread workgroup of these kernels, so the tiles would run in
+//     two rounds; 512 x 4 (the same tiles) fits two workgroups per CU.  TD(lambda)
+//     [64,40000] 13.17 -> 11.89 us, [96,30000] 13.62 -> 11.92 us (bfloat16 11.53 -> 8.87),
+//     [200,10000] 12.12 -> 10.37 us; GAE [64,40000] 17.46 -> 16.16 us, [200,10000]
+//     16.16 -> 14.41 us.  V-trace is not among them: at 512 x 4 its registers still allow
+//     only one workgroup per CU.
+struct LongShape {
+  int threads, segments;
+};
 template <class Op>
 struct wide_long_tiles : std::false_type {};
 template <class E>
 struct wide_long_tiles<ReturnsOp<false, false, E>> : std::true_type {};
-struct LongShape {
-  int threads, segments;  // 0, 0: the op's own (kLongThreads, long_segments)
-};
-LongShape wide_long_shape(int64_t E, int64_t T) {
+template <class Op>
+struct half_width_tiles : std::false_type {};
+template <bool TRUNC, class E>
+struct half_width_tiles<GaeOp<TRUNC, E>> : std::true_type {};
+template <bool TRUNC, class E>
+struct half_width_tiles<GaeStatsOp<TRUNC, E>> : std::true_type {};
+template <bool NV, bool TRUNC, class E>
+struct half_width_tiles<ReturnsOp<NV, TRUNC, E>> : std::integral_constant<bool, NV || TRUNC> {};
+template <class E>
+struct half_width_tiles<DoneGatedForwardOp<E>> : std::true_type {};
+template <bool FWD, class E>
+struct half_width_tiles<AffineScanOp<FWD, E>> : std::true_type {};
+
+template <class Op>
+LongShape long_shape(int64_t E, int64_t T) {
   const int64_t cus = device_cus();
   auto tiles = [&](int64_t tile) { return E * ((T + tile - 1) / tile); };
-  if (tiles(1024 * kSeg * 4) >= cus) return {1024, 4};
-  const int64_t t8 = tiles(1024 * kSeg * 2);
-  if (T >= 8 * 8192 && t8 < cus && 2 * t8 >= cus) return {1024, 2};
-  return {0, 0};
+  if constexpr (wide_long_tiles<Op>::value) {
+    if (tiles(1024 * kSeg * 4) >= cus) return {1024, 4};
+    const int64_t t8 = tiles(1024 * kSeg * 2);
+    if (T >= 8 * 8192 && t8 < cus && 2 * t8 >= cus) return {1024, 2};
+  }
+  const int q = long_segments<Op>(E, T);
+  if constexpr (half_width_tiles<Op>::value) {
+    static_assert(Op::kLongThreads == 1024, "8192-step tiles of 1024 x 2 become 512 x 4");
+    const int64_t t8 = tiles(1024 * kSeg * 2);
+    if (q == 2 && t8 > cus && t8 <= 2 * cus) return {512, 4};
+  }
+  return {Op::kLongThreads, q};
 }
 
 // Workgroups of the launch that launch() makes for Op at [E, T] (E, T > 0).
 template <class Op>
 int64_t launch_grid(int64_t E, int64_t T) {
-  if (T > kShortMaxT && wide_long_tiles<Op>::value) {
-    const LongShape sh = wide_long_shape(E, T);
-    if (sh.threads) return chain_grid(E, T, sh.threads, sh.segments);
+  if (T > kShortMaxT) {
+    const LongShape sh = long_shape<Op>(E, T);
+    return chain_grid(E, T, sh.threads, sh.segments);
   }
-  if (T > kShortMaxT) return chain_grid(E, T, Op::kLongThreads, long_segments<Op>(E, T));
   if (rows_seg(T) == 1) return rows_grid(E, T, 1, kNT);
   return rows_grid(E, T, 4, rows_threads(E, T));
 }
@@ -221,12 +250,15 @@ hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_
 
 template <class Op, bool VEC>
 hipError_t launch_long(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_t stream) {
+  const LongShape sh = long_shape<Op>(E, T);
   if constexpr (wide_long_tiles<Op>::value) {
-    const LongShape sh = wide_long_shape(E, T);
     if (sh.threads == 1024 && sh.segments == 4) return launch_chain<Op, 4, VEC, 1024>(op, E, T, ws, stream);
     if (sh.threads == 1024 && sh.segments == 2) return launch_chain<Op, 2, VEC, 1024>(op, E, T, ws, stream);
   }
-  const int q = long_segments<Op>(E, T);
+  if constexpr (half_width_tiles<Op>::value) {
+    if (sh.threads == 512 && sh.segments == 4) return launch_chain<Op, 4, VEC, 512>(op, E, T, ws, stream);
+  }
+  const int q = sh.segments;
   if constexpr (Op::kLongMaxSegments >= 8)
     if (q == 8) return launch_chain<Op, 8, VEC>(op, E, T, ws, stream);
   if constexpr (Op::kLongMaxSegments >= 4)

@@ -226,6 +226,27 @@ def test_lookback_fallback_paths_give_the_same_bits(op, shape, dtype, device):
     assert not _native.workspace_error(device)
 
 
+@pytest.mark.parametrize("op", ["gae", "lambda_returns", "discounted_returns", "eligibility_traces",
+                                "prefix_sum", "backward_scan", "forward_scan", "vtrace"])
+@pytest.mark.parametrize("shape", [(64, 40000), (200, 10001)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_tiles_between_one_and_two_per_cu(op, shape, device):
+    """Calls whose 8192-step tiles outnumber the compute units but not twice over: the
+    1024-thread ops take 512 x 4 tiles so that two workgroups fit a CU (V-trace keeps
+    1024 x 2); aligned and element-aligned rows, with truncations where the op has them, and
+    bfloat16 bit-identical to the float32 result rounded."""
+    import torch
+    from rl_triton import _native
+    _check(op, *shape, seed=61, device=device)
+    assert not _native.workspace_error(device)
+    inp, params = _inputs(op, *shape, 61)
+    rounded = {k: (v if v is None or k == "actions" else
+                   torch.as_tensor(v).to(torch.bfloat16).float().numpy()) for k, v in inp.items()}
+    got_b = run_api(op, rounded, params, device, dtype=torch.bfloat16)
+    ref = run_api(op, rounded, params, device, dtype=torch.float32)
+    for g, r in zip(got_b, ref):
+        assert torch.equal(g.view(torch.int16), r.to(torch.bfloat16).view(torch.int16))
+
+
 @pytest.mark.parametrize("boot", ["none", "full"])
 @pytest.mark.parametrize("shape", [(64, 65536), (300, 16385), (256, 16383), (1024, 1 << 16),
                                    (3, 500000), (8, 200001)],
