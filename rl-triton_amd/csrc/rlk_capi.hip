@@ -113,8 +113,10 @@ int rows_seg(int64_t T) { return T < 4 ? 1 : 4; }
 //     two rounds; 512 x 4 (the same tiles) fits two workgroups per CU.  TD(lambda)
 //     [64,40000] 13.17 -> 11.89 us, [96,30000] 13.62 -> 11.92 us (bfloat16 11.53 -> 8.87),
 //     [200,10000] 12.12 -> 10.37 us; GAE [64,40000] 17.46 -> 16.16 us, [200,10000]
-//     16.16 -> 14.41 us.  V-trace is not among them: at 512 x 4 its registers still allow
-//     only one workgroup per CU.
+//     16.16 -> 14.41 us; prefix sum [64,40000] 11.18 -> 8.93 us.  V-trace's registers allow
+//     one 512 x 4 workgroup per CU, so it takes 512 x 2 (4096-step tiles, two workgroups
+//     per CU): [64,40000] 18.6 -> 16.4 us, [200,10000] 17.2 -> 15.4 us, bfloat16
+//     [96,30000] 15.7 -> 15.0 us, float32 [96,30000] 19.4 -> 19.7 us.
 struct LongShape {
   int threads, segments;
 };
@@ -122,18 +124,22 @@ template <class Op>
 struct wide_long_tiles : std::false_type {};
 template <class E>
 struct wide_long_tiles<ReturnsOp<false, false, E>> : std::true_type {};
+// segments per thread of the 512-thread tiles a 1024 x 2 call between one and two tiles
+// per CU takes instead (0: keeps 1024 x 2)
 template <class Op>
-struct half_width_tiles : std::false_type {};
+struct half_width_segments : std::integral_constant<int, 0> {};
 template <bool TRUNC, class E>
-struct half_width_tiles<GaeOp<TRUNC, E>> : std::true_type {};
+struct half_width_segments<GaeOp<TRUNC, E>> : std::integral_constant<int, 4> {};
 template <bool TRUNC, class E>
-struct half_width_tiles<GaeStatsOp<TRUNC, E>> : std::true_type {};
+struct half_width_segments<GaeStatsOp<TRUNC, E>> : std::integral_constant<int, 4> {};
 template <bool NV, bool TRUNC, class E>
-struct half_width_tiles<ReturnsOp<NV, TRUNC, E>> : std::integral_constant<bool, NV || TRUNC> {};
+struct half_width_segments<ReturnsOp<NV, TRUNC, E>> : std::integral_constant<int, (NV || TRUNC) ? 4 : 0> {};
 template <class E>
-struct half_width_tiles<DoneGatedForwardOp<E>> : std::true_type {};
+struct half_width_segments<DoneGatedForwardOp<E>> : std::integral_constant<int, 4> {};
 template <bool FWD, class E>
-struct half_width_tiles<AffineScanOp<FWD, E>> : std::true_type {};
+struct half_width_segments<AffineScanOp<FWD, E>> : std::integral_constant<int, 4> {};
+template <bool TRUNC, class E>
+struct half_width_segments<VtraceOp<TRUNC, E>> : std::integral_constant<int, 2> {};
 
 template <class Op>
 LongShape long_shape(int64_t E, int64_t T) {
@@ -145,10 +151,11 @@ LongShape long_shape(int64_t E, int64_t T) {
     if (T >= 8 * 8192 && t8 < cus && 2 * t8 >= cus) return {1024, 2};
   }
   const int q = long_segments<Op>(E, T);
-  if constexpr (half_width_tiles<Op>::value) {
-    static_assert(Op::kLongThreads == 1024, "8192-step tiles of 1024 x 2 become 512 x 4");
+  constexpr int hq = half_width_segments<Op>::value;
+  if constexpr (hq != 0) {
+    static_assert(Op::kLongThreads == 1024, "a 1024 x 2 call becomes 512 x hq");
     const int64_t t8 = tiles(1024 * kSeg * 2);
-    if (q == 2 && t8 > cus && t8 <= 2 * cus) return {512, 4};
+    if (q == 2 && t8 > cus && t8 <= 2 * cus) return {512, hq};
   }
   return {Op::kLongThreads, q};
 }
@@ -255,8 +262,9 @@ hipError_t launch_long(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_t
     if (sh.threads == 1024 && sh.segments == 4) return launch_chain<Op, 4, VEC, 1024>(op, E, T, ws, stream);
     if (sh.threads == 1024 && sh.segments == 2) return launch_chain<Op, 2, VEC, 1024>(op, E, T, ws, stream);
   }
-  if constexpr (half_width_tiles<Op>::value) {
-    if (sh.threads == 512 && sh.segments == 4) return launch_chain<Op, 4, VEC, 512>(op, E, T, ws, stream);
+  constexpr int hq = half_width_segments<Op>::value;
+  if constexpr (hq != 0) {
+    if (sh.threads == 512 && sh.segments == hq) return launch_chain<Op, hq, VEC, 512>(op, E, T, ws, stream);
   }
   const int q = sh.segments;
   if constexpr (Op::kLongMaxSegments >= 8)
