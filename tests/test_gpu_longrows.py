@@ -228,12 +228,15 @@ def test_lookback_fallback_paths_give_the_same_bits(op, shape, dtype, device):
 
 @pytest.mark.parametrize("op", ["gae", "lambda_returns", "discounted_returns", "eligibility_traces",
                                 "prefix_sum", "backward_scan", "forward_scan", "vtrace"])
-@pytest.mark.parametrize("shape", [(64, 40000), (200, 10001)], ids=lambda s: f"{s[0]}x{s[1]}")
+@pytest.mark.parametrize("shape", [(64, 40000), (200, 10001), (257, 8192), (256, 16384),
+                                   (171, 24576), (256, 8192)], ids=lambda s: f"{s[0]}x{s[1]}")
 def test_tiles_between_one_and_two_per_cu(op, shape, device):
     """Calls whose 8192-step tiles outnumber the compute units but not twice over: the
-    1024-thread ops take 512 x 4 tiles so that two workgroups fit a CU (V-trace keeps
-    1024 x 2); aligned and element-aligned rows, with truncations where the op has them, and
-    bfloat16 bit-identical to the float32 result rounded."""
+    1024-thread ops take 512 x 4 tiles so that two workgroups fit a CU (V-trace 512 x 2);
+    aligned and element-aligned rows, with truncations where the op has them, and bfloat16
+    bit-identical to the float32 result rounded.  On a 256-CU MI355X, 257 and 512 tiles
+    ([257,8192], [256,16384]) are the rule's edges and 513 and 256 ([171,24576],
+    [256,8192]) fall just outside it."""
     import torch
     from rl_triton import _native
     _check(op, *shape, seed=61, device=device)
