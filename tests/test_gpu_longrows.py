@@ -373,3 +373,40 @@ def test_non_finite_input_after_a_reset(op, shape, device):
         assert np.array_equal(fin_g, fin_e)
     else:
         assert np.any(other), "the long row was expected to stop the nan at a tile boundary"
+
+
+def _shape_sweep(n=40, seed=4242):
+    """Seeded (op, E, T) cases spread over the long-row tile-shape rules: from one 8192-step
+    tile per call to about three per compute unit of a 256-CU GPU, one to forty tiles per
+    row with a ragged last tile, aligned rows and element-aligned ones."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        op = OPS[i % len(OPS)]
+        per_row = int(rng.choice([1, 2, 3, 5, 8, 16, 40]))
+        tiles = int(rng.integers(1, 800))
+        T = max(2052, per_row * 8192 - int(rng.integers(0, 8192)))
+        if rng.random() < 0.6:
+            T -= T % 4
+        E = max(1, min(tiles // per_row, 4_000_000 // T))
+        cases.append((op, E, T))
+    return cases
+
+
+@pytest.mark.parametrize("op,E,T", _shape_sweep(), ids=lambda v: str(v))
+def test_long_row_shape_sweep(op, E, T, device):
+    """Every tile shape the launcher picks for long rows (the op's own, the wide and few-row
+    discounted-returns shapes, the half-width shapes at one to two tiles per CU) against the
+    oracle, and bfloat16 bit-identical to the float32 result rounded."""
+    import torch
+    from rl_triton import _native
+    print(f"[sweep] {op} [{E},{T}]", flush=True)
+    _check(op, E, T, seed=E * 7 + T, device=device)
+    assert not _native.workspace_error(device)
+    inp, params = _inputs(op, E, T, E * 7 + T)
+    rounded = {k: (v if v is None or k == "actions" else
+                   torch.as_tensor(v).to(torch.bfloat16).float().numpy()) for k, v in inp.items()}
+    got_b = run_api(op, rounded, params, device, dtype=torch.bfloat16)
+    ref = run_api(op, rounded, params, device, dtype=torch.float32)
+    for g, r in zip(got_b, ref):
+        assert torch.equal(g.view(torch.int16), r.to(torch.bfloat16).view(torch.int16))
