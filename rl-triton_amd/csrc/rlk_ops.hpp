@@ -77,7 +77,10 @@ struct GaeOp {
       // VEC: T % 4 == 0 and t0 % 4 == 0, so a segment is all in or all padding, and only
       // its last step can be T - 1 (one comparison per segment instead of one per step)
       const bool at_end = VEC ? (i == S - 1 && t0 + S == T) : (t == T - 1);
-      const float vn = (at_end || R.tr[i] == 1.f) ? R.bt[i] : raw;
+      // `|`, not `||`: the short circuit compiled to a divergent branch on the path after
+      // the loads (C2 [4096,128] 3.82 -> 3.80 us, bfloat16 3.28 -> 3.18 us on MI355X)
+      const bool use_boot = at_end | (R.tr[i] == 1.f);
+      const float vn = use_boot ? R.bt[i] : raw;
       const float done = TRUNC ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
       const float a = fmaf(gamma * vn, 1.f - R.te[i], R.r[i]) - R.v[i];
       const bool in = VEC ? t0 < T : t < T;  // padding steps are the identity map
