@@ -146,6 +146,64 @@ def test_parity_random_shapes(case, device):
     _check(op, inp, params, device, rtol, atol, f"{op}[{E},{T}] boot={boot} trunc={trunc}")
 
 
+def _wide_cases(n=120, seed=77):
+    """Seeded cases over every op: rows of 1 to 300000 steps (short, multi-wave and
+    look-back paths), tensors placed 0-2 elements off alignment (the element-aligned paths),
+    done rates from 1e-4 to 0.3 for the forward scans, and each op's bootstrap and
+    truncation modes."""
+    ops = ["gae", "gae_masked", "vtrace", "retrace", "lambda_returns", "discounted_returns",
+           "eligibility_traces", "prefix_sum", "backward_scan", "forward_scan"]
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        op = ops[i % len(ops)]
+        band = int(rng.integers(0, 4))
+        T = int([rng.integers(1, 9), rng.integers(9, 129), rng.integers(129, 2049),
+                 math.exp(rng.uniform(math.log(2049), math.log(300000)))][band])
+        E = int(max(1, min(rng.integers(1, 5000), 1_500_000 // T)))
+        returns = op in ("lambda_returns", "discounted_returns")
+        boot = str(rng.choice(["none", "row", "full"])) if returns or op in ("gae", "gae_masked", "vtrace") else "row"
+        if returns and boot == "row":
+            boot = "full"
+        trunc = float(rng.choice([0.0, 0.03])) if returns or op in ("gae", "gae_masked", "vtrace") else 0.0
+        if op in ("gae", "gae_masked") and boot == "row":
+            trunc = 0.0
+        p_done = float(rng.choice([1e-4, 1e-2, 0.3]))
+        cases.append((op, E, T, boot, trunc, p_done, int(rng.choice([0, 0, 0, 1, 2])), 5000 + i))
+    return cases
+
+
+@pytest.mark.parametrize("case", _wide_cases(), ids=lambda c: f"{c[0]}-{c[1]}x{c[2]}-{c[3]}-{c[4]}-off{c[6]}")
+def test_parity_random_lengths_and_offsets(case, device):
+    """The seeded wide sweep against the float64 oracle at the suite's tolerances, with the
+    absolute tolerance of the undamped prefix sum scaled by max(1, max|expected|) at every
+    length, as discounted returns' is (its values grow with the done-free run); the float32
+    loop gate holds each result to the reference loop's own error.  Every third case also
+    runs in bfloat16, bit-identical to the float32 result rounded."""
+    from _common import suite_atol
+    from rl_triton import _native
+    op, E, T, boot, trunc, p_done, offset, seed = case
+    kw = {"p_done": p_done} if op in ("prefix_sum", "eligibility_traces") else {}
+    inp, params = make_inputs(op, E, T, seed=seed, p_trunc=trunc, boot=boot, **kw)
+    what = f"{op}[{E},{T}] boot={boot} trunc={trunc} offset={offset}"
+    got = [g.cpu().numpy() for g in run_api(op, inp, params, device, offset=offset)]
+    exp = run_oracle(op, inp, params)
+    for name, g, e in zip(OUTPUTS[op], got, exp):
+        atol = suite_atol(op, inp, e, T) if e.size else 1e-5
+        if T <= 2048 and op in ("discounted_returns", "prefix_sum") and e.size:
+            atol = 1e-5 * max(1.0, float(np.max(np.abs(e))))
+        assert_close(g, e, 1e-5, atol, f"{what}:{name}")
+    loop_gate(op, inp, params, got, exp, what)
+    assert not _native.workspace_error(device)
+    if seed % 3 == 0:
+        rounded = {k: (v if v is None or k == "actions" else
+                       torch.as_tensor(v).to(torch.bfloat16).float().numpy()) for k, v in inp.items()}
+        got_b = run_api(op, rounded, params, device, dtype=torch.bfloat16, offset=offset)
+        ref = run_api(op, rounded, params, device, dtype=torch.float32, offset=offset)
+        for g, r in zip(got_b, ref):
+            assert torch.equal(g.view(torch.int16), r.to(torch.bfloat16).view(torch.int16)), what
+
+
 @pytest.mark.parametrize("op", ["gae", "vtrace", "lambda_returns", "discounted_returns"])
 @pytest.mark.parametrize("boot", ["none", "row", "full"])
 @pytest.mark.parametrize("trunc", [0.0, 0.05])
