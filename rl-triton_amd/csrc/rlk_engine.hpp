@@ -1174,6 +1174,7 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
   using State = typename Map::State;
   constexpr bool HAS_HALO = !std::is_same<Halo, NoHalo>::value;
   __shared__ Map s_map[NW];
+  __shared__ Map s_pref[NW];  // s_map[v] o ... o s_map[0]: the tile's maps up to each wave
   __shared__ State s_carry;
   __shared__ int s_next;
   __shared__ uint32_t s_epoch;
@@ -1280,8 +1281,14 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
       __syncthreads();
       const uint32_t epoch = s_epoch;
       if (wave == 0) {
-        Map tm = Map::identity();
-        for (int v = 0; v < NW; ++v) tm = compose(s_map[v], tm);
+        // The wave maps' inclusive prefixes by one lane scan (lane v: waves 0..v), kept in
+        // LDS, so that a wave's entering state is one application once the tile's carry is
+        // known instead of a chain through the waves before it (prefix sum [8,2^20]
+        // 19.18 -> 18.96 us, discounted returns [3,500000] 7.65 -> 7.40 us on MI355X).
+        Map pm = lane < NW ? s_map[lane < NW ? lane : 0] : Map::identity();
+        pm = lane_scan(pm, NW);
+        if (lane < NW) s_pref[lane] = pm;
+        const Map tm = lane_bcast(pm, NW - 1);
         if (k != k_own) {
           publish_for<FWD>(tm, rc, row, k, tiles_per_row, epoch, fb, lane);
           if (lane == 0) s_next = k_own;
@@ -1304,7 +1311,7 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
       }
       // state entering this wave's chunk, then each segment row, then each lane
       State carry = s_carry;
-      for (int v = 0; v < wave; ++v) carry = s_map[v].apply(carry);
+      if (wave > 0) carry = s_pref[wave > 0 ? wave - 1 : 0].apply(carry);
 #pragma unroll
       for (int r = 0; r < Q; ++r) {
         State x_in = lane_prev(m[r].apply(carry));
