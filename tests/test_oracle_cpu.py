@@ -717,3 +717,81 @@ def test_float32_loops_c_equals_torch(op, kw):
     if op == "prefix_sum":
         p2 = {"boundary": "starts_at"}
         assert np.array_equal(orc.loop32(op, inp, p2)[0], _torch_loop(op, inp, p2)[0].numpy())
+
+
+# ---------------------------------------------------------------------------------------
+# the float32 loops themselves, pinned: against the reference's known answers (every golden
+# case whose call the reference's float32 loop takes) and against the float64 oracle on a
+# seeded medium shape.  A mistake shared by the C and torch restatements (which the test
+# above cannot see) fails here, so a gate of "no further from float64 than the float32
+# loop" cannot pass for want of a correct loop.
+# ---------------------------------------------------------------------------------------
+def _loop32_takes(case):
+    """The reference's float32 V-trace loop takes last_value only (no truncations and no
+    per-step bootstrap values); every other golden case has a float32 loop."""
+    inp = case["inputs"]
+    if case["op"] == "vtrace":
+        return inp.get("truncateds") is None and inp.get("bootstrap_values") is None
+    return True
+
+
+def _golden_arrays(case):
+    inp = {}
+    for k, v in case["inputs"].items():
+        if v is None:
+            inp[k] = None
+        elif k == "actions":
+            inp[k] = np.asarray(v, dtype=np.int64)
+        else:
+            inp[k] = np.asarray(v, dtype=np.float32)
+    return inp
+
+
+LOOP_GOLDEN = [c for c in golden_cases() if _loop32_takes(c)]
+
+
+def test_float32_loops_cover_every_op():
+    ops = {c["op"] for c in LOOP_GOLDEN}
+    assert ops == {"gae", "vtrace", "retrace", "lambda_returns", "discounted_returns",
+                   "eligibility_traces", "prefix_sum"}, ops
+
+
+@pytest.mark.parametrize("case", LOOP_GOLDEN, ids=lambda c: c["name"])
+def test_float32_loops_known_answers(case):
+    """Both float32 restatements of the reference's loops give the reference's own known
+    answers (float32 arithmetic: rtol = atol = 1e-5)."""
+    inp = _golden_arrays(case)
+    params = dict(case["params"])
+    c_out = orc.loop32(case["op"], inp, params)
+    t_out = _torch_loop(case["op"], inp, params)
+    for name, c, t in zip(OUTPUTS[case["op"]], c_out, t_out):
+        if name not in case["expected"]:
+            continue
+        want = np.asarray(case["expected"][name], dtype=np.float64)
+        assert_close(c, want, 1e-5, 1e-5, f"{case['name']}:{name} (C float32 loop)")
+        assert_close(t.numpy(), want, 1e-5, 1e-5, f"{case['name']}:{name} (torch float32 loop)")
+
+
+LOOP_F64_CASES = LOOP_CASES + [
+    ("retrace", dict(n_act=4, p_term=0.02)), ("eligibility_traces", dict()),
+    ("prefix_sum", dict(p_done=0.01)),
+]
+
+
+@pytest.mark.parametrize("op,kw", LOOP_F64_CASES, ids=lambda v: v if isinstance(v, str) else
+                         "-".join(f"{k}{w}" for k, w in v.items()))
+def test_float32_loops_near_float64(op, kw):
+    """Each float32 loop against the float64 oracle on a seeded [32, 512] case, at float32
+    tolerance: 1e-5 of the output scale (the magnitude of a discounted sum grows with the
+    horizon; a prefix sum's with the episode length)."""
+    inp, params = make_inputs(op, 32, 512, seed=61, **kw)
+    if op == "vtrace":
+        params = dict(params, rho_bar=0.8, c_bar=0.9)
+    if op == "retrace":
+        params = dict(params, c_bar=0.9, rho_bar=0.8)
+    want = run_oracle(op, inp, params)
+    got = orc.loop32(op, inp, params)
+    for name, g, w in zip(OUTPUTS[op], got, want):
+        scale = max(1.0, float(np.max(np.abs(w))))
+        err = float(np.max(np.abs(g.astype(np.float64) - w)))
+        assert err <= 1e-5 * scale, f"{op}:{name}: max abs err {err} (scale {scale})"
