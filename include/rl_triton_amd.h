@@ -118,7 +118,10 @@ int rlk_gae(const float *rewards, const float *values, const float *terminateds,
  * that needs the buffer also enqueues a small kernel on `stream` that clears it, as does
  * every RLK_WORKSPACE_MAX_CALLS-th such call after that, and every such call made while
  * `stream` captures a graph (so each replay starts from a clear buffer).  No memset and
- * no allocating routine is called. */
+ * no allocating routine is called.  The look-back error flag (word 3 of a workspace, see
+ * Workspace above) lives in that buffer too, where the caller cannot read it: NaN in the
+ * outputs is this entry's only sign of a wait that gave up, and overlapping calls are not
+ * detected. */
 #define RLK_NOALLOC_SCRATCH_BYTES (1 << 20)
 int rlk_gae_noalloc(const float *rewards, const float *values, const float *terminateds,
                     const float *truncateds, const float *bootstrap, int boot_mode,
