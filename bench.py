@@ -18,6 +18,9 @@ Printed JSON (one line, stdout):
                  runs back to back (queued behind a GPU spin), vs 8 TB/s; traffic = HBM
                  bytes per launch measured by rocprofv3 counters
                  (profiles/traffic_baseline_configs.json)
+  host_issue     the host clock around each public call of the timed loop: host time per
+                 step and per call (first steps apart); a step cannot end on the GPU before
+                 the host has issued it
   graph_replay   the same steps replayed from a captured HIP graph (no host work per call)
   ops            per-op device time, Gelem/s, GB/s and %-of-peak for both kernels
   stream_ceiling the same byte pattern streamed with no scan (librlk_stream_ceiling.so:
@@ -532,6 +535,27 @@ def time_graph_steps(torch, rl, sets, steps):
     return a.elapsed_time(b) / (reps * n)
 
 
+def time_eager_ops(torch, rl, sets, calls=2000):
+    """Each headline op alone, issued eagerly back to back through the public API (the
+    reference's "full-call" figure, benchmarks.md:328): HIP events around `calls` calls on
+    rotating input sets, per call, host time included."""
+    res = {}
+    for name, fn, idx in (("gae", run_gae, 0), ("vtrace", run_vtrace, 1)):
+        for i in range(50):
+            fn(rl, sets[i % len(sets)][idx])
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(calls):
+            fn(rl, sets[i % len(sets)][idx])
+        b.record()
+        torch.cuda.synchronize()
+        res[name] = round(1e3 * a.elapsed_time(b) / calls, 3)
+    log(f"[bench] eager calls back to back (host-inclusive): GAE {res['gae']:.2f} us/call, "
+        f"V-trace {res['vtrace']:.2f} us/call")
+    return res
+
+
 def time_launch_paths(torch, calls=2000):
     """The launch-bound path (the reference's ROADMAP.md:125-130 graph item): C1 [64, 512]
     GAE calls issued eagerly back to back (host-inclusive time per call) against the same
@@ -697,6 +721,31 @@ def cpu_baseline(torch, cpu_sets, budget_s):
                 "reference_published_ms": {"RTX 2000 Ada box host": 14.205, "H100 box host": 16.514}}}
 
 
+def host_issue(stamps, steps, ms_step):
+    """Host-side view of the timed loop: `stamps` holds the host clock before each public
+    call (GAE, then V-trace, per step) and after the last one.  The GPU cannot finish a step
+    before the host has issued it, so when the host needs longer per step than the kernels
+    (issue_us_per_step against the GPU clock's us_per_step) the loop runs at the host's
+    pace."""
+    calls = [1e6 * (b - a) for a, b in zip(stamps, stamps[1:])]
+    gae, vt = calls[0::2], calls[1::2]
+
+    def dist(v):
+        v = sorted(v)
+        q = lambda f: round(v[min(len(v) - 1, int(f * (len(v) - 1) + 0.5))], 2)  # noqa: E731
+        return {"median": q(0.5), "p10": q(0.1), "p90": q(0.9), "max": round(v[-1], 2)}
+
+    later = calls[6:] or calls
+    return {"issue_us_per_step": round(1e6 * (stamps[-1] - stamps[0]) / steps, 3),
+            "gpu_us_per_step": round(1e3 * ms_step, 3),
+            "gae_call_us": dist(gae), "vtrace_call_us": dist(vt),
+            "first_steps_call_us": [round(c, 2) for c in calls[:6]],
+            "later_steps_call_us_median": dist(later)["median"],
+            "note": "host clock around each public call in the timed loop (two perf_counter "
+                    "reads per step, ~0.1 us); a step cannot end on the GPU before the host "
+                    "has issued it"}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -749,19 +798,29 @@ def main(argv=None):
     torch.cuda.synchronize()
 
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    pc = time.perf_counter
+    stamps = [0.0] * (2 * a.steps + 1)  # host clock before each call, and after the last
     torch.cuda.synchronize()
     start.record()
-    t0 = time.perf_counter()
+    t0 = pc()
     for i in range(a.steps):  # from the set after the warm-up's last: the least recently used
         s = sets[(a.warmup + i) % n_sets]
+        stamps[2 * i] = pc()
         run_gae(rl_triton, s[0])
+        stamps[2 * i + 1] = pc()
         run_vtrace(rl_triton, s[1])
+    stamps[-1] = pc()
     end.record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    wall = pc() - t0
     ms_step = start.elapsed_time(end) / a.steps
     value = 2 * E * T / (ms_step * 1e-3) / 1e9
-    log(f"[bench] timed {a.steps} steps: {ms_step * 1e3:.2f} us/step (wall {wall:.3f} s)")
+    host = host_issue(stamps, a.steps, ms_step)
+    log(f"[bench] timed {a.steps} steps: {ms_step * 1e3:.2f} us/step on the GPU clock, "
+        f"host issue {host['issue_us_per_step']:.2f} us/step, wall {wall * 1e6:.1f} us")
+    log(f"[bench] host time per call (us): GAE median {host['gae_call_us']['median']}, "
+        f"V-trace median {host['vtrace_call_us']['median']}; first three steps "
+        f"{host['first_steps_call_us']}; later steps median {host['later_steps_call_us_median']}")
 
     op_ms = time_ops(torch, rl_triton, sets, max(200, min(a.steps, 2000)))
     ops = {}
@@ -775,7 +834,10 @@ def main(argv=None):
     dom = max(ops, key=lambda k: ops[k]["device_us"])
     roofline = {"bound": "hbm", "kernel": dom, "achieved": ops[dom]["gb_s"], "peak": PEAK_GBS,
                 "unit": "GB/s", "frac": round(ops[dom]["gb_s"] / PEAK_GBS, 4),
-                "traffic": measured_traffic({"gae": "C2_gae_4096x128", "vtrace": "C3_vtrace_4096x128"}[dom])}
+                "traffic": measured_traffic({"gae": "C2_gae_4096x128", "vtrace": "C3_vtrace_4096x128"}[dom]),
+                "bytes_per_launch": ops[dom]["bytes_per_launch"], "duration_us": ops[dom]["device_us"],
+                "duration_source": "HIP events on the launch stream around batches of 100 launches "
+                                   "queued back to back behind a GPU spin, no profiler attached"}
 
     ceiling = time_stream_ceiling(torch, sets)
     for name in ("gae", "vtrace"):
@@ -786,6 +848,9 @@ def main(argv=None):
     log(f"[bench] graph-replayed step: {graph_ms * 1e3:.2f} us "
         f"({2 * E * T / (graph_ms * 1e-3) / 1e9:.1f} Gelem/s)")
     launch_paths = time_launch_paths(torch)
+    eager_ops = time_eager_ops(torch, rl_triton, sets)
+    launch_paths["C2_gae_4096x128"] = {"eager_us_per_call": eager_ops["gae"]}
+    launch_paths["C3_vtrace_4096x128"] = {"eager_us_per_call": eager_ops["vtrace"]}
     del sets
     torch.cuda.empty_cache()
 
@@ -839,13 +904,18 @@ def main(argv=None):
                                "last_value, one public-API call each per step, inputs rotated over "
                                f"{n_sets} HBM-resident sets",
                    "num_envs": E, "seq_len": T, "gamma": 0.99, "lambda": 0.95,
-                   "rho_bar": 1.0, "c_bar": 1.0, "timing": "value: eager public-API calls, HIP events around the timed region"},
+                   "rho_bar": 1.0, "c_bar": 1.0,
+                   "timing": "value: eager public-API calls, HIP events around the timed region; "
+                             "the timed steps start at the input set after the warm-up's last "
+                             "(the least recently used), so no timed call reads inputs the "
+                             "warm-up left in the 256 MB MALL; host_issue holds the host clock's "
+                             "view of the same loop"},
         "roofline": roofline, "ops": ops, "stream_ceiling": ceiling,
         "independent_ceilings": independent, "configs": configs, "configs_bf16_io": configs_bf16,
         "extensions": extensions, "element_aligned_rows": element_aligned,
         "graph_replay": {"ms_per_step": round(graph_ms, 6),
                          "gelem_s": round(2 * E * T / (graph_ms * 1e-3) / 1e9, 3)},
-        "launch_paths": launch_paths,
+        "launch_paths": launch_paths, "host_issue": host,
         "parity_max_abs_err": errs, "parity_vs_reference_loops_max_abs_err": errs_loops,
         "cpu_baseline": cpu,
     }

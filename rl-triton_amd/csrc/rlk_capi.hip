@@ -240,6 +240,21 @@ std::atomic<int> g_fallback_polls{kFallbackPolls};
 
 // Long rows: one tile of kLongThreads * 4 * Q steps per workgroup, grid = nslots * (tiles
 // of the fullest slot) (see chain_kernel in rlk_engine.hpp).
+//
+// Placement of the tiles in the block index.  By default the slots interleave (block b
+// holds a tile of slot b % nslots), so position j of every row is dispatched before
+// position j + 1 of any, and with 8 XCDs taking blocks round-robin a row's tiles share one
+// XCD.  A call of at most 16 rows whose tiles fill every CU at least once takes the rows
+// one after another instead (a row's tiles consecutive, spread over the XCDs).  Measured on
+// MI355X, A/B twice in one process, bit-identical results: V-trace [16,131072]
+// 13.39 -> 12.50 us, GAE [16,131072] 12.78 -> 11.69, TD(lambda) [16,131072] 9.65 -> 8.86,
+// discounted returns [8,262144] 9.18 -> 8.46 and [16,131072] 8.28 -> 8.22, prefix sum
+// [16,131072] 8.32 -> 7.80; [8,2^20], [4,2^19..2^21] unchanged.  Where the grid is smaller
+// than the chip ([16,65536], [12,131072], [16,40000]) or the rows are many ([32..200] rows)
+// the row-major order lost up to 1.35 us (TD(lambda) [96,30000]), so those keep the
+// interleave.
+inline int chain_row_major(int64_t E, int64_t grid) { return E <= 16 && grid >= device_cus() ? 1 : 0; }
+
 template <class Op, int Q, bool VEC, int NT = Op::kLongThreads>
 hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_t stream) {
   static_assert(NT * kSeg * Q >= kMinTile, "the workspace is sized for the smallest tile");
@@ -250,7 +265,9 @@ hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_
   uint64_t* fb = ws + kStatusOffset + kStatusWords * status_tiles(E, T);
   int spin_limit = g_spin_limit.load(std::memory_order_relaxed);
   int fallback_polls = g_fallback_polls.load(std::memory_order_relaxed);
-  void* args[] = {const_cast<Op*>(&op), &E, &T, &tpr, &ws, &fb, &spin_limit, &fallback_polls};
+  int row_major = chain_row_major(E, grid);
+  void* args[] = {const_cast<Op*>(&op), &E, &T, &tpr, &ws, &fb, &spin_limit, &fallback_polls,
+                  &row_major};
   return hipLaunchKernel(reinterpret_cast<const void*>(&chain_kernel<Op, NT, Q, VEC>),
                          dim3((unsigned)grid), dim3(NT), args, 0, stream);
 }

@@ -1163,7 +1163,8 @@ __global__ __launch_bounds__(NT) void rows_strided_kernel(const Op op, int64_t E
 template <class Op, int NT, int Q, bool VEC>
 __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T, int tiles_per_row,
                                                    uint64_t* __restrict__ ws, uint64_t* __restrict__ fb,
-                                                   int spin_limit, int fallback_polls) {
+                                                   int spin_limit, int fallback_polls,
+                                                   int row_major) {
   constexpr bool FWD = Op::kForward;
   constexpr int NW = NT / kWave;
   constexpr int WSTEPS = Q * kWave * kSeg;  // steps per wave chunk
@@ -1183,26 +1184,37 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
   const int lane = __lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int nslots = lookback_slots(E);
-  const int slot = (int)(blockIdx.x % (unsigned)nslots);
   const uint64_t wgs_per_slot = gridDim.x / (unsigned)nslots;
+  // Placement of the slots' tiles in the block index (see launch_chain): slot-interleaved,
+  // block b -> slot b % nslots, or row-major, the blocks of a slot consecutive.
+  const int slot = row_major ? (int)(blockIdx.x / (unsigned)wgs_per_slot)
+                             : (int)(blockIdx.x % (unsigned)nslots);
   uint64_t* sc = ws + kHeaderWords + kSlotWords * slot;
   const int64_t rows_in_slot = (E - slot + nslots - 1) / nslots;
   const uint64_t tiles_in_slot = (uint64_t)rows_in_slot * (uint64_t)tiles_per_row;
   // The workgroup's tile, from its block index: slot, then position in the slot's scan
   // order (lower block indices first, so a tile's predecessors are normally dispatched
   // before it; the look-back does not rely on that).
-  const uint64_t q_t = blockIdx.x / (unsigned)nslots;
+  const uint64_t q_t = row_major ? blockIdx.x % (unsigned)wgs_per_slot : blockIdx.x / (unsigned)nslots;
 
   // The slot's epoch is read first and used once the tile's loads are in flight.  Every
-  // workgroup counts itself in the slot's counter once it has the epoch (the count is issued
-  // after the epoch load has returned).  The one that completes the count has then seen
-  // every workgroup of the slot read the epoch: once its tile's look-back is done (the
-  // count's result is back long before) it resets the count and advances the slot's epoch
-  // for the next call.
+  // workgroup counts itself in the slot's counter once it has the epoch.  The one that
+  // completes the count has then seen every workgroup of the slot read the epoch: once its
+  // tile's look-back is done (the count's result is back long before) it resets the count
+  // and advances the slot's epoch for the next call.
+  //
+  // "Once it has the epoch" is a data dependency, not an assumption about the schedule: the
+  // count's increment is computed from the loaded epoch word (1 + its upper half, which is
+  // always 0: the word holds an epoch below 2^30), so the atomic cannot issue before the
+  // load has returned its value.  Without it the two relaxed accesses to different
+  // addresses could be performed in either order, and a workgroup whose count came first
+  // could read the epoch its slot's last workgroup had already advanced, then tag its
+  // status words with the next call's epoch (a silently wrong carry in that call).
   uint64_t e_raw = 0, drawn = 0;
   if (tid == 0) e_raw = atomic_ld(sc + 24);
   auto count_drawn = [&]() {
-    drawn = __hip_atomic_fetch_add(sc + 16, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t one = 1 + (e_raw >> 32);
+    drawn = __hip_atomic_fetch_add(sc + 16, one, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (drawn >= wgs_per_slot) atomic_st(ws + 3, (uint64_t)1);  // counters were not at rest
   };
   // It advances the epoch of every slot this call leaves unused whose index falls on its
@@ -1244,7 +1256,7 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
       }
       const bool first = FWD ? (k == 0) : (k == tiles_per_row - 1);
       const State rc = (first && wave == 0) ? row_carry(op, row, T) : State{};
-      if (it == 0 && tid == 0) {  // the epoch load was issued first: it is back by now
+      if (it == 0 && tid == 0) {  // the epoch load was issued before the tile's loads
         s_epoch = (uint32_t)e_raw & kEpochMask;
         count_drawn();
       }
