@@ -256,15 +256,20 @@ __device__ __forceinline__ void load_seg(const E* __restrict__ p, int t0, int T,
   } else if constexpr (S % 4 == 0) {
     // element-aligned quads; the launch guarantees T >= 4.  No branch around the load: a
     // join after it would make the compiler wait for the load there, and the loads of a
-    // segment's arrays would no longer overlap.
+    // segment's arrays would no longer overlap.  Segments start at multiples of four, so
+    // the one partial quad of a row (T % 4 != 0) starts at 4 * (T / 4); it is read as the
+    // row's last four elements, and its steps sit c = 4 - T % 4 places further in: one
+    // shift for the whole row.  Padding quads beyond it read the same four elements (their
+    // values never matter).  Per quad only a lane mask (inside the row or not) stays live
+    // until the load returns, not a per-lane shift.
+    const int c = 4 - (T & 3);
 #pragma unroll
     for (int q = 0; q < S / 4; ++q) {
       const int t = t0 + 4 * q;
-      const int base = t + 4 <= T ? t : T - 4;  // the row's last quad for a partial or padding quad
-      const float4 f = load_quad_ua(p + base);
-      const int sh = t - base;  // 0 inside the row, 1..3 in the partial quad, >= 4 beyond it
+      const bool edge = t + 4 > T;  // the partial quad, or padding
+      const float4 f = load_quad_ua(p + (edge ? T - 4 : t));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[4 * q + i] = quad_elem(f, i + sh);
+      for (int i = 0; i < 4; ++i) v[4 * q + i] = edge ? quad_elem(f, i + c) : quad_elem(f, i);
     }
   } else {
     // segments of 1-3 steps (rows shorter than four steps)
@@ -1186,16 +1191,19 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
   const int nslots = lookback_slots(E);
   const uint64_t wgs_per_slot = gridDim.x / (unsigned)nslots;
   // Placement of the slots' tiles in the block index (see launch_chain): slot-interleaved,
-  // block b -> slot b % nslots, or row-major, the blocks of a slot consecutive.
-  const int slot = row_major ? (int)(blockIdx.x / (unsigned)wgs_per_slot)
-                             : (int)(blockIdx.x % (unsigned)nslots);
+  // block b -> slot b % nslots at position b / nslots, or row-major, the blocks of a slot
+  // consecutive (slot b / wgs_per_slot at position b % wgs_per_slot).  One division either
+  // way.
+  const unsigned pl_div = row_major ? (unsigned)wgs_per_slot : (unsigned)nslots;
+  const unsigned pl_quo = blockIdx.x / pl_div, pl_rem = blockIdx.x - pl_quo * pl_div;
+  const int slot = (int)(row_major ? pl_quo : pl_rem);
   uint64_t* sc = ws + kHeaderWords + kSlotWords * slot;
   const int64_t rows_in_slot = (E - slot + nslots - 1) / nslots;
   const uint64_t tiles_in_slot = (uint64_t)rows_in_slot * (uint64_t)tiles_per_row;
   // The workgroup's tile, from its block index: slot, then position in the slot's scan
   // order (lower block indices first, so a tile's predecessors are normally dispatched
   // before it; the look-back does not rely on that).
-  const uint64_t q_t = row_major ? blockIdx.x % (unsigned)wgs_per_slot : blockIdx.x / (unsigned)nslots;
+  const uint64_t q_t = row_major ? pl_rem : pl_quo;
 
   // The slot's epoch is read first and used once the tile's loads are in flight.  Every
   // workgroup counts itself in the slot's counter once it has the epoch.  The one that
