@@ -233,3 +233,25 @@ def test_bf16_drift_at_the_quantisation_floor(op, T, device):
               f"{err_b / floor:.2f} | {float(np.max(np.abs(e))):.3g} |")
         assert err_b <= 1.25 * floor + 1e-6, f"{op} T={T} {name}: bf16 {err_b:.2e}, floor {floor:.2e}"
         assert err_f < 1e-5
+
+
+# bfloat16 long rows at every long-row tile shape (1024 x 8, 512 x 4, 1024 x 2, the
+# few-row and many-row placements), with arrays 16-byte aligned and 8 bytes off that: the
+# float32 result rounded, bit for bit.
+LONG_BF16 = [("prefix_sum", (8, 1048576)), ("eligibility_traces", (8, 1048576)),
+          ("discounted_returns", (16, 131072)), ("vtrace", (16, 131072)), ("gae", (16, 131072)),
+          ("lambda_returns", (16, 131072)), ("gae_masked", (16, 131072)),
+          ("backward_scan", (3, 65536)), ("forward_scan", (3, 65536)), ("gae", (64, 40000)),
+          ("vtrace", (200, 10000)), ("prefix_sum", (64, 40000)), ("discounted_returns", (3, 500000))]
+
+
+@pytest.mark.parametrize("offset", [0, 4], ids=["aligned16", "aligned8"])
+@pytest.mark.parametrize("op,shape", LONG_BF16, ids=lambda v: v if isinstance(v, str) else f"{v[0]}x{v[1]}")
+def test_bf16_long_rows_are_float32_result_rounded(op, shape, offset, device):
+    inp, params = _inputs(op, shape, seed=37)
+    inp = _bf16_values(inp)
+    got = run_api(op, inp, params, device, dtype=BF16, offset=offset)
+    ref = run_api(op, inp, params, device, dtype=torch.float32)
+    for name, g, r in zip(OUTPUTS[op], got, ref):
+        same = _bits(g) == _bits(r.to(BF16))
+        assert bool(same.all()), f"{op}{shape} offset {offset}:{name}: {int((~same).sum())} elements differ"
