@@ -184,24 +184,24 @@ struct paired_rows : std::false_type {};
 template <int NA, bool TRUNC>
 struct paired_rows<RetraceOp<NA, TRUNC, float>> : std::true_type {};
 
-template <class Op, int NT, int S, bool VEC>
+template <class Op, int NT, int S, bool VEC, int SP>
 hipError_t launch_rows(const Op& op, int64_t E, int T, hipStream_t stream) {
   int log2L = ceil_log2((T + S - 1) / S);
   const int64_t grid = rows_grid(E, T, S, NT);
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   void* args[] = {const_cast<Op*>(&op), &E, &T, &log2L};
   // 4-step rows of 33..2048 steps: the instance whose scan width is fixed
-  const void* k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC>);
+  const void* k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC, 0, SP>);
   if constexpr (S == 4 && VEC && NT == kNTWide && paired_rows<Op>::value) {
     if (log2L == 5) {
-      k = reinterpret_cast<const void*>(&rows_pair_kernel<Op, NT / 2, 32>);
+      k = reinterpret_cast<const void*>(&rows_pair_kernel<Op, NT / 2, 32, SP>);
       return hipLaunchKernel(k, dim3((unsigned)grid), dim3(NT / 2), args, 0, stream);
     }
   }
   if constexpr (S == 4) {
-    if (log2L == 4) k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC, 16>);
-    else if (log2L == 5) k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC, 32>);
-    else if (log2L >= 6) k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC, kWave>);
+    if (log2L == 4) k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC, 16, SP>);
+    else if (log2L == 5) k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC, 32, SP>);
+    else if (log2L >= 6) k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC, kWave, SP>);
   }
   return hipLaunchKernel(k, dim3((unsigned)grid), dim3(NT), args, 0, stream);
 }
@@ -222,13 +222,13 @@ struct strided_rows<VtraceOp<TRUNC, E>> : std::false_type {};
 template <int NA, bool TRUNC, class E>
 struct strided_rows<RetraceOp<NA, TRUNC, E>> : std::false_type {};
 
-template <class Op>
+template <class Op, int SP>
 hipError_t launch_strided(const Op& op, int64_t E, int T, hipStream_t stream) {
   static_assert(kStridedThreads * kSeg * kStridedSegments == kShortMaxT, "one row per workgroup");
   if (E > 0x7fffffffLL) return hipErrorInvalidValue;
   int unused = 0;
   void* args[] = {const_cast<Op*>(&op), &E, &T, &unused};
-  return hipLaunchKernel(reinterpret_cast<const void*>(&rows_strided_kernel<Op, kStridedThreads, kStridedSegments, true>),
+  return hipLaunchKernel(reinterpret_cast<const void*>(&rows_strided_kernel<Op, kStridedThreads, kStridedSegments, true, SP>),
                          dim3((unsigned)E), dim3(kStridedThreads), args, 0, stream);
 }
 
@@ -255,7 +255,7 @@ std::atomic<int> g_fallback_polls{kFallbackPolls};
 // interleave.
 inline int chain_row_major(int64_t E, int64_t grid) { return E <= 16 && grid >= device_cus() ? 1 : 0; }
 
-template <class Op, int Q, bool VEC, int NT = Op::kLongThreads>
+template <class Op, int Q, bool VEC, int SP, int NT = Op::kLongThreads>
 hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_t stream) {
   static_assert(NT * kSeg * Q >= kMinTile, "the workspace is sized for the smallest tile");
   constexpr int64_t tile = (int64_t)NT * kSeg * Q;
@@ -268,27 +268,96 @@ hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_
   int row_major = chain_row_major(E, grid);
   void* args[] = {const_cast<Op*>(&op), &E, &T, &tpr, &ws, &fb, &spin_limit, &fallback_polls,
                   &row_major};
-  return hipLaunchKernel(reinterpret_cast<const void*>(&chain_kernel<Op, NT, Q, VEC>),
+  return hipLaunchKernel(reinterpret_cast<const void*>(&chain_kernel<Op, NT, Q, VEC, SP>),
                          dim3((unsigned)grid), dim3(NT), args, 0, stream);
 }
 
-template <class Op, bool VEC>
+template <class Op, bool VEC, int SP>
 hipError_t launch_long(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_t stream) {
   const LongShape sh = long_shape<Op>(E, T);
   if constexpr (wide_long_tiles<Op>::value) {
-    if (sh.threads == 1024 && sh.segments == 4) return launch_chain<Op, 4, VEC, 1024>(op, E, T, ws, stream);
-    if (sh.threads == 1024 && sh.segments == 2) return launch_chain<Op, 2, VEC, 1024>(op, E, T, ws, stream);
+    if (sh.threads == 1024 && sh.segments == 4) return launch_chain<Op, 4, VEC, SP, 1024>(op, E, T, ws, stream);
+    if (sh.threads == 1024 && sh.segments == 2) return launch_chain<Op, 2, VEC, SP, 1024>(op, E, T, ws, stream);
   }
   constexpr int hq = half_width_segments<Op>::value;
   if constexpr (hq != 0) {
-    if (sh.threads == 512 && sh.segments == hq) return launch_chain<Op, hq, VEC, 512>(op, E, T, ws, stream);
+    if (sh.threads == 512 && sh.segments == hq) return launch_chain<Op, hq, VEC, SP, 512>(op, E, T, ws, stream);
   }
   const int q = sh.segments;
   if constexpr (Op::kLongMaxSegments >= 8)
-    if (q == 8) return launch_chain<Op, 8, VEC>(op, E, T, ws, stream);
+    if (q == 8) return launch_chain<Op, 8, VEC, SP>(op, E, T, ws, stream);
   if constexpr (Op::kLongMaxSegments >= 4)
-    if (q == 4) return launch_chain<Op, 4, VEC>(op, E, T, ws, stream);
-  return launch_chain<Op, 2, VEC>(op, E, T, ws, stream);
+    if (q == 4) return launch_chain<Op, 4, VEC, SP>(op, E, T, ws, stream);
+  return launch_chain<Op, 2, VEC, SP>(op, E, T, ws, stream);
+}
+
+// Output stores: non-temporal (the default) or write-through (sc1, store_quad_wt), per
+// launch, by what measured faster on MI355X (one process, three builds -- nt, sc1 and
+// plain stores -- alternated, 88 op x shape x storage cases; µs, nt -> sc1):
+//   * bfloat16 outputs: sc1 everywhere, 1-4% faster in every case but one (Retrace
+//     [4096,128], equal): V-trace [4096,128] 3.49 -> 3.34, prefix sum [16,131072]
+//     6.77 -> 6.54, TD(lambda) [16,131072] 7.07 -> 6.83;
+//   * float32 short rows that span several waves (more than 256 steps) in launches writing
+//     at least 1 MB, or launches writing at least 12 MB: sc1, 2-4% (TD(lambda) [256,2048]
+//     3.35 -> 3.25, Retrace [256,2048] 6.71 -> 6.49, V-trace [1024,512] 4.38 -> 4.21,
+//     V-trace [16384,128] 11.19 -> 10.75); rows of up to 256 steps in smaller launches keep
+//     nt (GAE [4096,128] 3.77 against 3.94, V-trace 3.99 against 4.20, GAE [2048,256] 3.83
+//     against 3.98), as does GAE [64,512] (128 KB written, 2.25 against 2.27);
+//   * float32 long rows: sc1 when the grid is at most one tile per CU, for every op but
+//     V-trace and Retrace (discounted returns [16,131072] 8.00 -> 7.86, prefix sum
+//     [16,131072] 7.66 -> 7.49, TD(lambda) [8,262144] 8.92 -> 8.79); nt with more tiles
+//     (discounted [64,40000] 8.99 against 9.58) and for V-trace ([16,131072] 12.40 against
+//     12.70, [256,8192] 11.46 against 12.15).
+// Plain stores were never the fastest by more than 3% and lost up to 13% elsewhere.  The
+// policy is a kernel template argument (SP), so a non-temporal instance is the same code
+// as before write-through stores existed.
+template <class Op>
+struct n_outputs : std::integral_constant<int, 1> {};
+template <bool TRUNC, class E>
+struct n_outputs<VtraceOp<TRUNC, E>> : std::integral_constant<int, 2> {};
+template <int NA, bool TRUNC, class E>
+struct n_outputs<RetraceOp<NA, TRUNC, E>> : std::integral_constant<int, 2> {};
+template <bool TRUNC, class E>
+struct n_outputs<GaeStatsOp<TRUNC, E>> : std::integral_constant<int, 2> {};
+template <bool TRUNC, class E>
+struct n_outputs<MaskedGaeStatsOp<TRUNC, E>> : std::integral_constant<int, 2> {};
+template <class Op>
+struct long_rows_write_through : std::true_type {};
+template <bool TRUNC, class E>
+struct long_rows_write_through<VtraceOp<TRUNC, E>> : std::false_type {};
+template <int NA, bool TRUNC, class E>
+struct long_rows_write_through<RetraceOp<NA, TRUNC, E>> : std::false_type {};
+
+enum class Kernel { kRows, kStrided, kChain };
+// The policies a kernel can be launched with for an op: bfloat16 outputs and the strided
+// rows kernel always write through, float32 V-trace and Retrace long rows never; only the
+// policies listed here are instantiated.
+template <class Op, Kernel K>
+struct store_policies {
+  static constexpr bool kBf16 = std::is_same<typename Op::Elem, bf16>::value;
+  static constexpr bool kWriteThrough = kBf16 || K != Kernel::kChain || long_rows_write_through<Op>::value;
+  static constexpr bool kNonTemporal = !kBf16 && K != Kernel::kStrided;
+  static_assert(kWriteThrough || kNonTemporal, "some store policy");
+};
+template <class Op, Kernel K>
+int store_write_through(int64_t E, int64_t T) {
+  using P = store_policies<Op, K>;
+  if constexpr (!P::kNonTemporal) return 1;
+  if constexpr (!P::kWriteThrough) return 0;
+  if constexpr (K == Kernel::kChain) return launch_grid<Op>(E, T) <= device_cus() ? 1 : 0;
+  const int64_t out_bytes = E * T * (int64_t)sizeof(float) * n_outputs<Op>::value;
+  return (((T + 3) / 4 > kWave && out_bytes >= (int64_t{1} << 20)) || out_bytes >= (int64_t{12} << 20)) ? 1 : 0;
+}
+// Calls f(std::integral_constant<int, SP>) with SP the launch's store policy.
+template <class Op, Kernel K, class F>
+hipError_t dispatch_store_policy(int64_t E, int64_t T, F&& f) {
+  using P = store_policies<Op, K>;
+  if constexpr (P::kWriteThrough && P::kNonTemporal) {
+    if (store_write_through<Op, K>(E, T)) return f(std::integral_constant<int, 1>{});
+    return f(std::integral_constant<int, 0>{});
+  } else {
+    return f(std::integral_constant<int, P::kWriteThrough ? 1 : 0>{});
+  }
 }
 
 template <class Op>
@@ -303,16 +372,23 @@ int launch(const Op& op, int64_t E, int64_t T, bool vec, void* workspace, size_t
     uint64_t* ws = reinterpret_cast<uint64_t*>(workspace);
     if (ws == nullptr || workspace_bytes_given < workspace_bytes(E, T) || !aligned16(ws))
       return RLK_ERR_WORKSPACE;
-    e = vec ? launch_long<Op, true>(op, E, Ti, ws, s) : launch_long<Op, false>(op, E, Ti, ws, s);
+    e = dispatch_store_policy<Op, Kernel::kChain>(E, T, [&](auto sp) {
+      constexpr int SP = decltype(sp)::value;
+      return vec ? launch_long<Op, true, SP>(op, E, Ti, ws, s) : launch_long<Op, false, SP>(op, E, Ti, ws, s);
+    });
   } else if (strided_rows<Op>::value && vec && T > kShortMaxT / 2) {
-    e = launch_strided(op, E, Ti, s);
-  } else if (rows_seg(T) == 1) {
-    e = launch_rows<Op, kNT, 1, false>(op, E, Ti, s);
-  } else if (rows_threads(E, T) == kNT) {
-    e = vec ? launch_rows<Op, kNT, 4, true>(op, E, Ti, s) : launch_rows<Op, kNT, 4, false>(op, E, Ti, s);
+    e = dispatch_store_policy<Op, Kernel::kStrided>(E, T, [&](auto sp) {
+      return launch_strided<Op, decltype(sp)::value>(op, E, Ti, s);
+    });
   } else {
-    e = vec ? launch_rows<Op, kNTWide, 4, true>(op, E, Ti, s)
-            : launch_rows<Op, kNTWide, 4, false>(op, E, Ti, s);
+    e = dispatch_store_policy<Op, Kernel::kRows>(E, T, [&](auto sp) {
+      constexpr int SP = decltype(sp)::value;
+      if (rows_seg(T) == 1) return launch_rows<Op, kNT, 1, false, SP>(op, E, Ti, s);
+      if (rows_threads(E, T) == kNT)
+        return vec ? launch_rows<Op, kNT, 4, true, SP>(op, E, Ti, s) : launch_rows<Op, kNT, 4, false, SP>(op, E, Ti, s);
+      return vec ? launch_rows<Op, kNTWide, 4, true, SP>(op, E, Ti, s)
+                 : launch_rows<Op, kNTWide, 4, false, SP>(op, E, Ti, s);
+    });
   }
   return e == hipSuccess ? RLK_OK : RLK_ERR_LAUNCH;
 }

@@ -185,6 +185,23 @@ __device__ __forceinline__ void store_quad(bf16* p, float4 v) {
   if constexpr (NT) __builtin_nontemporal_store(w, reinterpret_cast<nt_u2*>(p));
   else *reinterpret_cast<nt_u2*>(p) = w;
 }
+// The same stores with the sc1 cache-policy bit (write-through towards memory) instead of
+// nt.  Which of the two a launch uses is the launcher's choice, by call shape: the kernels'
+// SP template argument (0 non-temporal, 1 write-through), passed on to the op's emit, so
+// that each kernel instance holds the stores of one policy only (a runtime branch around
+// two copies of the output loop made kernels up to 3.5% slower on MI355X).
+// A VALU write to the data registers of a store of more than 8 bytes must come at least 2
+// wait states after it on gfx950, or the store may send the new values; the compiler pads
+// its own stores for this but not inline assembly, so the 16-byte form carries its own
+// s_nop 1 (2 wait states).
+__device__ __forceinline__ void store_quad_wt(float* p, float4 v) {
+  const nt_f4 w = {v.x, v.y, v.z, v.w};
+  asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" : : "v"(p), "v"(w) : "memory");
+}
+__device__ __forceinline__ void store_quad_wt(bf16* p, float4 v) {
+  const nt_u2 w = {pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+  asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(w) : "memory");
+}
 // Four consecutive elements at any element boundary: one 16-byte (bfloat16: 8-byte) access
 // that need not be aligned to its size.  gfx950 runs compute in unaligned access mode, and
 // the compiler emits a single dwordx4 (dwordx2) access for these element-aligned vector
@@ -278,15 +295,20 @@ __device__ __forceinline__ void load_seg(const E* __restrict__ p, int t0, int T,
   }
 }
 
-// Steps beyond T are not stored.
+// Steps beyond T are not stored.  wt: vector quads take store_quad_wt.
 template <int S, bool VEC, class E>
-__device__ __forceinline__ void store_seg(E* __restrict__ p, int t0, int T, const float (&v)[S]) {
+__device__ __forceinline__ void store_seg(E* __restrict__ p, int t0, int T, const float (&v)[S],
+                                          bool wt = false) {
   static_assert(!VEC || S % 4 == 0, "vector segments hold whole quads");
   if constexpr (VEC) {
 #pragma unroll
     for (int q = 0; q < S / 4; ++q) {
       const int t = t0 + 4 * q;
-      if (t < T) store_quad<S == 4>(p + t, make_float4(v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]));
+      const float4 f = make_float4(v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+      if (t < T) {
+        if (wt) store_quad_wt(p + t, f);
+        else store_quad<S == 4>(p + t, f);
+      }
     }
   } else if constexpr (S % 4 == 0) {
 #pragma unroll
@@ -656,7 +678,7 @@ __device__ __forceinline__ M lane_scan(M m, int W) {
 // [4096,128] 4.12 -> 3.99 us, GAE 3.99 -> 3.80 us, GAE [8192,64] 3.97 -> 3.78 us, TD(lambda)
 // [256,2048] 3.61 -> 3.48 us, element-aligned V-trace [4096,127] 4.80 -> 4.66 us on MI355X
 // (bit-identical results).
-template <class Op, int NT, int S, bool VEC, int WT = 0>
+template <class Op, int NT, int S, bool VEC, int WT = 0, int SP = 0>
 __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T, int log2L_arg) {
   constexpr bool FWD = Op::kForward;
   constexpr int NW = NT / kWave;
@@ -711,7 +733,7 @@ __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T,
   if ((li & (W - 1)) == 0) x_in = carry;
   State xs[S];
   replay<FWD, S>(steps, x_in, xs);
-  if (active) op.template emit<S, VEC>(R, h, xs, x_in, row, t0, T);
+  if (active) op.template emit<S, VEC, SP>(R, h, xs, x_in, row, t0, T);
   if constexpr (Op::kBlockStats) {
     Stats st;
     if (active) op.template stats<S>(R, xs, t0, T, st);
@@ -730,7 +752,7 @@ __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T,
 // them.  Orders without that read (one row scanned and stored after the other, or both
 // scanned first) interleaved the second row's loads with the first row's arithmetic, and
 // C4 Retrace [4096,128] took 6.95 us instead of 6.41.
-template <class Op, int NT, int WT>
+template <class Op, int NT, int WT, int SP = 0>
 __global__ __launch_bounds__(NT) void rows_pair_kernel(const Op op, int64_t E, int T, int) {
   constexpr bool FWD = Op::kForward;
   constexpr int S = 4, RPT = 2;
@@ -786,7 +808,7 @@ __global__ __launch_bounds__(NT) void rows_pair_kernel(const Op op, int64_t E, i
     if (li == 0) x_in = carry[u];
     State xs[S];
     replay<FWD, S>(steps[u], x_in, xs);
-    if (active[u]) op.template emit<S, true>(R[u], h[u], xs, x_in, row[u], t0, T);
+    if (active[u]) op.template emit<S, true, SP>(R[u], h[u], xs, x_in, row[u], t0, T);
   }
 }
 
@@ -1088,7 +1110,7 @@ constexpr int kSeg = 4;  // steps per segment of the long-row path
 // (q*64 + l)*4 of the wave's chunk), so every vector access of a wave covers 1 KB.  Against
 // one segment per thread (rows_kernel with NT = 512) a row has half the waves, so its wave
 // maps chain through LDS in at most NW - 1 = 3 applies instead of 7.  Launch: grid = E.
-template <class Op, int NT, int Q, bool VEC>
+template <class Op, int NT, int Q, bool VEC, int SP = 0>
 __global__ __launch_bounds__(NT) void rows_strided_kernel(const Op op, int64_t E, int T, int) {
   constexpr bool FWD = Op::kForward;
   constexpr int NW = NT / kWave;
@@ -1158,14 +1180,14 @@ __global__ __launch_bounds__(NT) void rows_strided_kernel(const Op op, int64_t E
     carry = rowagg[r].apply(carry);
     State xs[S];
     replay<FWD, S>(steps[r], x_in, xs);
-    op.template emit<S, VEC>(R[r], h[r], xs, x_in, row, seg_t0(r), T);
+    op.template emit<S, VEC, SP>(R[r], h[r], xs, x_in, row, seg_t0(r), T);
     if constexpr (Op::kBlockStats) op.template stats<S>(R[r], xs, seg_t0(r), T, st);
   }
   if constexpr (Op::kBlockStats) block_stats<NT>(st, op.partials);
 }
 
 
-template <class Op, int NT, int Q, bool VEC>
+template <class Op, int NT, int Q, bool VEC, int SP = 0>
 __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T, int tiles_per_row,
                                                    uint64_t* __restrict__ ws, uint64_t* __restrict__ fb,
                                                    int spin_limit, int fallback_polls,
@@ -1339,7 +1361,7 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
         carry = rowagg[r].apply(carry);
         State xs[kSeg];
         replay<FWD, kSeg>(steps[r], x_in, xs);
-        op.template emit<kSeg, VEC>(R[r], h[r], xs, x_in, row, seg_t0(r), T);
+        op.template emit<kSeg, VEC, SP>(R[r], h[r], xs, x_in, row, seg_t0(r), T);
         if constexpr (Op::kBlockStats) op.template stats<kSeg>(R[r], xs, seg_t0(r), T, st);
       }
       break;

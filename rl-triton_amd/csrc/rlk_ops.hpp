@@ -28,6 +28,7 @@ __device__ __forceinline__ void fill_regs(float (&v)[S], float x) {
 // ------------------------------------------------------------------------------------------
 template <bool TRUNC, class E = float>
 struct GaeOp {
+  using Elem = E;  // storage type of the float arrays
   static constexpr bool kForward = false;
   static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
   // long-row tiles: threads per workgroup and most 4-step segments per thread that stay
@@ -43,6 +44,7 @@ struct GaeOp {
   E* out;
   int boot_mode;
   float gamma, gl;  // gl = gamma*lambda
+
 
   template <int S>
   struct Regs {
@@ -90,10 +92,10 @@ struct GaeOp {
   }
   __device__ const E* row_carry_src(int64_t, int) const { return nullptr; }
 
-  template <int S, bool VEC>
+  template <int S, bool VEC, int SP = 0>
   __device__ void emit(const Regs<S>&, float, const float (&xs)[S], float, int64_t row, int t0,
                        int T) const {
-    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, SP != 0);
   }
 };
 
@@ -114,15 +116,15 @@ struct GaeStatsOp : GaeOp<TRUNC, E> {
   template <int S>
   using Regs = typename GaeOp<TRUNC, E>::template Regs<S>;
 
-  template <int S, bool VEC>
+  template <int S, bool VEC, int SP = 0>
   __device__ void emit(const Regs<S>& R, float, const float (&xs)[S], float, int64_t row, int t0,
                        int T) const {
     float rt[S];
 #pragma unroll
     for (int i = 0; i < S; ++i) rt[i] = xs[i] + R.v[i];
     const int64_t o = row * (int64_t)T;
-    store_seg<S, VEC>(this->out + o, t0, T, xs);
-    store_seg<S, VEC>(returns + o, t0, T, rt);
+    store_seg<S, VEC>(this->out + o, t0, T, xs, SP != 0);
+    store_seg<S, VEC>(returns + o, t0, T, rt, SP != 0);
   }
   // every step of the row counts
   template <int S>
@@ -150,6 +152,7 @@ struct GaeStatsOp : GaeOp<TRUNC, E> {
 // ------------------------------------------------------------------------------------------
 template <bool TRUNC, class E = float>
 struct MaskedGaeOp {
+  using Elem = E;  // storage type of the float arrays
   static constexpr bool kForward = false;
   static constexpr bool kBlockStats = false;
   static constexpr int kLongThreads = 512, kLongMaxSegments = 4;  // five-word maps
@@ -164,6 +167,7 @@ struct MaskedGaeOp {
   E* out;
   int boot_mode;
   float gamma, gl;  // gl = gamma*lambda
+
 
   template <int S>
   struct Regs {
@@ -209,13 +213,13 @@ struct MaskedGaeOp {
     }
   }
 
-  template <int S, bool VEC>
+  template <int S, bool VEC, int SP = 0>
   __device__ void emit(const Regs<S>&, NoHalo, const NvX (&xs)[S], NvX, int64_t row, int t0,
                        int T) const {
     float a[S];
 #pragma unroll
     for (int i = 0; i < S; ++i) a[i] = xs[i].x;
-    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, a);
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, a, SP != 0);
   }
 };
 
@@ -233,7 +237,7 @@ struct MaskedGaeStatsOp : MaskedGaeOp<TRUNC, E> {
   template <int S>
   using Regs = typename MaskedGaeOp<TRUNC, E>::template Regs<S>;
 
-  template <int S, bool VEC>
+  template <int S, bool VEC, int SP = 0>
   __device__ void emit(const Regs<S>& R, NoHalo, const NvX (&xs)[S], NvX, int64_t row, int t0,
                        int T) const {
     float a[S], rt[S];
@@ -243,8 +247,8 @@ struct MaskedGaeStatsOp : MaskedGaeOp<TRUNC, E> {
       rt[i] = xs[i].x + R.v[i];
     }
     const int64_t o = row * (int64_t)T;
-    store_seg<S, VEC>(this->out + o, t0, T, a);
-    store_seg<S, VEC>(returns + o, t0, T, rt);
+    store_seg<S, VEC>(this->out + o, t0, T, a, SP != 0);
+    store_seg<S, VEC>(returns + o, t0, T, rt, SP != 0);
   }
   template <int S>
   __device__ void stats(const Regs<S>& R, const NvX (&xs)[S], int t0, int T, Stats& st) const {
@@ -267,6 +271,7 @@ struct MaskedGaeStatsOp : MaskedGaeOp<TRUNC, E> {
 // ------------------------------------------------------------------------------------------
 template <bool TRUNC, class E = float>
 struct VtraceOp {
+  using Elem = E;  // storage type of the float arrays
   static constexpr bool kForward = false;
   static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
   static constexpr int kLongThreads = 1024, kLongMaxSegments = 2;
@@ -283,6 +288,7 @@ struct VtraceOp {
   E* adv;
   int boot_mode;
   float gamma, rho_bar, c_bar;
+
 
   template <int S>
   struct Regs {
@@ -341,7 +347,7 @@ struct VtraceOp {
   }
   __device__ const E* row_carry_src(int64_t, int) const { return nullptr; }
 
-  template <int S, bool VEC>
+  template <int S, bool VEC, int SP = 0>
   __device__ void emit(const Regs<S>& R, float vh, const float (&xs)[S], float x_next, int64_t row,
                        int t0, int T) const {
     float tg[S], ad[S];
@@ -355,8 +361,8 @@ struct VtraceOp {
       ad[i] = R.rho[i] * (fmaf(gamma * nt, 1.f - R.te[i], R.r[i]) - R.v[i]);
     }
     const int64_t o = row * (int64_t)T;
-    store_seg<S, VEC>(targets + o, t0, T, tg);
-    store_seg<S, VEC>(adv + o, t0, T, ad);
+    store_seg<S, VEC>(targets + o, t0, T, tg, SP != 0);
+    store_seg<S, VEC>(adv + o, t0, T, ad, SP != 0);
   }
 };
 
@@ -370,6 +376,7 @@ struct VtraceOp {
 // ------------------------------------------------------------------------------------------
 template <int NA, bool TRUNC, class E = float>
 struct RetraceOp {
+  using Elem = E;  // storage type of the float arrays
   static constexpr bool kForward = false;
   static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
   static constexpr int kLongThreads = 512, kLongMaxSegments = 2;  // 256 VGPRs: the A-wide rows
@@ -387,6 +394,7 @@ struct RetraceOp {
   E* adv;
   int A;
   float gamma, lambda, c_bar, rho_bar;
+
 
   template <int S>
   struct Regs {
@@ -493,7 +501,7 @@ struct RetraceOp {
   }
   __device__ const E* row_carry_src(int64_t, int) const { return nullptr; }
 
-  template <int S, bool VEC>
+  template <int S, bool VEC, int SP = 0>
   __device__ void emit(const Regs<S>& R, Halo2 h, const float (&xs)[S], float x_next, int64_t row,
                        int t0, int T) const {
     float tg[S], ad[S];
@@ -507,8 +515,8 @@ struct RetraceOp {
       ad[i] = R.rho[i] * (fmaf(gamma * nxt, 1.f - R.te[i], R.r[i]) - R.q[i]);
     }
     const int64_t o = row * (int64_t)T;
-    store_seg<S, VEC>(targets + o, t0, T, tg);
-    store_seg<S, VEC>(adv + o, t0, T, ad);
+    store_seg<S, VEC>(targets + o, t0, T, tg, SP != 0);
+    store_seg<S, VEC>(adv + o, t0, T, ad, SP != 0);
   }
 };
 
@@ -521,6 +529,7 @@ struct RetraceOp {
 // ------------------------------------------------------------------------------------------
 template <bool NV, bool TRUNC, class E = float>
 struct ReturnsOp {
+  using Elem = E;  // storage type of the float arrays
   static constexpr bool kForward = false;
   static constexpr bool kBlockStats = false;  // no per-workgroup output statistics
   // plain discounted returns (two arrays read): 512-thread tiles of up to 8 segments per
@@ -537,6 +546,7 @@ struct ReturnsOp {
   E* out;
   int boot_mode;
   float gamma, g1l, gl;  // gamma, gamma*(1-lambda), gamma*lambda (discounted: gl = gamma)
+
 
   template <int S>
   struct Regs {
@@ -581,10 +591,10 @@ struct ReturnsOp {
     return boot_mode == kBootNone ? nullptr : boot_last(boot, boot_mode, row, T);
   }
 
-  template <int S, bool VEC>
+  template <int S, bool VEC, int SP = 0>
   __device__ void emit(const Regs<S>&, NoHalo, const float (&xs)[S], float, int64_t row, int t0,
                        int T) const {
-    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, SP != 0);
   }
 };
 
@@ -598,6 +608,7 @@ struct ReturnsOp {
 // ------------------------------------------------------------------------------------------
 template <class E = float>
 struct DoneGatedForwardOp {
+  using Elem = E;  // storage type of the float arrays
   static constexpr bool kForward = true;
   static constexpr bool kBlockStats = false;
   static constexpr int kLongThreads = 1024, kLongMaxSegments = 8;
@@ -609,6 +620,7 @@ struct DoneGatedForwardOp {
   E* out;
   float decay;
   int ends_at;
+
 
   template <int S>
   struct Regs {
@@ -642,10 +654,10 @@ struct DoneGatedForwardOp {
   }
   __device__ const E* row_carry_src(int64_t row, int) const { return seed ? seed + row : nullptr; }
 
-  template <int S, bool VEC>
+  template <int S, bool VEC, int SP = 0>
   __device__ void emit(const Regs<S>&, float, const float (&xs)[S], float, int64_t row, int t0,
                        int T) const {
-    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, SP != 0);
   }
 };
 
@@ -655,6 +667,7 @@ struct DoneGatedForwardOp {
 // ------------------------------------------------------------------------------------------
 template <bool FWD, class E = float>
 struct AffineScanOp {
+  using Elem = E;  // storage type of the float arrays
   static constexpr bool kForward = FWD;
   static constexpr bool kBlockStats = false;
   static constexpr int kLongThreads = 1024, kLongMaxSegments = 8;
@@ -664,6 +677,7 @@ struct AffineScanOp {
   const E* v;
   const E* carry;  // nullable, [E]
   E* out;
+
 
   template <int S>
   struct Regs {
@@ -687,10 +701,10 @@ struct AffineScanOp {
     }
   }
   __device__ const E* row_carry_src(int64_t row, int) const { return carry ? carry + row : nullptr; }
-  template <int S, bool VEC>
+  template <int S, bool VEC, int SP = 0>
   __device__ void emit(const Regs<S>&, NoHalo, const float (&xs)[S], float, int64_t row, int t0,
                        int T) const {
-    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs);
+    store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, SP != 0);
   }
 };
 
