@@ -184,7 +184,7 @@ struct paired_rows : std::false_type {};
 template <int NA, bool TRUNC>
 struct paired_rows<RetraceOp<NA, TRUNC, float>> : std::true_type {};
 
-template <class Op, int NT, int S, bool VEC, int SP>
+template <class Op, int NT, int S, int VEC, int SP>
 hipError_t launch_rows(const Op& op, int64_t E, int T, hipStream_t stream) {
   int log2L = ceil_log2((T + S - 1) / S);
   const int64_t grid = rows_grid(E, T, S, NT);
@@ -255,8 +255,9 @@ std::atomic<int> g_fallback_polls{kFallbackPolls};
 // interleave.
 inline int chain_row_major(int64_t E, int64_t grid) { return E <= 16 && grid >= device_cus() ? 1 : 0; }
 
-template <class Op, int Q, bool VEC, int SP, int NT = Op::kLongThreads>
-hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_t stream) {
+// VEC = kPhased: phase0 = the element phase of row 0's arrays.
+template <class Op, int Q, int VEC, int SP, int NT = Op::kLongThreads>
+hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_t stream, int phase0) {
   static_assert(NT * kSeg * Q >= kMinTile, "the workspace is sized for the smallest tile");
   constexpr int64_t tile = (int64_t)NT * kSeg * Q;
   int tpr = (int)((T + tile - 1) / tile);
@@ -267,28 +268,28 @@ hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_
   int fallback_polls = g_fallback_polls.load(std::memory_order_relaxed);
   int row_major = chain_row_major(E, grid);
   void* args[] = {const_cast<Op*>(&op), &E, &T, &tpr, &ws, &fb, &spin_limit, &fallback_polls,
-                  &row_major};
+                  &row_major, &phase0};
   return hipLaunchKernel(reinterpret_cast<const void*>(&chain_kernel<Op, NT, Q, VEC, SP>),
                          dim3((unsigned)grid), dim3(NT), args, 0, stream);
 }
 
-template <class Op, bool VEC, int SP>
-hipError_t launch_long(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_t stream) {
+template <class Op, int VEC, int SP>
+hipError_t launch_long(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_t stream, int phase0) {
   const LongShape sh = long_shape<Op>(E, T);
   if constexpr (wide_long_tiles<Op>::value) {
-    if (sh.threads == 1024 && sh.segments == 4) return launch_chain<Op, 4, VEC, SP, 1024>(op, E, T, ws, stream);
-    if (sh.threads == 1024 && sh.segments == 2) return launch_chain<Op, 2, VEC, SP, 1024>(op, E, T, ws, stream);
+    if (sh.threads == 1024 && sh.segments == 4) return launch_chain<Op, 4, VEC, SP, 1024>(op, E, T, ws, stream, phase0);
+    if (sh.threads == 1024 && sh.segments == 2) return launch_chain<Op, 2, VEC, SP, 1024>(op, E, T, ws, stream, phase0);
   }
   constexpr int hq = half_width_segments<Op>::value;
   if constexpr (hq != 0) {
-    if (sh.threads == 512 && sh.segments == hq) return launch_chain<Op, hq, VEC, SP, 512>(op, E, T, ws, stream);
+    if (sh.threads == 512 && sh.segments == hq) return launch_chain<Op, hq, VEC, SP, 512>(op, E, T, ws, stream, phase0);
   }
   const int q = sh.segments;
   if constexpr (Op::kLongMaxSegments >= 8)
-    if (q == 8) return launch_chain<Op, 8, VEC, SP>(op, E, T, ws, stream);
+    if (q == 8) return launch_chain<Op, 8, VEC, SP>(op, E, T, ws, stream, phase0);
   if constexpr (Op::kLongMaxSegments >= 4)
-    if (q == 4) return launch_chain<Op, 4, VEC, SP>(op, E, T, ws, stream);
-  return launch_chain<Op, 2, VEC, SP>(op, E, T, ws, stream);
+    if (q == 4) return launch_chain<Op, 4, VEC, SP>(op, E, T, ws, stream, phase0);
+  return launch_chain<Op, 2, VEC, SP>(op, E, T, ws, stream, phase0);
 }
 
 // Output stores: non-temporal (the default) or write-through (sc1, store_quad_wt), per
@@ -360,9 +361,23 @@ hipError_t dispatch_store_policy(int64_t E, int64_t T, F&& f) {
   }
 }
 
+// Ops that take long rows in the phased access mode: all but Retrace (whose [E, T, A]
+// arrays have no common row phase) and the statistics ops of compute_gae_normalized (the
+// steps a phased row takes ahead of its tiles would be missing from their statistics).
+template <class Op>
+struct phased_rows : std::true_type {};
+template <int NA, bool TRUNC, class E>
+struct phased_rows<RetraceOp<NA, TRUNC, E>> : std::false_type {};
+template <bool TRUNC, class E>
+struct phased_rows<GaeStatsOp<TRUNC, E>> : std::false_type {};
+template <bool TRUNC, class E>
+struct phased_rows<MaskedGaeStatsOp<TRUNC, E>> : std::false_type {};
+
+// vec: kAligned access.  phase0 >= 0: the element phase every [E, T] array of the call
+// shares at row 0 (common_phase), for the phased access of long rows when T % 4 != 0.
 template <class Op>
 int launch(const Op& op, int64_t E, int64_t T, bool vec, void* workspace, size_t workspace_bytes_given,
-           void* stream) {
+           void* stream, int phase0 = -1) {
   if (E < 0 || T < 0 || T > (int64_t{1} << 30)) return RLK_ERR_INVALID_ARGUMENT;
   if (E == 0 || T == 0) return RLK_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -372,9 +387,14 @@ int launch(const Op& op, int64_t E, int64_t T, bool vec, void* workspace, size_t
     uint64_t* ws = reinterpret_cast<uint64_t*>(workspace);
     if (ws == nullptr || workspace_bytes_given < workspace_bytes(E, T) || !aligned16(ws))
       return RLK_ERR_WORKSPACE;
+    const bool phased = phased_rows<Op>::value && !vec && phase0 >= 0 && T % 4 != 0;
     e = dispatch_store_policy<Op, Kernel::kChain>(E, T, [&](auto sp) {
       constexpr int SP = decltype(sp)::value;
-      return vec ? launch_long<Op, true, SP>(op, E, Ti, ws, s) : launch_long<Op, false, SP>(op, E, Ti, ws, s);
+      if constexpr (phased_rows<Op>::value) {
+        if (phased) return launch_long<Op, kPhased, SP>(op, E, Ti, ws, s, phase0);
+      }
+      return vec ? launch_long<Op, kAligned, SP>(op, E, Ti, ws, s, 0)
+                 : launch_long<Op, kElementAligned, SP>(op, E, Ti, ws, s, 0);
     });
   } else if (strided_rows<Op>::value && vec && T > kShortMaxT / 2) {
     e = dispatch_store_policy<Op, Kernel::kStrided>(E, T, [&](auto sp) {
@@ -412,6 +432,22 @@ template <class E, class... R>
 bool quad_aligned(const E* p, const R*... rest) {
   return quad_aligned(p) && quad_aligned(rest...);
 }
+// The element phase (address / sizeof(E), mod 4) that every non-null array shares, or -1
+// when two differ or one is not element-aligned.  Arrays of one call hold [E, T] rows at
+// the same offsets, so a shared phase at row 0 makes every row's phase shared too.
+template <class E, class... P>
+int common_phase(const P*... ptrs) {
+  int ph = -1;
+  for (const E* p : {static_cast<const E*>(ptrs)...}) {
+    if (p == nullptr) continue;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    if (a % sizeof(E) != 0) return -1;
+    const int q = (int)((a / sizeof(E)) & 3);
+    if (ph >= 0 && q != ph) return -1;
+    ph = q;
+  }
+  return ph;
+}
 
 // ---------------------------------------------------------------------------------------
 // Entry points, one template per estimator over the storage type E (float or bf16); the
@@ -428,14 +464,16 @@ int gae_impl(const E* rewards, const E* values, const E* terminateds, const E* t
   const bool vec = seq_len % 4 == 0 &&
                    quad_aligned(rewards, values, terminateds, truncateds, advantages) &&
                    (boot_mode != RLK_BOOT_FULL || quad_aligned(bootstrap));
+  const int ph = common_phase<E>(rewards, values, terminateds, truncateds, advantages,
+                                 boot_mode == RLK_BOOT_FULL ? bootstrap : nullptr);
   if (truncateds) {
     GaeOp<true, E> op{rewards, values, terminateds, truncateds, boot, advantages, boot_mode, gamma,
                       gamma * lambda_};
-    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream, ph);
   }
   GaeOp<false, E> op{rewards, values, terminateds, nullptr, boot, advantages, boot_mode, gamma,
                      gamma * lambda_};
-  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream, ph);
 }
 
 template <class E>
@@ -451,14 +489,16 @@ int gae_masked_impl(const E* rewards, const E* values, const E* terminateds, con
   const bool vec = seq_len % 4 == 0 &&
                    quad_aligned(rewards, values, terminateds, truncateds, mask, advantages) &&
                    (boot_mode != RLK_BOOT_FULL || quad_aligned(bootstrap));
+  const int ph = common_phase<E>(rewards, values, terminateds, truncateds, mask, advantages,
+                                 boot_mode == RLK_BOOT_FULL ? bootstrap : nullptr);
   if (truncateds) {
     MaskedGaeOp<true, E> op{rewards, values, terminateds, truncateds, boot, mask, advantages,
                             boot_mode, gamma, gamma * lambda_};
-    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream, ph);
   }
   MaskedGaeOp<false, E> op{rewards, values, terminateds, nullptr, boot, mask, advantages,
                            boot_mode, gamma, gamma * lambda_};
-  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream, ph);
 }
 
 // Partials of compute_gae_normalized: kStatWords doubles per workgroup of the first launch,
@@ -555,14 +595,17 @@ int vtrace_impl(const E* log_pi_target, const E* log_pi_behavior, const E* value
                    quad_aligned(log_pi_target, log_pi_behavior, values, rewards, terminateds,
                                 truncateds, targets, advantages) &&
                    (boot_mode != RLK_BOOT_FULL || quad_aligned(bootstrap));
+  const int ph = common_phase<E>(log_pi_target, log_pi_behavior, values, rewards, terminateds,
+                                 truncateds, targets, advantages,
+                                 boot_mode == RLK_BOOT_FULL ? bootstrap : nullptr);
   if (truncateds) {
     VtraceOp<true, E> op{log_pi_target, log_pi_behavior, values, rewards, terminateds, truncateds,
                          boot, targets, advantages, boot_mode, gamma, rho_bar, c_bar};
-    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream, ph);
   }
   VtraceOp<false, E> op{log_pi_target, log_pi_behavior, values, rewards, terminateds, nullptr,
                         boot, targets, advantages, boot_mode, gamma, rho_bar, c_bar};
-  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream, ph);
 }
 
 template <class E>
@@ -617,14 +660,16 @@ int lambda_returns_impl(const E* rewards, const E* next_values, const E* termina
   const bool vec = seq_len % 4 == 0 &&
                    quad_aligned(rewards, next_values, terminateds, truncateds, returns) &&
                    (boot_mode != RLK_BOOT_FULL || quad_aligned(bootstrap));
+  const int ph = common_phase<E>(rewards, next_values, terminateds, truncateds, returns,
+                                 boot_mode == RLK_BOOT_FULL ? bootstrap : nullptr);
   if (truncateds) {
     ReturnsOp<true, true, E> op{rewards, next_values, terminateds, truncateds, boot, returns,
                                 boot_mode, gamma, gamma * (1.f - lambda_), gamma * lambda_};
-    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream, ph);
   }
   ReturnsOp<true, false, E> op{rewards, next_values, terminateds, nullptr, boot, returns,
                                boot_mode, gamma, gamma * (1.f - lambda_), gamma * lambda_};
-  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream, ph);
 }
 
 template <class E>
@@ -638,14 +683,16 @@ int discounted_returns_impl(const E* rewards, const E* terminateds, const E* tru
   const E* boot = boot_mode == RLK_BOOT_NONE ? nullptr : bootstrap;
   const bool vec = seq_len % 4 == 0 && quad_aligned(rewards, terminateds, truncateds, returns) &&
                    (boot_mode != RLK_BOOT_FULL || quad_aligned(bootstrap));
+  const int ph = common_phase<E>(rewards, terminateds, truncateds, returns,
+                                 boot_mode == RLK_BOOT_FULL ? bootstrap : nullptr);
   if (truncateds) {
     ReturnsOp<false, true, E> op{rewards, nullptr, terminateds, truncateds, boot, returns,
                                  boot_mode, gamma, 0.f, gamma};
-    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream, ph);
   }
   ReturnsOp<false, false, E> op{rewards, nullptr, terminateds, nullptr, boot, returns, boot_mode,
                                 gamma, 0.f, gamma};
-  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream, ph);
 }
 
 // eligibility traces (decay = gamma * lambda, gated on done[t-1]) and the episodic prefix
@@ -658,7 +705,8 @@ int done_gated_impl(const E* x, const E* dones, const E* seed, E* out, int64_t n
   if (!x || !dones || !out) return RLK_ERR_INVALID_ARGUMENT;
   DoneGatedForwardOp<E> op{x, dones, seed, out, decay, ends_at};
   const bool vec = seq_len % 4 == 0 && quad_aligned(x, dones, out);
-  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream,
+                common_phase<E>(x, dones, out));
 }
 
 template <class E>
@@ -669,12 +717,13 @@ int affine_scan_impl(const E* u, const E* v, const E* carry, E* out, int64_t num
   if (!u || !v || !out || (direction != RLK_BACKWARD && direction != RLK_FORWARD))
     return RLK_ERR_INVALID_ARGUMENT;
   const bool vec = seq_len % 4 == 0 && quad_aligned(u, v, out);
+  const int ph = common_phase<E>(u, v, out);
   if (direction == RLK_FORWARD) {
     AffineScanOp<true, E> op{u, v, carry, out};
-    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+    return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream, ph);
   }
   AffineScanOp<false, E> op{u, v, carry, out};
-  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
+  return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream, ph);
 }
 
 // ---------------------------------------------------------------------------------------

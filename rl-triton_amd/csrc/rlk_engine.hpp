@@ -240,27 +240,61 @@ __device__ __forceinline__ void store_one_nt(bf16* p, float v) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Segment loads / stores.  VEC: T % 4 == 0 and every base pointer aligned to four elements
-// (16 bytes for float32, 8 for bfloat16), so a segment start t0 (a multiple of 4) is
-// aligned and each quad is all-in or all-out.  A 4-step segment is one quad per lane with
-// the lanes of a wave on consecutive quads (both kernels lay segments out that way), so it
-// streams non-temporally.
+// Segment loads / stores, in one of three access modes (the VEC template argument):
 //
-// Otherwise (T % 4 != 0, or a pointer off a four-element boundary) the quads are only
-// element-aligned.  A quad wholly inside the row is still one access (load_quad_ua); the
-// row's partial last quad is read as the row's last four elements and shifted into place.
-// Rows shorter than four steps use segments of one step (S = 1), element by element.
+// kAligned (1): T % 4 == 0 and every base pointer aligned to four elements (16 bytes for
+// float32, 8 for bfloat16), so a segment start t0 (a multiple of 4) is aligned and each
+// quad is all-in or all-out.  A 4-step segment is one quad per lane with the lanes of a
+// wave on consecutive quads (every kernel lays segments out that way), so it streams
+// non-temporally.
 //
-// Loads are unconditional: a step beyond T reads the row's last element (VEC: its last
-// quad).  Padding steps are masked to the identity map in coef() and are not stored, so
-// their register contents never matter.
+// kPhased (2, long rows only): T % 4 != 0, and every [E, T] array of the call starts at the
+// same element phase (address / element size, mod 4).  Each row's segments are shifted to
+// its own four-element boundary (t0 = 4j + shift, shift = -ph backward, (4 - ph) % 4
+// forward, ph the row's phase 0..3; see chain_kernel), so every quad is one aligned access
+// again.  A row's first quad reaches up to 3 steps before step 0, its last up to 3 beyond
+// step T - 1: both stay inside the aligned 16-byte (bfloat16: 8-byte) block that holds the
+// row's first (last) element, so they never leave a mapped page, and their foreign steps
+// are masked (step_in) and not stored.  Stores of those two quads go element by element.
+//
+// kElementAligned (0): every other case.  A quad wholly inside the row is still one access
+// (load_quad_ua); the row's partial last quad is read as the row's last four elements and
+// shifted into place.  Rows shorter than four steps use segments of one step (S = 1),
+// element by element.
+//
+// Loads are unconditional: a step beyond T reads the row's last element (kAligned,
+// kPhased: its last quad).  Padding steps are masked to the identity map in coef() and are
+// not stored, so their register contents never matter.
 // ---------------------------------------------------------------------------------------
+constexpr int kElementAligned = 0, kAligned = 1, kPhased = 2;
+
+// Step t (of a segment starting at t0) lies inside the row [0, T).  kAligned segments are
+// all-in or all-out; only kPhased steps can lie before the row.
+template <int VEC>
+__device__ __forceinline__ bool step_in(int t0, int t, int T) {
+  if constexpr (VEC == kAligned) return t0 < T;
+  else if constexpr (VEC == kPhased) return (unsigned)t < (unsigned)T;
+  else return t < T;
+}
 __device__ __forceinline__ int clamp_step(int t, int T) { return t < 0 ? 0 : (t < T ? t : T - 1); }
 
-template <int S, bool VEC, class E>
+template <int S, int VEC, class E>
 __device__ __forceinline__ void load_seg(const E* __restrict__ p, int t0, int T, float (&v)[S]) {
-  static_assert(!VEC || S % 4 == 0, "vector segments hold whole quads");
-  if constexpr (VEC) {
+  static_assert(VEC == kElementAligned || S % 4 == 0, "vector segments hold whole quads");
+  if constexpr (VEC == kPhased) {
+    // t0 + ph is a multiple of 4 (ph the row's phase): every quad start is aligned.  Quads
+    // beyond the row read the one that holds step T - 1 (tq, at the same phase).
+    const int tq = (T - 1) - ((T - 1 - t0) & 3);
+#pragma unroll
+    for (int q = 0; q < S / 4; ++q) {
+      const int t = t0 + 4 * q;
+      const float4 f = load_quad<S == 4>(p + (t < T ? t : tq));
+      v[4 * q + 0] = f.x;
+      v[4 * q + 1] = f.y;
+      v[4 * q + 2] = f.z;
+      v[4 * q + 3] = f.w;
+    }
+  } else if constexpr (VEC == kAligned) {
 #pragma unroll
     for (int q = 0; q < S / 4; ++q) {
       const int t = t0 + 4 * q;
@@ -296,11 +330,29 @@ __device__ __forceinline__ void load_seg(const E* __restrict__ p, int t0, int T,
 }
 
 // Steps beyond T are not stored.  wt: vector quads take store_quad_wt.
-template <int S, bool VEC, class E>
+template <int S, int VEC, class E>
 __device__ __forceinline__ void store_seg(E* __restrict__ p, int t0, int T, const float (&v)[S],
                                           bool wt = false) {
-  static_assert(!VEC || S % 4 == 0, "vector segments hold whole quads");
-  if constexpr (VEC) {
+  static_assert(VEC == kElementAligned || S % 4 == 0, "vector segments hold whole quads");
+  if constexpr (VEC == kPhased) {
+#pragma unroll
+    for (int q = 0; q < S / 4; ++q) {
+      const int t = t0 + 4 * q;
+      if (t >= 0 && t + 4 <= T) {
+        const float4 f = make_float4(v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+        if (wt) store_quad_wt(p + t, f);
+        else store_quad<S == 4>(p + t, f);
+      } else if (t < T) {  // the row's first or last quad: its own steps only
+        // Not step_in's test: written as that, the compiler kept coef's per-step masks (one
+        // per step of every segment) live up to here, and the 1024-thread instances spilled
+        // 24-176 B per lane.
+        const int lo = -t, hi = T - t;  // element i of the quad is step t + i
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (i >= lo && i < hi) p[t + i] = from_f32<E>(v[4 * q + i]);
+      }
+    }
+  } else if constexpr (VEC == kAligned) {
 #pragma unroll
     for (int q = 0; q < S / 4; ++q) {
       const int t = t0 + 4 * q;
@@ -355,7 +407,7 @@ __device__ __forceinline__ const E* boot_last(const E* boot, int mode, int64_t r
 //   PER_STEP = true:  a per-step array is read in full; with a per-row value (or none) the
 //                     segment loads read `any_row` (any readable [T] row) and are discarded.
 // boot_prepare turns the raw registers into bt[i] = boot(t0 + i).
-template <int S, bool VEC, bool PER_STEP, class E>
+template <int S, int VEC, bool PER_STEP, class E>
 __device__ __forceinline__ void boot_load(const E* __restrict__ boot, int mode, int64_t row,
                                           int t0, int T, float (&seg)[S], float& last,
                                           const E* any_row) {
@@ -678,8 +730,9 @@ __device__ __forceinline__ M lane_scan(M m, int W) {
 // [4096,128] 4.12 -> 3.99 us, GAE 3.99 -> 3.80 us, GAE [8192,64] 3.97 -> 3.78 us, TD(lambda)
 // [256,2048] 3.61 -> 3.48 us, element-aligned V-trace [4096,127] 4.80 -> 4.66 us on MI355X
 // (bit-identical results).
-template <class Op, int NT, int S, bool VEC, int WT = 0, int SP = 0>
+template <class Op, int NT, int S, int VEC, int WT = 0, int SP = 0>
 __global__ __launch_bounds__(NT) void rows_kernel(const Op op, int64_t E, int T, int log2L_arg) {
+  static_assert(VEC != kPhased, "phased access is for long rows");
   constexpr bool FWD = Op::kForward;
   constexpr int NW = NT / kWave;
   using Regs = typename Op::template Regs<S>;
@@ -1110,8 +1163,9 @@ constexpr int kSeg = 4;  // steps per segment of the long-row path
 // (q*64 + l)*4 of the wave's chunk), so every vector access of a wave covers 1 KB.  Against
 // one segment per thread (rows_kernel with NT = 512) a row has half the waves, so its wave
 // maps chain through LDS in at most NW - 1 = 3 applies instead of 7.  Launch: grid = E.
-template <class Op, int NT, int Q, bool VEC, int SP = 0>
+template <class Op, int NT, int Q, int VEC, int SP = 0>
 __global__ __launch_bounds__(NT) void rows_strided_kernel(const Op op, int64_t E, int T, int) {
+  static_assert(VEC != kPhased, "phased access is for long rows");
   constexpr bool FWD = Op::kForward;
   constexpr int NW = NT / kWave;
   constexpr int S = 4;
@@ -1187,11 +1241,11 @@ __global__ __launch_bounds__(NT) void rows_strided_kernel(const Op op, int64_t E
 }
 
 
-template <class Op, int NT, int Q, bool VEC, int SP = 0>
+template <class Op, int NT, int Q, int VEC, int SP = 0>
 __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T, int tiles_per_row,
                                                    uint64_t* __restrict__ ws, uint64_t* __restrict__ fb,
                                                    int spin_limit, int fallback_polls,
-                                                   int row_major) {
+                                                   int row_major, int phase0) {
   constexpr bool FWD = Op::kForward;
   constexpr int NW = NT / kWave;
   constexpr int WSTEPS = Q * kWave * kSeg;  // steps per wave chunk
@@ -1267,11 +1321,25 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
     const int jpos = (int)(q_t - (uint64_t)lr * tiles_per_row);
     const int64_t row = slot + (int64_t)nslots * lr;
     const int k_own = FWD ? jpos : tiles_per_row - 1 - jpos;
+    // kPhased: the row's element phase ph (phase0 is row 0's) shifts its tiles to the row's
+    // four-element boundaries: backward by -ph, so they cover [-ph, tiles*tile - ph) and
+    // leave the row's last steps from tiles*tile - ph on (0..3 of them); forward by
+    // (4 - ph) % 4, leaving steps 0 .. shift-1.  Those steps come first in scan order: the
+    // first tile in scan order takes them as one more quad (pre_t0) ahead of its own,
+    // applied to the row's carry.  The tile count stays ceil(T / tile).
+    int shift = 0;
+    if constexpr (VEC == kPhased) {
+      const int ph = (int)(((uint64_t)phase0 + (uint64_t)row * (uint64_t)T) & 3u);
+      shift = FWD ? ((4 - ph) & 3) : -ph;
+    }
+    const int pre_t0 = FWD ? shift - kSeg : tiles_per_row * (NW * WSTEPS) + shift;
+    // ... when they hold a step of the row (otherwise the quad would lie wholly outside it)
+    const bool pre_live = VEC == kPhased && (FWD ? shift > 0 : pre_t0 < T);
     // Tile k_own, or first a predecessor the look-back hands back (its map computed here,
     // then this tile again from its loads).
     for (int k = k_own, it = 0;; ++it) {
       // lane space -> time: this wave's chunk, and the first step of segment row r
-      const int wbase = (k * NW + (FWD ? wave : NW - 1 - wave)) * WSTEPS;
+      const int wbase = (k * NW + (FWD ? wave : NW - 1 - wave)) * WSTEPS + shift;
       const int lt = FWD ? lane : kWave - 1 - lane;
       auto seg_t0 = [&](int r) { return wbase + ((FWD ? r : Q - 1 - r) * kWave + lt) * kSeg; };
 
@@ -1285,7 +1353,8 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
           edge = op.halo_load(row, clamp_step(FWD ? wbase - 1 : wbase + WSTEPS, T), T);
       }
       const bool first = FWD ? (k == 0) : (k == tiles_per_row - 1);
-      const State rc = (first && wave == 0) ? row_carry(op, row, T) : State{};
+      State rc = (first && wave == 0) ? row_carry(op, row, T) : State{};
+      [[maybe_unused]] Regs Rp;  // kPhased: the steps ahead of the row's tiles (below)
       if (it == 0 && tid == 0) {  // the epoch load was issued before the tile's loads
         s_epoch = (uint32_t)e_raw & kEpochMask;
         count_drawn();
@@ -1314,6 +1383,27 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
         op.template coef<kSeg, VEC>(R[r], h[r], row, seg_t0(r), T, steps[r]);
         m[r] = lane_scan(fold_segment<FWD, kSeg>(steps[r]), kWave);
         rowagg[r] = lane_bcast(m[r], kWave - 1);
+      }
+      if constexpr (VEC == kPhased) {
+        // The steps ahead of the row's tiles (pre_t0), on every lane of wave 0 alike: the
+        // row's carry through them, and their outputs, stored by lane 0 of the tile's own
+        // workgroup.  Loaded here, after the tile's coefficients: loaded with the tile's
+        // own loads, the quad's registers stayed live across them and the 1024-thread
+        // instances spilled 20-68 B per lane; here it costs wave 0 of one tile per row one
+        // load's latency (prefix sum [8,2^20-1] 20.59 -> 19.55 us, GAE [64,40001]
+        // 19.41 -> 17.52 us on MI355X).
+        if (first && wave == 0 && pre_live) {
+          op.template load<kSeg, VEC>(row, pre_t0, T, Rp);
+          op.template prepare<kSeg, VEC>(Rp, row, pre_t0, T);
+          Halo hp{};
+          if constexpr (HAS_HALO) hp = op.halo_load(row, clamp_step(FWD ? pre_t0 - 1 : pre_t0 + kSeg, T), T);
+          Map sp[kSeg];
+          op.template coef<kSeg, VEC>(Rp, hp, row, pre_t0, T, sp);
+          State xp[kSeg];
+          replay<FWD, kSeg>(sp, rc, xp);
+          if (k == k_own && lane == 0) op.template emit<kSeg, VEC, SP>(Rp, hp, xp, rc, row, pre_t0, T);
+          rc = fold_segment<FWD, kSeg>(sp).apply(rc);
+        }
       }
       // the chunk's map: segment rows composed in scan order
       Map wm = Map::identity();

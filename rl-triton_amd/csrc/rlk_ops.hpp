@@ -52,7 +52,7 @@ struct GaeOp {
     float blast;
   };
 
-  template <int S, bool VEC>
+  template <int S, int VEC>
   __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
     const int64_t o = row * (int64_t)T;
     load_seg<S, VEC>(r + o, t0, T, R.r);
@@ -62,7 +62,7 @@ struct GaeOp {
     else fill_regs(R.tr, 0.f);
     boot_load<S, VEC, TRUNC>(boot, boot_mode, row, t0, T, R.bt, R.blast, r + o);
   }
-  template <int S, bool VEC>
+  template <int S, int VEC>
   __device__ void prepare(Regs<S>& R, int64_t, int t0, int T) const {
     boot_prepare<S, TRUNC>(boot_mode, t0, T, R.bt, R.blast);
   }
@@ -70,29 +70,29 @@ struct GaeOp {
   __device__ float export_first(const Regs<S>& R) const { return R.v[0]; }
   __device__ float halo_load(int64_t row, int t, int T) const { return to_f32(v[row * (int64_t)T + t]); }
 
-  template <int S, bool VEC = false>
+  template <int S, int VEC = kElementAligned>
   __device__ void coef(const Regs<S>& R, float vh, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
       const float raw = (i + 1 < S) ? R.v[i + 1] : vh;
-      // VEC: T % 4 == 0 and t0 % 4 == 0, so a segment is all in or all padding, and only
-      // its last step can be T - 1 (one comparison per segment instead of one per step)
-      const bool at_end = VEC ? (i == S - 1 && t0 + S == T) : (t == T - 1);
+      // kAligned: T % 4 == 0 and t0 % 4 == 0, so a segment is all in or all padding, and
+      // only its last step can be T - 1 (one comparison per segment instead of one per step)
+      const bool at_end = VEC == kAligned ? (i == S - 1 && t0 + S == T) : (t == T - 1);
       // `|`, not `||`: the short circuit compiled to a divergent branch on the path after
       // the loads (C2 [4096,128] 3.82 -> 3.80 us, bfloat16 3.28 -> 3.18 us on MI355X)
       const bool use_boot = at_end | (R.tr[i] == 1.f);
       const float vn = use_boot ? R.bt[i] : raw;
       const float done = TRUNC ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
       const float a = fmaf(gamma * vn, 1.f - R.te[i], R.r[i]) - R.v[i];
-      const bool in = VEC ? t0 < T : t < T;  // padding steps are the identity map
+      const bool in = step_in<VEC>(t0, t, T);  // padding steps are the identity map
       m[i].add = in ? a : 0.f;
       m[i].mul = in ? gl * (1.f - done) : 1.f;
     }
   }
   __device__ const E* row_carry_src(int64_t, int) const { return nullptr; }
 
-  template <int S, bool VEC, int SP = 0>
+  template <int S, int VEC, int SP = 0>
   __device__ void emit(const Regs<S>&, float, const float (&xs)[S], float, int64_t row, int t0,
                        int T) const {
     store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, SP != 0);
@@ -116,9 +116,10 @@ struct GaeStatsOp : GaeOp<TRUNC, E> {
   template <int S>
   using Regs = typename GaeOp<TRUNC, E>::template Regs<S>;
 
-  template <int S, bool VEC, int SP = 0>
+  template <int S, int VEC, int SP = 0>
   __device__ void emit(const Regs<S>& R, float, const float (&xs)[S], float, int64_t row, int t0,
                        int T) const {
+    static_assert(VEC != kPhased, "stats() does not see the steps ahead of a phased row's tiles");
     float rt[S];
 #pragma unroll
     for (int i = 0; i < S; ++i) rt[i] = xs[i] + R.v[i];
@@ -175,7 +176,7 @@ struct MaskedGaeOp {
     float blast;
   };
 
-  template <int S, bool VEC>
+  template <int S, int VEC>
   __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
     const int64_t o = row * (int64_t)T;
     load_seg<S, VEC>(r + o, t0, T, R.r);
@@ -190,7 +191,7 @@ struct MaskedGaeOp {
       R.blast = 0.f;
     }
   }
-  template <int S, bool VEC>
+  template <int S, int VEC>
   __device__ void prepare(Regs<S>& R, int64_t, int t0, int T) const {
     if constexpr (TRUNC) boot_prepare<S, true>(boot_mode, t0, T, R.bt, R.blast);
   }
@@ -199,7 +200,7 @@ struct MaskedGaeOp {
     return NvX{to_f32(*boot_last(boot, boot_mode, row, T)), 0.f};
   }
 
-  template <int S, bool VEC = false>
+  template <int S, int VEC = kElementAligned>
   __device__ void coef(const Regs<S>& R, NoHalo, int64_t, int t0, int T, SkipAffine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
@@ -207,13 +208,13 @@ struct MaskedGaeOp {
       const float done = TRUNC ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
       const float g1 = gamma * (1.f - R.te[i]);
       const float d = sel ? fmaf(gamma * R.bt[i], 1.f - R.te[i], R.r[i]) - R.v[i] : R.r[i] - R.v[i];
-      const bool kept = (VEC ? t0 < T : t0 + i < T) && R.mk[i] != 0.f;  // padding steps too
+      const bool kept = (step_in<VEC>(t0, t0 + i, T)) && R.mk[i] != 0.f;  // padding steps too
       m[i] = kept ? SkipAffine{0.f, R.v[i], sel ? 0.f : g1, gl * (1.f - done), d}
                   : SkipAffine::identity();
     }
   }
 
-  template <int S, bool VEC, int SP = 0>
+  template <int S, int VEC, int SP = 0>
   __device__ void emit(const Regs<S>&, NoHalo, const NvX (&xs)[S], NvX, int64_t row, int t0,
                        int T) const {
     float a[S];
@@ -237,9 +238,10 @@ struct MaskedGaeStatsOp : MaskedGaeOp<TRUNC, E> {
   template <int S>
   using Regs = typename MaskedGaeOp<TRUNC, E>::template Regs<S>;
 
-  template <int S, bool VEC, int SP = 0>
+  template <int S, int VEC, int SP = 0>
   __device__ void emit(const Regs<S>& R, NoHalo, const NvX (&xs)[S], NvX, int64_t row, int t0,
                        int T) const {
+    static_assert(VEC != kPhased, "stats() does not see the steps ahead of a phased row's tiles");
     float a[S], rt[S];
 #pragma unroll
     for (int i = 0; i < S; ++i) {
@@ -296,7 +298,7 @@ struct VtraceOp {
     float blast;
   };
 
-  template <int S, bool VEC>
+  template <int S, int VEC>
   __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
     const int64_t o = row * (int64_t)T;
     load_seg<S, VEC>(lpt + o, t0, T, R.rho);
@@ -308,7 +310,7 @@ struct VtraceOp {
     else fill_regs(R.tr, 0.f);
     boot_load<S, VEC, TRUNC>(boot, boot_mode, row, t0, T, R.bt, R.blast, r + o);
   }
-  template <int S, bool VEC>
+  template <int S, int VEC>
   __device__ void prepare(Regs<S>& R, int64_t, int t0, int T) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
@@ -331,23 +333,23 @@ struct VtraceOp {
     return last ? bt : raw;
   }
 
-  template <int S, bool VEC = false>
+  template <int S, int VEC = kElementAligned>
   __device__ void coef(const Regs<S>& R, float vh, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
-      const bool last = VEC ? (i == S - 1 && t0 + S == T) : (t == T - 1);
+      const bool last = VEC == kAligned ? (i == S - 1 && t0 + S == T) : (t == T - 1);
       const float vn = next_value((i + 1 < S) ? R.v[i + 1] : vh, R.tr[i], R.bt[i], last);
       const float done = TRUNC ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i];
       const float a = R.rho[i] * (fmaf(gamma * vn, 1.f - R.te[i], R.r[i]) - R.v[i]);
-      const bool in = VEC ? t0 < T : t < T;
+      const bool in = step_in<VEC>(t0, t, T);
       m[i].add = in ? a : 0.f;
       m[i].mul = in ? gamma * R.c[i] * (1.f - done) : 1.f;
     }
   }
   __device__ const E* row_carry_src(int64_t, int) const { return nullptr; }
 
-  template <int S, bool VEC, int SP = 0>
+  template <int S, int VEC, int SP = 0>
   __device__ void emit(const Regs<S>& R, float vh, const float (&xs)[S], float x_next, int64_t row,
                        int t0, int T) const {
     float tg[S], ad[S];
@@ -356,7 +358,7 @@ struct VtraceOp {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const float raw = (i + 1 < S) ? tg[i + 1] : x_next + vh;
-      const bool last = VEC ? (i == S - 1 && t0 + S == T) : (t0 + i == T - 1);
+      const bool last = VEC == kAligned ? (i == S - 1 && t0 + S == T) : (t0 + i == T - 1);
       const float nt = next_value(raw, R.tr[i], R.bt[i], last);
       ad[i] = R.rho[i] * (fmaf(gamma * nt, 1.f - R.te[i], R.r[i]) - R.v[i]);
     }
@@ -420,8 +422,9 @@ struct RetraceOp {
 
   // Unlike the other ops, the [S, A] action blocks are reduced to (rho, c, E_pi[Q']) here,
   // at load time, so a segment holds three values per step instead of 2A.
-  template <int S, bool VEC>
+  template <int S, int VEC>
   __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
+    static_assert(VEC != kPhased, "the [E, T, A] arrays have no common row phase");
     const int64_t o = row * (int64_t)T;
     float m[S];
     load_seg<S, VEC>(q + o, t0, T, R.q);
@@ -431,7 +434,7 @@ struct RetraceOp {
     else fill_regs(R.tr, 0.f);
     load_seg<S, VEC>(mu + o, t0, T, m);
     int64_t at[S];
-    if constexpr (VEC) {
+    if constexpr (VEC == kAligned) {
       // a quad of actions is 32 contiguous bytes, 16-byte aligned (the launch checks the
       // pointer): two 16-byte loads instead of four 8-byte ones (Retrace [4096,128]
       // 6.60 -> 6.53 us on MI355X); a quad beyond T reads the row's last quad
@@ -447,7 +450,7 @@ struct RetraceOp {
 #pragma unroll
       for (int i = 0; i < S; ++i) at[i] = act[o + clamp_step(t0 + i, T)];
     }
-    if constexpr (NA > 0 && VEC && (S * NA) % 4 == 0 && S * NA <= 16) {
+    if constexpr (NA > 0 && VEC == kAligned && (S * NA) % 4 == 0 && S * NA <= 16) {
       // the [S, NA] blocks are contiguous and 16-byte aligned; a quad beyond T reads the
       // row's first quad instead.  (Larger blocks take the per-step path below: two tiles
       // of them would not fit the register file.)
@@ -473,7 +476,7 @@ struct RetraceOp {
       }
     }
   }
-  template <int S, bool VEC>
+  template <int S, int VEC>
   __device__ void prepare(Regs<S>&, int64_t, int, int) const {}
   template <int S>
   __device__ Halo2 export_first(const Regs<S>& R) const { return Halo2{R.c[0], R.q[0]}; }
@@ -485,23 +488,23 @@ struct RetraceOp {
     return Halo2{c, to_f32(q[i])};
   }
 
-  template <int S, bool VEC = false>
+  template <int S, int VEC = kElementAligned>
   __device__ void coef(const Regs<S>& R, Halo2 h, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
-      const bool before_end = VEC ? (i < S - 1 ? t0 < T : t0 + S < T) : (t < T - 1);
+      const bool before_end = VEC == kAligned ? (i < S - 1 ? t0 < T : t0 + S < T) : (t < T - 1);
       const float c_next = before_end ? ((i + 1 < S) ? R.c[i + 1] : h.a) : 0.f;
       const float done = fminf(R.te[i] + R.tr[i], 1.f);
       const float a = fmaf(gamma * R.enq[i], 1.f - R.te[i], R.r[i]) - R.q[i];
-      const bool in = VEC ? t0 < T : t < T;  // vector segments are all-in or all-out
+      const bool in = step_in<VEC>(t0, t, T);  // vector segments are all-in or all-out
       m[i].add = in ? a : 0.f;
       m[i].mul = in ? gamma * c_next * (1.f - done) : 1.f;
     }
   }
   __device__ const E* row_carry_src(int64_t, int) const { return nullptr; }
 
-  template <int S, bool VEC, int SP = 0>
+  template <int S, int VEC, int SP = 0>
   __device__ void emit(const Regs<S>& R, Halo2 h, const float (&xs)[S], float x_next, int64_t row,
                        int t0, int T) const {
     float tg[S], ad[S];
@@ -510,7 +513,7 @@ struct RetraceOp {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
-      const bool before_end = VEC ? (i < S - 1 ? t0 < T : t0 + S < T) : (t < T - 1);
+      const bool before_end = VEC == kAligned ? (i < S - 1 ? t0 < T : t0 + S < T) : (t < T - 1);
       const float nxt = before_end ? ((i + 1 < S) ? tg[i + 1] : x_next + h.b) : 0.f;
       ad[i] = R.rho[i] * (fmaf(gamma * nxt, 1.f - R.te[i], R.r[i]) - R.q[i]);
     }
@@ -554,7 +557,7 @@ struct ReturnsOp {
     float blast;
   };
 
-  template <int S, bool VEC>
+  template <int S, int VEC>
   __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
     const int64_t o = row * (int64_t)T;
     load_seg<S, VEC>(r + o, t0, T, R.r);
@@ -569,12 +572,12 @@ struct ReturnsOp {
       R.blast = 0.f;
     }
   }
-  template <int S, bool VEC>
+  template <int S, int VEC>
   __device__ void prepare(Regs<S>& R, int64_t, int t0, int T) const {
     if constexpr (TRUNC) boot_prepare<S, true>(boot_mode, t0, T, R.bt, R.blast);
   }
 
-  template <int S, bool VEC = false>
+  template <int S, int VEC = kElementAligned>
   __device__ void coef(const Regs<S>& R, NoHalo, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
@@ -582,7 +585,7 @@ struct ReturnsOp {
       const float nd = 1.f - (TRUNC ? fminf(R.te[i] + R.tr[i], 1.f) : R.te[i]);
       float a = NV ? fmaf(g1l * nd, R.nv[i], R.r[i]) : R.r[i];
       if constexpr (TRUNC) a = fmaf(gamma * R.tr[i], R.bt[i], a);
-      const bool in = VEC ? t0 < T : t < T;  // vector segments are all-in or all-out
+      const bool in = step_in<VEC>(t0, t, T);  // vector segments are all-in or all-out
       m[i].add = in ? a : 0.f;
       m[i].mul = in ? gl * nd : 1.f;
     }
@@ -591,7 +594,7 @@ struct ReturnsOp {
     return boot_mode == kBootNone ? nullptr : boot_last(boot, boot_mode, row, T);
   }
 
-  template <int S, bool VEC, int SP = 0>
+  template <int S, int VEC, int SP = 0>
   __device__ void emit(const Regs<S>&, NoHalo, const float (&xs)[S], float, int64_t row, int t0,
                        int T) const {
     store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, SP != 0);
@@ -627,34 +630,40 @@ struct DoneGatedForwardOp {
     float x[S], d[S];
   };
 
-  template <int S, bool VEC>
+  template <int S, int VEC>
   __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
     const int64_t o = row * (int64_t)T;
     load_seg<S, VEC>(x + o, t0, T, R.x);
     load_seg<S, VEC>(dones + o, t0, T, R.d);
   }
-  template <int S, bool VEC>
+  template <int S, int VEC>
   __device__ void prepare(Regs<S>&, int64_t, int, int) const {}
   template <int S>
   __device__ float export_last(const Regs<S>& R) const { return R.d[S - 1]; }
   __device__ float halo_load(int64_t row, int t, int T) const { return to_f32(dones[row * (int64_t)T + t]); }
 
-  template <int S, bool VEC = false>
+  template <int S, int VEC = kElementAligned>
   __device__ void coef(const Regs<S>& R, float dh, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       const int t = t0 + i;
       float gate;
-      if (ends_at) gate = (i > 0) ? R.d[i - 1] : (t == 0 ? 0.f : dh);
-      else gate = R.d[i];
-      const bool in = VEC ? t0 < T : t < T;  // vector segments are all-in or all-out
+      if (ends_at) {
+        // kPhased segments can hold step 0 past their first position, after steps of the
+        // row before (done[-1] = 0 all the same)
+        if constexpr (VEC == kPhased) gate = t == 0 ? 0.f : (i > 0 ? R.d[i - 1] : dh);
+        else gate = (i > 0) ? R.d[i - 1] : (t == 0 ? 0.f : dh);
+      } else {
+        gate = R.d[i];
+      }
+      const bool in = step_in<VEC>(t0, t, T);  // vector segments are all-in or all-out
       m[i].mul = in ? decay * (1.f - gate) : 1.f;
       m[i].add = in ? R.x[i] : 0.f;
     }
   }
   __device__ const E* row_carry_src(int64_t row, int) const { return seed ? seed + row : nullptr; }
 
-  template <int S, bool VEC, int SP = 0>
+  template <int S, int VEC, int SP = 0>
   __device__ void emit(const Regs<S>&, float, const float (&xs)[S], float, int64_t row, int t0,
                        int T) const {
     store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, SP != 0);
@@ -683,25 +692,25 @@ struct AffineScanOp {
   struct Regs {
     float u[S], v[S];
   };
-  template <int S, bool VEC>
+  template <int S, int VEC>
   __device__ void load(int64_t row, int t0, int T, Regs<S>& R) const {
     const int64_t o = row * (int64_t)T;
     load_seg<S, VEC>(u + o, t0, T, R.u);
     load_seg<S, VEC>(v + o, t0, T, R.v);
   }
-  template <int S, bool VEC>
+  template <int S, int VEC>
   __device__ void prepare(Regs<S>&, int64_t, int, int) const {}
-  template <int S, bool VEC = false>
+  template <int S, int VEC = kElementAligned>
   __device__ void coef(const Regs<S>& R, NoHalo, int64_t, int t0, int T, Affine (&m)[S]) const {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
-      const bool in = VEC ? t0 < T : t0 + i < T;
+      const bool in = step_in<VEC>(t0, t0 + i, T);
       m[i].mul = in ? R.v[i] : 1.f;
       m[i].add = in ? R.u[i] : 0.f;
     }
   }
   __device__ const E* row_carry_src(int64_t row, int) const { return carry ? carry + row : nullptr; }
-  template <int S, bool VEC, int SP = 0>
+  template <int S, int VEC, int SP = 0>
   __device__ void emit(const Regs<S>&, NoHalo, const float (&xs)[S], float, int64_t row, int t0,
                        int T) const {
     store_seg<S, VEC>(out + row * (int64_t)T, t0, T, xs, SP != 0);

@@ -88,6 +88,10 @@ def test_host_only_entry_points():
     b = lib.rlk_workspace_bytes(16, 1 << 20)
     assert 0 < a < b and a % 8 == 0
     assert lib.rlk_workspace_bytes(0, 1 << 20) == 0
+    # 80 B per 4096-step tile of every row, whatever the row's alignment
+    w = lib.rlk_workspace_bytes
+    assert w(1, 8192) == w(1, 4097) == w(1, 8189) and w(1, 8193) - w(1, 8192) == 80
+    assert w(3, 8191) == w(3, 8192) and w(3, 8193) - w(3, 8192) == 240
 
 
 def test_entry_points_reject_bad_arguments_without_launching():
