@@ -192,7 +192,7 @@ hipError_t launch_rows(const Op& op, int64_t E, int T, hipStream_t stream) {
   void* args[] = {const_cast<Op*>(&op), &E, &T, &log2L};
   // 4-step rows of 33..2048 steps: the instance whose scan width is fixed
   const void* k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC, 0, SP>);
-  if constexpr (S == 4 && VEC && NT == kNTWide && paired_rows<Op>::value) {
+  if constexpr (S == 4 && VEC == kAligned && NT == kNTWide && paired_rows<Op>::value) {
     if (log2L == 5) {
       k = reinterpret_cast<const void*>(&rows_pair_kernel<Op, NT / 2, 32, SP>);
       return hipLaunchKernel(k, dim3((unsigned)grid), dim3(NT / 2), args, 0, stream);
