@@ -17,8 +17,12 @@
  *     default stream).  Nothing allocates and nothing synchronises.
  *   - Any element-aligned pointers are accepted.  The fastest form is seq_len % 4 == 0
  *     with every [num_envs, seq_len] array 16-byte aligned (bfloat16: 8-byte), which
- *     the kernels read and write with aligned non-temporal 16-byte accesses; otherwise
- *     they use element-aligned 16-byte accesses (about 15% slower).
+ *     the kernels read and write with aligned non-temporal 16-byte accesses.  Rows longer
+ *     than 2048 steps of seq_len % 4 != 0 whose arrays all start at the same element
+ *     offset modulo 4 (freshly allocated arrays do) are shifted to their own 16-byte
+ *     boundaries and keep aligned accesses (within ~5% of the aligned form); Retrace and
+ *     the normalised GAE entries excepted.  Other calls use element-aligned 16-byte
+ *     accesses (about 10-20% slower).
  *   - Bootstrap mode: RLK_BOOT_NONE (bootstrap == NULL, value 0), RLK_BOOT_ROW
  *     (bootstrap is [num_envs]: the continuation value after step seq_len-1, the
  *     reference's `last_value`), RLK_BOOT_FULL (bootstrap is [num_envs, seq_len], the
