@@ -100,6 +100,16 @@ size_t rlk_workspace_bytes(int64_t num_envs, int64_t seq_len);
  * there.  The fallback paths give the same bits as the ordinary one.  Returns RLK_OK. */
 int rlk_debug_lookback(int give_up_polls, int fallback_polls);
 
+/* For tests of the output stores only; no counterpart in the reference.  The kernels store
+ * their outputs non-temporally or write-through, chosen per launch by the call's shape and
+ * storage type (a speed choice; the bits stored are the same).  policy 0 or 1 forces
+ * non-temporal or write-through stores, process-wide, for the calls launched after it,
+ * wherever the launch is built with that policy (bfloat16 outputs and the 1025..2048-step
+ * strided rows are write-through only; float32 V-trace and Retrace long rows non-temporal
+ * only); -1 restores the rule.  Returns RLK_OK, or RLK_ERR_INVALID_ARGUMENT for another
+ * value. */
+int rlk_debug_store_policy(int policy);
+
 /* GAE advantages.  Replaces the gae_fused_kernel launch in compute_gae
  * (src/rl_triton/ops/gae.py:164-190; kernel src/rl_triton/kernels/gae.py:62-180), and
  * its chunked fallback for seq_len > 131072 (ops/gae.py:192-215).

@@ -349,12 +349,18 @@ int store_write_through(int64_t E, int64_t T) {
   const int64_t out_bytes = E * T * (int64_t)sizeof(float) * n_outputs<Op>::value;
   return (((T + 3) / 4 > kWave && out_bytes >= (int64_t{1} << 20)) || out_bytes >= (int64_t{12} << 20)) ? 1 : 0;
 }
+// rlk_debug_store_policy: -1 the rule above, 0 / 1 non-temporal / write-through wherever
+// the launch has an instance of that policy.
+std::atomic<int> g_store_policy{-1};
+
 // Calls f(std::integral_constant<int, SP>) with SP the launch's store policy.
 template <class Op, Kernel K, class F>
 hipError_t dispatch_store_policy(int64_t E, int64_t T, F&& f) {
   using P = store_policies<Op, K>;
   if constexpr (P::kWriteThrough && P::kNonTemporal) {
-    if (store_write_through<Op, K>(E, T)) return f(std::integral_constant<int, 1>{});
+    const int forced = g_store_policy.load(std::memory_order_relaxed);
+    if (forced >= 0 ? forced == 1 : store_write_through<Op, K>(E, T) != 0)
+      return f(std::integral_constant<int, 1>{});
     return f(std::integral_constant<int, 0>{});
   } else {
     return f(std::integral_constant<int, P::kWriteThrough ? 1 : 0>{});
@@ -822,6 +828,12 @@ size_t rlk_workspace_bytes(int64_t num_envs, int64_t seq_len) {
 int rlk_debug_lookback(int give_up_polls, int fallback_polls) {
   g_spin_limit.store(give_up_polls < 0 ? kSpinLimit : give_up_polls, std::memory_order_relaxed);
   g_fallback_polls.store(fallback_polls < 0 ? kFallbackPolls : fallback_polls, std::memory_order_relaxed);
+  return RLK_OK;
+}
+
+int rlk_debug_store_policy(int policy) {
+  if (policy < -1 || policy > 1) return RLK_ERR_INVALID_ARGUMENT;
+  g_store_policy.store(policy, std::memory_order_relaxed);
   return RLK_OK;
 }
 

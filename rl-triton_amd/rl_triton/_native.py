@@ -52,6 +52,7 @@ SIGNATURES = {
     "rlk_status_string": [_INT],
     "rlk_version": [],
     "rlk_debug_lookback": [_INT, _INT],
+    "rlk_debug_store_policy": [_INT],
 }
 # the bfloat16 twins take the same arguments (rlk_bf16 arrays in place of float ones)
 for _name in ("rlk_gae", "rlk_gae_masked", "rlk_gae_normalized", "rlk_gae_normalized_masked", "rlk_vtrace", "rlk_retrace", "rlk_lambda_returns",
