@@ -6,9 +6,10 @@ overwritten with new data and other eager work (uncaptured calls of the same op,
 runs on the default stream; every replay's outputs must equal, bit for bit, an eager call on
 the same inputs, and match the float64 oracle on those inputs at the suite's tolerances
 (rtol = atol = 1e-5 up to 2048 steps, the horizon-scaled atol beyond; normalised advantages
-with that tolerance divided by the batch std).  Rows longer than 2048 steps use the look-back workspace: both the
-documented order (a warm-up call on the capture stream creates it before capture) and a
-first call inside the capture are covered.
+with that tolerance divided by the batch std).  Rows longer than 2048 steps use the
+look-back workspace: both the documented order (a warm-up call on the capture stream
+creates it before capture) and a first call inside the capture are covered.  [3,5001]
+takes the phased access of long rows whose length is not a multiple of four.
 """
 import pytest
 import torch
@@ -103,7 +104,8 @@ def _against_oracle(op, inp, params, outs, T, what):
 
 @pytest.mark.parametrize("warm", [True, False], ids=["warmed", "first-call-in-capture"])
 @pytest.mark.parametrize("op", OPS)
-@pytest.mark.parametrize("shape", [(64, 512), (16, 2048), (3, 5000)], ids=lambda s: f"{s[0]}x{s[1]}")
+@pytest.mark.parametrize("shape", [(64, 512), (16, 2048), (3, 5000), (3, 5001)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
 def test_graph_replays_match_eager(op, shape, warm, device, monkeypatch):
     monkeypatch.delenv("RL_TRITON_CORRECTNESS_WARNINGS")  # host-side scans cannot be captured
     inp, params = _inputs(op, shape, seed=41)
