@@ -228,7 +228,7 @@ hipError_t launch_strided(const Op& op, int64_t E, int T, hipStream_t stream) {
   if (E > 0x7fffffffLL) return hipErrorInvalidValue;
   int unused = 0;
   void* args[] = {const_cast<Op*>(&op), &E, &T, &unused};
-  return hipLaunchKernel(reinterpret_cast<const void*>(&rows_strided_kernel<Op, kStridedThreads, kStridedSegments, true, SP>),
+  return hipLaunchKernel(reinterpret_cast<const void*>(&rows_strided_kernel<Op, kStridedThreads, kStridedSegments, kAligned, SP>),
                          dim3((unsigned)E), dim3(kStridedThreads), args, 0, stream);
 }
 
@@ -409,11 +409,12 @@ int launch(const Op& op, int64_t E, int64_t T, bool vec, void* workspace, size_t
   } else {
     e = dispatch_store_policy<Op, Kernel::kRows>(E, T, [&](auto sp) {
       constexpr int SP = decltype(sp)::value;
-      if (rows_seg(T) == 1) return launch_rows<Op, kNT, 1, false, SP>(op, E, Ti, s);
+      if (rows_seg(T) == 1) return launch_rows<Op, kNT, 1, kElementAligned, SP>(op, E, Ti, s);
       if (rows_threads(E, T) == kNT)
-        return vec ? launch_rows<Op, kNT, 4, true, SP>(op, E, Ti, s) : launch_rows<Op, kNT, 4, false, SP>(op, E, Ti, s);
-      return vec ? launch_rows<Op, kNTWide, 4, true, SP>(op, E, Ti, s)
-                 : launch_rows<Op, kNTWide, 4, false, SP>(op, E, Ti, s);
+        return vec ? launch_rows<Op, kNT, 4, kAligned, SP>(op, E, Ti, s)
+                   : launch_rows<Op, kNT, 4, kElementAligned, SP>(op, E, Ti, s);
+      return vec ? launch_rows<Op, kNTWide, 4, kAligned, SP>(op, E, Ti, s)
+                 : launch_rows<Op, kNTWide, 4, kElementAligned, SP>(op, E, Ti, s);
     });
   }
   return e == hipSuccess ? RLK_OK : RLK_ERR_LAUNCH;

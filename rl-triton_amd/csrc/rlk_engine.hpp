@@ -830,7 +830,7 @@ __global__ __launch_bounds__(NT) void rows_pair_kernel(const Op op, int64_t E, i
     const int64_t row_id = ((int64_t)blockIdx.x * RPT + u) * (NT >> log2L) + (tid >> log2L);
     active[u] = row_id < E;
     row[u] = active[u] ? row_id : E - 1;  // idle lanes of the last workgroup read a real row
-    op.template load<S, true>(row[u], t0, T, R[u]);
+    op.template load<S, kAligned>(row[u], t0, T, R[u]);
   }
   Halo edge{};
   if constexpr (HAS_HALO) {
@@ -840,7 +840,7 @@ __global__ __launch_bounds__(NT) void rows_pair_kernel(const Op op, int64_t E, i
 #pragma unroll
   for (int u = 0; u < RPT; ++u) {
     carry[u] = row_carry(op, row[u], T);
-    op.template prepare<S, true>(R[u], row[u], t0, T);
+    op.template prepare<S, kAligned>(R[u], row[u], t0, T);
   }
   Halo h[RPT];
   Map steps[RPT][S];
@@ -851,7 +851,7 @@ __global__ __launch_bounds__(NT) void rows_pair_kernel(const Op op, int64_t E, i
       h[u] = lane_prev(scan_export<Op, S>(op, R[u]));
       if (lane == 0) h[u] = edge;  // unused: the row's first segment in scan order
     }
-    op.template coef<S, true>(R[u], h[u], row[u], t0, T, steps[u]);
+    op.template coef<S, kAligned>(R[u], h[u], row[u], t0, T, steps[u]);
     m[u] = lane_scan(fold_segment<FWD, S>(steps[u]), WT);
   }
 #pragma unroll
@@ -861,7 +861,7 @@ __global__ __launch_bounds__(NT) void rows_pair_kernel(const Op op, int64_t E, i
     if (li == 0) x_in = carry[u];
     State xs[S];
     replay<FWD, S>(steps[u], x_in, xs);
-    if (active[u]) op.template emit<S, true, SP>(R[u], h[u], xs, x_in, row[u], t0, T);
+    if (active[u]) op.template emit<S, kAligned, SP>(R[u], h[u], xs, x_in, row[u], t0, T);
   }
 }
 
