@@ -508,13 +508,34 @@ int gae_masked_impl(const E* rewards, const E* values, const E* terminateds, con
   return launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream, ph);
 }
 
-// Partials of compute_gae_normalized: kStatWords doubles per workgroup of the first launch,
-// for the larger of the two ops' grids (the masked op uses narrower long-row tiles).
+// First launches of more workgroups than this have their partials summed by a tree of
+// reduce_partials_kernel levels (kReduceSlice triples into one per level) until at most
+// this many remain, which normalize_kernel's workgroups then each read.  The crossover,
+// measured on MI355X (float32, µs per call): 2048 triples read directly 24.1, through one
+// level 24.7 ([32768,128]); 4096 triples 44.9 directly, 42.5 through a level ([65536,128]).
+// Against every normalising workgroup reading every triple, the tree takes [2^20,128]
+// (65536 triples) from 761 to 630 µs and [16384,2048] from 167 to 139 µs.
+constexpr int64_t kDirectParts = 2048;
+
+// Triples of the partials buffer for a first launch of `nparts` workgroups: its own, then
+// each tree level's.
+int64_t partials_triples(int64_t nparts) {
+  int64_t total = nparts;
+  for (int64_t n = nparts; n > kDirectParts;) {
+    n = (n + kReduceSlice - 1) / kReduceSlice;
+    total += n;
+  }
+  return total;
+}
+
+// Partials of compute_gae_normalized: kStatWords doubles per workgroup of the first launch
+// and per tree level, for the larger of the two ops' grids (the masked op uses narrower
+// long-row tiles).
 size_t gae_normalized_partials(int64_t num_envs, int64_t seq_len) {
   if (num_envs <= 0 || seq_len <= 0) return 0;
   const int64_t a = launch_grid<GaeStatsOp<true>>(num_envs, seq_len);
   const int64_t b = launch_grid<MaskedGaeStatsOp<true>>(num_envs, seq_len);
-  return (size_t)(a > b ? a : b) * kStatWords * sizeof(double);
+  return (size_t)partials_triples(a > b ? a : b) * kStatWords * sizeof(double);
 }
 
 // The two launches of a normalised GAE: `op` (GaeStatsOp or MaskedGaeStatsOp, partials not
@@ -528,14 +549,26 @@ int normalized_launch(StatsOp op, E* advantages, int64_t num_envs, int64_t seq_l
   double* parts = reinterpret_cast<double*>(partials);
   const int64_t nparts = launch_grid<StatsOp>(num_envs, seq_len);
   if (parts == nullptr || (reinterpret_cast<uintptr_t>(parts) & 7u) != 0 ||
-      partials_bytes < (size_t)nparts * kStatWords * sizeof(double) || nparts > 0x7fffffffLL)
+      partials_bytes < (size_t)partials_triples(nparts) * kStatWords * sizeof(double) ||
+      nparts > 0x7fffffffLL)
     return RLK_ERR_WORKSPACE;
   op.partials = parts;
   const int st = launch(op, num_envs, seq_len, vec, workspace, workspace_bytes, stream);
   if (st != RLK_OK) return st;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int np = (int)nparts;
+  while (np > kDirectParts) {
+    const int next = (np + kReduceSlice - 1) / kReduceSlice;
+    double* up = parts + kStatWords * (int64_t)np;
+    void* rargs[] = {&parts, &np, &up};
+    if (hipLaunchKernel(reinterpret_cast<const void*>(&reduce_partials_kernel<kReduceNT>),
+                        dim3((unsigned)next), dim3(kReduceNT), rargs, 0, s) != hipSuccess)
+      return RLK_ERR_LAUNCH;
+    parts = up;
+    np = next;
+  }
   constexpr int kNormNT = 256;
   int64_t n = num_envs * seq_len;
-  int np = (int)nparts;
   const bool nvec = n % 4 == 0 && quad_aligned(advantages);
   const int64_t units = nvec ? n / 4 : n;
   int64_t grid = (units + kNormNT - 1) / kNormNT;
@@ -543,8 +576,7 @@ int normalized_launch(StatsOp op, E* advantages, int64_t num_envs, int64_t seq_l
   void* args[] = {&advantages, &parts, &np, &n, &eps};
   const void* kernel = nvec ? reinterpret_cast<const void*>(&normalize_kernel<kNormNT, true, E>)
                             : reinterpret_cast<const void*>(&normalize_kernel<kNormNT, false, E>);
-  const hipError_t e = hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(kNormNT), args, 0,
-                                       reinterpret_cast<hipStream_t>(stream));
+  const hipError_t e = hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(kNormNT), args, 0, s);
   return e == hipSuccess ? RLK_OK : RLK_ERR_LAUNCH;
 }
 

@@ -127,8 +127,14 @@ def test_entry_points_reject_bad_arguments_without_launching():
                 args[i] = 0
         assert getattr(lib, name)(*args) == 0, name
     # a normalised call's partials must hold three float64 per workgroup of the first launch
+    # (512-thread workgroups of 16 rows at T = 128, 4 at T = 300, 256 one-step rows), then,
+    # above 2048 of them, one per 2048 for each level of the tree that sums them
     need = lib.rlk_gae_normalized_partials_bytes(4096, 128)
-    assert need > 0 and need % 24 == 0
+    assert need == 256 * 24
+    p = lib.rlk_gae_normalized_partials_bytes
+    assert p(8192, 300) == 2048 * 24 and p(8193, 300) == (2049 + 2) * 24
+    assert p(65536, 128) == (4096 + 2) * 24
+    assert p(4096 * 524291, 1) == (8388656 + 4097 + 3) * 24
     assert lib.rlk_gae_normalized(fake, fake, fake, None, None, 0, fake, fake, 4096, 128, 0.99,
                                   0.95, 1e-8, None, 0, fake, need - 8, None) == -2
 

@@ -153,9 +153,10 @@ def test_bf16_drift_against_float64(op, shape, device):
         assert err <= bound, f"{op}{shape}:{name}: max abs err {err:.3e} > bound {bound:.3e}"
 
 
-@pytest.mark.parametrize("shape", [(2, 3), (33, 257), (4096, 128), (3, 5000)],
+@pytest.mark.parametrize("shape", [(2, 3), (33, 257), (4096, 128), (3, 5000), (8193, 300)],
                          ids=lambda s: f"{s[0]}x{s[1]}")
 def test_bf16_gae_normalized(shape, device):
+    # [8193, 300]: 2049 workgroups' partials, summed by a tree level before the normalisation
     inp, params = make_inputs("gae_normalized", *shape, seed=9, p_trunc=0.02, boot="full")
     inp = _bf16_values(inp)
     params = dict(params, eps=1e-8)

@@ -9,7 +9,8 @@ the same inputs, and match the float64 oracle on those inputs at the suite's tol
 with that tolerance divided by the batch std).  Rows longer than 2048 steps use the
 look-back workspace: both the documented order (a warm-up call on the capture stream
 creates it before capture) and a first call inside the capture are covered.  [3,5001]
-takes the phased access of long rows whose length is not a multiple of four.
+takes the phased access of long rows whose length is not a multiple of four; [8193,300] the
+tree that sums a normalised call's partials.
 """
 import pytest
 import torch
@@ -138,3 +139,10 @@ def test_graph_replays_match_eager(op, shape, warm, device, monkeypatch):
             assert _same(o, w), f"{op}{shape} replay {rep}: differs from the eager call"
         _against_oracle(op, new, params, outs, shape[1], f"{op}{shape} replay {rep}")
     del graph
+
+
+@pytest.mark.parametrize("op", ["gae_normalized", "gae_normalized_masked"])
+def test_graph_replays_with_a_partials_tree(op, device, monkeypatch):
+    """[8193, 300]: 2049 workgroups in the statistics launch, so the captured call holds a
+    level of the partials' tree (reduce_partials_kernel) between it and the normalisation."""
+    test_graph_replays_match_eager(op, (8193, 300), True, device, monkeypatch)
