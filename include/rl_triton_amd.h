@@ -41,6 +41,13 @@
  *     look-back wait gave up or the counters were not at rest (results of that call are
  *     invalid); [8..2055] 64 slots (start counter and epoch of a slot of rows); then two
  *     places of up to five status words per tile.
+ *   - Sizes: num_envs up to what device memory holds, seq_len up to 2^30.  HIP launches at
+ *     most 2^32 - 1 work-items per grid dimension; a call whose launch would need more
+ *     (from about 3.2 billion steps of 3-step rows, or about 4.2 million rows of 2049
+ *     steps) is issued as launches over consecutive row ranges, in row order on `stream`.
+ *     Rows are independent, so only the number of launches changes (the normalised GAE's
+ *     statistics cover all of them).  The reference's Triton kernels compute a row's
+ *     offset as program_id * stride in 32-bit integers (src/rl_triton/kernels/gae.py:38-39).
  *   - Return value: RLK_OK or a negative RLK_ERR_* code; rlk_status_string() names it.
  *     Empty inputs (num_envs == 0 or seq_len == 0) return RLK_OK without a launch.
  *   - bfloat16 I/O: every estimator has an `_bf16` twin whose float arrays (inputs,

@@ -188,7 +188,7 @@ template <class Op, int NT, int S, int VEC, int SP>
 hipError_t launch_rows(const Op& op, int64_t E, int T, hipStream_t stream) {
   int log2L = ceil_log2((T + S - 1) / S);
   const int64_t grid = rows_grid(E, T, S, NT);
-  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  if (grid * NT > 0xffffffffLL) return hipErrorInvalidValue;  // launch() splits such calls
   void* args[] = {const_cast<Op*>(&op), &E, &T, &log2L};
   // 4-step rows of 33..2048 steps: the instance whose scan width is fixed
   const void* k = reinterpret_cast<const void*>(&rows_kernel<Op, NT, S, VEC, 0, SP>);
@@ -225,7 +225,7 @@ struct strided_rows<RetraceOp<NA, TRUNC, E>> : std::false_type {};
 template <class Op, int SP>
 hipError_t launch_strided(const Op& op, int64_t E, int T, hipStream_t stream) {
   static_assert(kStridedThreads * kSeg * kStridedSegments == kShortMaxT, "one row per workgroup");
-  if (E > 0x7fffffffLL) return hipErrorInvalidValue;
+  if (E * kStridedThreads > 0xffffffffLL) return hipErrorInvalidValue;  // launch() splits such calls
   int unused = 0;
   void* args[] = {const_cast<Op*>(&op), &E, &T, &unused};
   return hipLaunchKernel(reinterpret_cast<const void*>(&rows_strided_kernel<Op, kStridedThreads, kStridedSegments, kAligned, SP>),
@@ -262,7 +262,7 @@ hipError_t launch_chain(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_
   constexpr int64_t tile = (int64_t)NT * kSeg * Q;
   int tpr = (int)((T + tile - 1) / tile);
   const int64_t grid = chain_grid(E, T, NT, Q);
-  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  if (grid * NT > 0xffffffffLL) return hipErrorInvalidValue;  // launch() splits such calls
   uint64_t* fb = ws + kStatusOffset + kStatusWords * status_tiles(E, T);
   int spin_limit = g_spin_limit.load(std::memory_order_relaxed);
   int fallback_polls = g_fallback_polls.load(std::memory_order_relaxed);
@@ -379,6 +379,113 @@ struct phased_rows<GaeStatsOp<TRUNC, E>> : std::false_type {};
 template <bool TRUNC, class E>
 struct phased_rows<MaskedGaeStatsOp<TRUNC, E>> : std::false_type {};
 
+// ---------------------------------------------------------------------------------------
+// Calls beyond one launch.  HIP launches at most 2^32 - 1 work-items per grid dimension
+// (hip_runtime_api.h, hipLaunchKernel), and every launch here is one-dimensional with at
+// most 1024 threads per workgroup.  Rows are independent, so a call whose launch would
+// need more than kMaxLaunchBlocks workgroups runs as calls over consecutive row ranges,
+// in row order on the same stream, each within the limit.  It takes ~3.2 billion steps of
+// short rows (~13 GB per float32 array at 3 steps per row), or ~4.2 million long rows of
+// one tile each: sizes MI355X's 288 GB holds.
+// ---------------------------------------------------------------------------------------
+constexpr int64_t kMaxLaunchBlocks = ((int64_t{1} << 32) - 1) / 1024;
+
+template <class P>
+void skip(P*& p, int64_t n) {
+  if (p != nullptr) p += n;
+}
+// boot: one value per row (RLK_BOOT_ROW) or [E, T] (RLK_BOOT_FULL)
+template <class E>
+void skip_boot(const E*& boot, int boot_mode, int64_t r0, int64_t T) {
+  skip(boot, boot_mode == RLK_BOOT_FULL ? r0 * T : r0);
+}
+
+// An op's arrays advanced by r0 rows: [E, T] arrays by r0 * T elements, [E, T, A] ones by
+// r0 * T * A, per-row ones by r0.  (The statistics ops' partials are placed by the caller.)
+template <bool TR, class E>
+void skip_rows(GaeOp<TR, E>& op, int64_t r0, int64_t T) {
+  const int64_t n = r0 * T;
+  skip(op.r, n), skip(op.v, n), skip(op.term, n), skip(op.trunc, n), skip(op.out, n);
+  skip_boot(op.boot, op.boot_mode, r0, T);
+}
+template <bool TR, class E>
+void skip_rows(GaeStatsOp<TR, E>& op, int64_t r0, int64_t T) {
+  skip_rows(static_cast<GaeOp<TR, E>&>(op), r0, T);
+  skip(op.returns, r0 * T);
+}
+template <bool TR, class E>
+void skip_rows(MaskedGaeOp<TR, E>& op, int64_t r0, int64_t T) {
+  const int64_t n = r0 * T;
+  skip(op.r, n), skip(op.v, n), skip(op.term, n), skip(op.trunc, n), skip(op.mask, n);
+  skip(op.out, n);
+  skip_boot(op.boot, op.boot_mode, r0, T);
+}
+template <bool TR, class E>
+void skip_rows(MaskedGaeStatsOp<TR, E>& op, int64_t r0, int64_t T) {
+  skip_rows(static_cast<MaskedGaeOp<TR, E>&>(op), r0, T);
+  skip(op.returns, r0 * T);
+}
+template <bool TR, class E>
+void skip_rows(VtraceOp<TR, E>& op, int64_t r0, int64_t T) {
+  const int64_t n = r0 * T;
+  skip(op.lpt, n), skip(op.lpb, n), skip(op.v, n), skip(op.r, n), skip(op.term, n);
+  skip(op.trunc, n), skip(op.targets, n), skip(op.adv, n);
+  skip_boot(op.boot, op.boot_mode, r0, T);
+}
+template <int NA, bool TR, class E>
+void skip_rows(RetraceOp<NA, TR, E>& op, int64_t r0, int64_t T) {
+  const int64_t n = r0 * T;
+  skip(op.pi, n * op.A), skip(op.nq, n * op.A);
+  skip(op.mu, n), skip(op.q, n), skip(op.act, n), skip(op.r, n), skip(op.term, n);
+  skip(op.trunc, n), skip(op.targets, n), skip(op.adv, n);
+}
+template <bool NV, bool TR, class E>
+void skip_rows(ReturnsOp<NV, TR, E>& op, int64_t r0, int64_t T) {
+  const int64_t n = r0 * T;
+  skip(op.r, n), skip(op.nv, n), skip(op.term, n), skip(op.trunc, n), skip(op.out, n);
+  skip_boot(op.boot, op.boot_mode, r0, T);
+}
+template <class E>
+void skip_rows(DoneGatedForwardOp<E>& op, int64_t r0, int64_t T) {
+  const int64_t n = r0 * T;
+  skip(op.x, n), skip(op.dones, n), skip(op.out, n), skip(op.seed, r0);
+}
+template <bool FWD, class E>
+void skip_rows(AffineScanOp<FWD, E>& op, int64_t r0, int64_t T) {
+  const int64_t n = r0 * T;
+  skip(op.u, n), skip(op.v, n), skip(op.out, n), skip(op.carry, r0);
+}
+
+// Rows per launch of a call: all E when one launch holds the call, else the most rows
+// (a multiple of 512 where that is at least 512: whole workgroups of every short-row shape)
+// whose launch stays within kMaxLaunchBlocks.
+template <class Op>
+int64_t rows_per_launch(int64_t E, int64_t T) {
+  const int64_t g = launch_grid<Op>(E, T);
+  if (g <= kMaxLaunchBlocks) return E;
+  int64_t n = (int64_t)((double)E * (double)kMaxLaunchBlocks / (double)g);  // grid ~ rows
+  n = n < 1 ? 1 : n > E ? E : n;
+  for (const int64_t unit : {int64_t{512}, int64_t{1}}) {
+    if (n < unit) continue;
+    int64_t m = n / unit * unit;
+    while (m > unit && launch_grid<Op>(m, T) > kMaxLaunchBlocks) m -= unit;
+    if (launch_grid<Op>(m, T) <= kMaxLaunchBlocks) return m;
+  }
+  return 1;  // one row of at most 2^30 steps is at most 2^18 tiles
+}
+
+// Workgroups of all the launches of a call, following launch()'s row ranges: the
+// statistics ops write one partial per workgroup.
+template <class Op>
+int64_t call_blocks(int64_t E, int64_t T) {
+  if (E <= 0 || T <= 0) return 0;
+  const int64_t rows = rows_per_launch<Op>(E, T);
+  if (rows >= E) return launch_grid<Op>(E, T);
+  int64_t total = 0;
+  for (int64_t r0 = 0; r0 < E; r0 += rows) total += call_blocks<Op>(rows < E - r0 ? rows : E - r0, T);
+  return total;
+}
+
 // vec: kAligned access.  phase0 >= 0: the element phase every [E, T] array of the call
 // shares at row 0 (common_phase), for the phased access of long rows when T % 4 != 0.
 template <class Op>
@@ -386,6 +493,21 @@ int launch(const Op& op, int64_t E, int64_t T, bool vec, void* workspace, size_t
            void* stream, int phase0 = -1) {
   if (E < 0 || T < 0 || T > (int64_t{1} << 30)) return RLK_ERR_INVALID_ARGUMENT;
   if (E == 0 || T == 0) return RLK_OK;
+  const int64_t rows = rows_per_launch<Op>(E, T);
+  if (rows < E) {
+    int64_t blocks = 0;  // the statistics ops' partials of the ranges before this one
+    for (int64_t r0 = 0; r0 < E; r0 += rows) {
+      const int64_t n = rows < E - r0 ? rows : E - r0;
+      Op part = op;
+      skip_rows(part, r0, T);
+      if constexpr (Op::kBlockStats) part.partials = op.partials + kStatWords * blocks;
+      const int ph = phase0 < 0 ? -1 : (int)((phase0 + (r0 & 3) * (T & 3)) & 3);
+      const int st = launch(part, n, T, vec, workspace, workspace_bytes_given, stream, ph);
+      if (st != RLK_OK) return st;
+      blocks += call_blocks<Op>(n, T);
+    }
+    return RLK_OK;
+  }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int Ti = (int)T;
   hipError_t e;
@@ -533,8 +655,8 @@ int64_t partials_triples(int64_t nparts) {
 // long-row tiles).
 size_t gae_normalized_partials(int64_t num_envs, int64_t seq_len) {
   if (num_envs <= 0 || seq_len <= 0) return 0;
-  const int64_t a = launch_grid<GaeStatsOp<true>>(num_envs, seq_len);
-  const int64_t b = launch_grid<MaskedGaeStatsOp<true>>(num_envs, seq_len);
+  const int64_t a = call_blocks<GaeStatsOp<true>>(num_envs, seq_len);
+  const int64_t b = call_blocks<MaskedGaeStatsOp<true>>(num_envs, seq_len);
   return (size_t)partials_triples(a > b ? a : b) * kStatWords * sizeof(double);
 }
 
@@ -547,7 +669,7 @@ int normalized_launch(StatsOp op, E* advantages, int64_t num_envs, int64_t seq_l
                       size_t partials_bytes, void* stream) {
   if (num_envs < 0 || seq_len < 0 || seq_len > (int64_t{1} << 30)) return RLK_ERR_INVALID_ARGUMENT;
   double* parts = reinterpret_cast<double*>(partials);
-  const int64_t nparts = launch_grid<StatsOp>(num_envs, seq_len);
+  const int64_t nparts = call_blocks<StatsOp>(num_envs, seq_len);
   if (parts == nullptr || (reinterpret_cast<uintptr_t>(parts) & 7u) != 0 ||
       partials_bytes < (size_t)partials_triples(nparts) * kStatWords * sizeof(double) ||
       nparts > 0x7fffffffLL)

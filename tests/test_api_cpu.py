@@ -135,6 +135,9 @@ def test_entry_points_reject_bad_arguments_without_launching():
     assert p(8192, 300) == 2048 * 24 and p(8193, 300) == (2049 + 2) * 24
     assert p(65536, 128) == (4096 + 2) * 24
     assert p(4096 * 524291, 1) == (8388656 + 4097 + 3) * 24
+    # beyond one launch (2^32 work-items): two launches over 268434944 and 4608 rows of
+    # 64 per workgroup, one partial per workgroup of each
+    assert p(4096 * 65537, 3) == (4194296 + 72 + 2049 + 2) * 24
     assert lib.rlk_gae_normalized(fake, fake, fake, None, None, 0, fake, fake, 4096, 128, 0.99,
                                   0.95, 1e-8, None, 0, fake, need - 8, None) == -2
 
