@@ -384,9 +384,9 @@ struct phased_rows<MaskedGaeStatsOp<TRUNC, E>> : std::false_type {};
 // (hip_runtime_api.h, hipLaunchKernel), and every launch here is one-dimensional with at
 // most 1024 threads per workgroup.  Rows are independent, so a call whose launch would
 // need more than kMaxLaunchBlocks workgroups runs as calls over consecutive row ranges,
-// in row order on the same stream, each within the limit.  It takes ~3.2 billion steps of
-// short rows (~13 GB per float32 array at 3 steps per row), or ~4.2 million long rows of
-// one tile each: sizes MI355X's 288 GB holds.
+// in row order on the same stream, each within the limit.  Short rows reach it from 0.8
+// billion steps (3-step rows, 64 per workgroup: 3.2 GB per float32 array) to 8.6 billion,
+// long rows from ~4.2 million rows of one tile each: sizes MI355X's 288 GB holds.
 // ---------------------------------------------------------------------------------------
 constexpr int64_t kMaxLaunchBlocks = ((int64_t{1} << 32) - 1) / 1024;
 
