@@ -9,6 +9,9 @@ must equal the result for the pattern; the split falls inside a repetition.
   * the normalised GAE, whose statistics partials continue across the two launches: the
     oracle's raw advantages for the pattern normalised with the call's mean (the
     pattern's) and its std (unbiased over all rows, not the pattern's own).
+* Every other op at [4096 * 65537, 3] (split alike), its arrays advanced by whole rows in
+  each launch: [E, T], [E, T, A] (Retrace) and per-row ones (bootstrap, seed), against the
+  float64 oracle on the pattern.
 * Long rows, [4096 * 1025, 2049] in bfloat16 (one 32768-step tile per row, 4198400
   workgroups of 1024 threads, split 4193792 + 4608 rows; T odd, so phased access): the
   episodic prefix sum with seeds, bit-identical in every repetition to the float32
@@ -19,7 +22,7 @@ import numpy as np
 import pytest
 import torch
 
-from _common import assert_close, make_inputs, run_oracle, suite_atol
+from _common import OUTPUTS, assert_close, make_inputs, run_oracle, suite_atol
 
 pytestmark = pytest.mark.gpu
 
@@ -116,3 +119,29 @@ def test_prefix_sum_long_rows_over_two_launches_bf16(device, big_memory):
     for c in range(0, k, 8):
         same = rows[c:c + 8] == want
         assert bool(same.all()), f"repetitions {c}..{c + 7}: {int((~same).sum())} elements differ"
+
+
+@pytest.mark.parametrize("op", ["gae", "gae_masked", "vtrace", "retrace", "lambda_returns",
+                                "discounted_returns", "eligibility_traces", "backward_scan",
+                                "forward_scan"])
+def test_every_op_short_rows_over_two_launches(op, device, big_memory):
+    from test_gpu_graph import _call, _inputs
+    k, T = 65537, 3
+    pat, params = _inputs(op, (P, T), seed=11)
+    exp = run_oracle(op, pat, params)
+    per_rep = sum(np.asarray(v).nbytes for v in pat.values() if v is not None)
+    per_rep += sum(np.asarray(e, np.float32).nbytes for e in exp)
+    big_memory(int(per_rep * k * 1.2 / 2 ** 30) + 4)
+    print(f"[split] {op} [{P * k},{T}]", flush=True)
+    big = {}
+    for name, v in pat.items():
+        t = None if v is None else torch.as_tensor(v).to(device)
+        big[name] = None if t is None else t.repeat(k, *([1] * (t.dim() - 1)))
+    outs = _call(op, big, params)
+    torch.cuda.synchronize()
+    del big
+    base_op = "gae" if op == "gae_masked" else op
+    for name, o, e in zip(OUTPUTS[op], outs, exp):
+        e64 = torch.as_tensor(np.asarray(e, np.float64), device=device)
+        worst = _worst(o, e64, k, 1e-5, suite_atol(base_op, pat, e, T))
+        assert worst <= 0.0, f"{op}:{name}: beyond the tolerance by {worst}"
