@@ -940,7 +940,8 @@ def main(argv=None):
                    "timing": "value: eager public-API calls, HIP events around the timed region; "
                              "the timed steps start at the input set after the warm-up's last "
                              "(the least recently used), so no timed call reads inputs the "
-                             "warm-up left in the 256 MB MALL; host_issue holds the host clock's "
+                             "warm-up left in the 256 MB MALL; each step's arguments are "
+                             "unpacked from the set's tuples; host_issue holds the host clock's "
                              "view of the same loop"},
         "roofline": roofline, "ops": ops, "stream_ceiling": ceiling,
         "independent_ceilings": independent, "configs": configs, "configs_bf16_io": configs_bf16,
