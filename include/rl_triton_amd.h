@@ -171,8 +171,9 @@ int rlk_gae_masked(const float *rewards, const float *values, const float *termi
  * in a fixed order.  Two launches: the scan writes A, the returns and one float64
  * (count, sum, sum of squares) triple per workgroup into `partials` (at least
  * rlk_gae_normalized_partials_bytes(num_envs, seq_len) bytes, 8-byte aligned, no
- * initialisation needed); a second kernel normalises A in place.  `workspace` as for
- * rlk_gae. */
+ * initialisation needed); a second kernel normalises A in place.  Scans of more than 2048
+ * workgroups first sum their triples in a tree of 2048 to one (one more launch per level,
+ * its triples in the same buffer).  `workspace` as for rlk_gae. */
 size_t rlk_gae_normalized_partials_bytes(int64_t num_envs, int64_t seq_len);
 int rlk_gae_normalized(const float *rewards, const float *values, const float *terminateds,
                        const float *truncateds, const float *bootstrap, int boot_mode,
