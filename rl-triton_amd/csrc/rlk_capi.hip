@@ -142,7 +142,7 @@ template <bool TRUNC, class E>
 struct half_width_segments<VtraceOp<TRUNC, E>> : std::integral_constant<int, 2> {};
 
 template <class Op>
-LongShape long_shape(int64_t E, int64_t T) {
+LongShape cu_shape(int64_t E, int64_t T) {
   const int64_t cus = device_cus();
   auto tiles = [&](int64_t tile) { return E * ((T + tile - 1) / tile); };
   if constexpr (wide_long_tiles<Op>::value) {
@@ -158,6 +158,49 @@ LongShape long_shape(int64_t E, int64_t T) {
     if (q == 2 && t8 > cus && t8 <= 2 * cus) return {512, hq};
   }
   return {Op::kLongThreads, q};
+}
+
+inline int64_t tile_steps(LongShape s) { return (int64_t)s.threads * kSeg * s.segments; }
+
+// Rows much shorter than the tiles cu_shape picks.  Its rules size a tile for the CUs and
+// the look-back chain along a row, so a call of many rows of a few thousand steps ran one
+// tile per row that was mostly padding: a 2560-step row in a 32768-step tile, the prefix
+// sum [4096,2560] at 114 us against 22 us for a streaming kernel of its bytes.  Where more
+// than a quarter of a row's tile steps would be padding, the call takes the largest of the
+// op's tiles that pads a row by at most a quarter, or else the one that pads it least
+// (the larger on a tie).  Tiles of one size run at the op's own thread count, 4096-step
+// tiles at 512 threads; an 8192-step tile of a 1024-thread op between one and two tiles
+// per CU takes 512 threads, as in cu_shape.
+template <class Op>
+LongShape long_shape(int64_t E, int64_t T) {
+  const LongShape sh = cu_shape<Op>(E, T);
+  auto padded = [&](int64_t tile) { return (T + tile - 1) / tile * tile; };
+  auto fits = [&](int64_t tile) { return 4 * padded(tile) <= 5 * T; };  // padding <= T / 4
+  if (fits(tile_steps(sh))) return sh;
+  // the op's tiles, largest first: kLongThreads x q for q = kLongMaxSegments .. kMinQ, then
+  // the 4096-step tile of 512 x kMinQ
+  int64_t tiles[8];
+  int n = 0;
+  for (int q = Op::kLongMaxSegments; q >= kMinQ; q /= 2) tiles[n++] = (int64_t)Op::kLongThreads * kSeg * q;
+  if (tiles[n - 1] > kMinTile) tiles[n++] = kMinTile;
+  int64_t best = tiles[0];
+  for (int i = 0; i < n; ++i) {
+    if (fits(tiles[i])) {
+      best = tiles[i];
+      break;
+    }
+    if (padded(tiles[i]) < padded(best)) best = tiles[i];
+  }
+  // smaller tiles that would leave the CUs between one and two tiles each keep cu_shape's
+  const int64_t t = E * ((T + best - 1) / best), cus = device_cus();
+  if (t > cus && t < 2 * cus) return sh;
+  if (best == kMinTile) return {512, kMinQ};
+  const LongShape r{Op::kLongThreads, (int)(best / ((int64_t)Op::kLongThreads * kSeg))};
+  constexpr int hq = half_width_segments<Op>::value;
+  if constexpr (hq != 0) {
+    if (r.segments == 2 && t > cus && t <= 2 * cus) return {512, hq};
+  }
+  return r;
 }
 
 // Workgroups of the launch that launch() makes for Op at [E, T] (E, T > 0).
@@ -283,6 +326,9 @@ hipError_t launch_long(const Op& op, int64_t E, int T, uint64_t* ws, hipStream_t
   constexpr int hq = half_width_segments<Op>::value;
   if constexpr (hq != 0) {
     if (sh.threads == 512 && sh.segments == hq) return launch_chain<Op, hq, VEC, SP, 512>(op, E, T, ws, stream, phase0);
+  }
+  if constexpr (Op::kLongThreads == 1024 && hq != kMinQ) {
+    if (sh.threads == 512 && sh.segments == kMinQ) return launch_chain<Op, kMinQ, VEC, SP, 512>(op, E, T, ws, stream, phase0);
   }
   const int q = sh.segments;
   if constexpr (Op::kLongMaxSegments >= 8)

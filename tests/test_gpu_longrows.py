@@ -250,6 +250,29 @@ def test_tiles_between_one_and_two_per_cu(op, shape, device):
         assert torch.equal(g.view(torch.int16), r.to(torch.bfloat16).view(torch.int16))
 
 
+@pytest.mark.parametrize("op", OPS)
+@pytest.mark.parametrize("shape", [(512, 2500), (1000, 2101), (256, 5000), (300, 10001),
+                                   (64, 12000), (4096, 2561)], ids=lambda s: f"{s[0]}x{s[1]}")
+def test_rows_much_shorter_than_the_cu_tile(op, shape, device):
+    """Many rows of a few thousand steps, where the tile that gives every CU one would be
+    mostly padding: the launcher takes smaller tiles (4096 steps at 512 threads, or the
+    op's 8192-step ones), one to three per row with a ragged last tile, aligned and
+    element-aligned rows; against the oracle, and bfloat16 bit-identical to the float32
+    result rounded."""
+    import torch
+    from rl_triton import _native
+    print(f"[short-long rows] {op} {shape}", flush=True)
+    _check(op, *shape, seed=67, device=device)
+    assert not _native.workspace_error(device)
+    inp, params = _inputs(op, *shape, 67)
+    rounded = {k: (v if v is None or k == "actions" else
+                   torch.as_tensor(v).to(torch.bfloat16).float().numpy()) for k, v in inp.items()}
+    got_b = run_api(op, rounded, params, device, dtype=torch.bfloat16)
+    ref = run_api(op, rounded, params, device, dtype=torch.float32)
+    for g, r in zip(got_b, ref):
+        assert torch.equal(g.view(torch.int16), r.to(torch.bfloat16).view(torch.int16))
+
+
 @pytest.mark.parametrize("boot", ["none", "full"])
 @pytest.mark.parametrize("shape", [(64, 65536), (300, 16385), (256, 16383), (1024, 1 << 16),
                                    (3, 500000), (8, 200001)],

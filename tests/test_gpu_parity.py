@@ -637,7 +637,7 @@ def _check_normalized(inp, params, device, what, long_rows=False):
 @pytest.mark.parametrize("boot", ["none", "row", "full"])
 @pytest.mark.parametrize("trunc", [0.0, 0.05])
 @pytest.mark.parametrize("shape", [(2, 3), (4, 128), (33, 257), (16, 2048), (3, 5000), (2, 40000),
-                                   (64, 40000)],
+                                   (64, 40000), (512, 2500)],
                          ids=lambda s: f"{s[0]}x{s[1]}")
 def test_gae_normalized_parity(boot, trunc, shape, device):
     if boot == "row" and trunc > 0:
