@@ -252,13 +252,15 @@ def test_tiles_between_one_and_two_per_cu(op, shape, device):
 
 @pytest.mark.parametrize("op", OPS)
 @pytest.mark.parametrize("shape", [(512, 2500), (1000, 2101), (256, 5000), (300, 10001),
-                                   (64, 12000), (4096, 2561)], ids=lambda s: f"{s[0]}x{s[1]}")
+                                   (64, 12000), (4096, 2561), (16, 40000), (24, 20001)],
+                         ids=lambda s: f"{s[0]}x{s[1]}")
 def test_rows_much_shorter_than_the_cu_tile(op, shape, device):
     """Many rows of a few thousand steps, where the tile that gives every CU one would be
     mostly padding: the launcher takes smaller tiles (4096 steps at 512 threads, or the
     op's 8192-step ones), one to three per row with a ragged last tile, aligned and
-    element-aligned rows; against the oracle, and bfloat16 bit-identical to the float32
-    result rounded."""
+    element-aligned rows.  And few rows whose smallest CU-sized tiles leave CUs idle
+    ([16,40000], [24,20001]): 4096-step tiles, five to ten per row.  Against the oracle,
+    and bfloat16 bit-identical to the float32 result rounded."""
     import torch
     from rl_triton import _native
     print(f"[short-long rows] {op} {shape}", flush=True)
