@@ -150,7 +150,19 @@ LongShape cu_shape(int64_t E, int64_t T) {
     const int64_t t8 = tiles(1024 * kSeg * 2);
     if (T >= 8 * 8192 && t8 < cus && 2 * t8 >= cus) return {1024, 2};
   }
-  const int q = long_segments<Op>(E, T);
+  int q = long_segments<Op>(E, T);
+  // More tiles than CUs at that size, fewer at twice the size: the larger tiles, in one
+  // round with some CUs idle, beat the smaller ones in two.  Measured on MI355X (the
+  // larger tiles' share of the CUs 0.53-0.88, A/B in one process): GAE [150,10000]
+  // 13.7 -> 10.3 us, [64,40000] 16.1 -> 14.2, TD(lambda) [160,10000] 10.1 -> 7.6, prefix
+  // sum [48,131072] 18.6 -> 14.9, [40,100000] 14.6 -> 12.5.  Calls whose tiles already fit
+  // one round keep them ([128,12000], [16,131072]: twice the tile lost 6-25%).
+  if (q < Op::kLongMaxSegments) {
+    const int64_t tile = (int64_t)Op::kLongThreads * kSeg * q;
+    if (tiles(tile) > cus && tiles(2 * tile) < cus) q *= 2;
+  }
+  // (Below, q == 2 with more 8192-step tiles than CUs is left only to ops whose largest
+  // tile that is: V-trace.)
   constexpr int hq = half_width_segments<Op>::value;
   if constexpr (hq != 0) {
     static_assert(Op::kLongThreads == 1024, "a 1024 x 2 call becomes 512 x hq");
@@ -200,9 +212,11 @@ LongShape long_shape(int64_t E, int64_t T) {
     }
     if (padded(tiles[i]) < padded(best)) best = tiles[i];
   }
-  // smaller tiles that would leave the CUs between one and two tiles each keep cu_shape's
-  const int64_t t = E * ((T + best - 1) / best), cus = device_cus();
-  if (t > cus && t < 2 * cus) return sh;
+  // a call whose tiles fit the CUs in one round keeps them rather than take smaller tiles
+  // in more than one
+  const int64_t cus = device_cus(), t = E * ((T + best - 1) / best);
+  const int64_t t_sh = E * ((T + tile_steps(sh) - 1) / tile_steps(sh));
+  if (t_sh <= cus && t > cus) return sh;
   if (best == kMinTile) return {512, kMinQ};
   const LongShape r{Op::kLongThreads, (int)(best / ((int64_t)Op::kLongThreads * kSeg))};
   constexpr int hq = half_width_segments<Op>::value;

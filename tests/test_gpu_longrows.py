@@ -232,11 +232,12 @@ def test_lookback_fallback_paths_give_the_same_bits(op, shape, dtype, device):
                                    (171, 24576), (256, 8192)], ids=lambda s: f"{s[0]}x{s[1]}")
 def test_tiles_between_one_and_two_per_cu(op, shape, device):
     """Calls whose 8192-step tiles outnumber the compute units but not twice over: the
-    1024-thread ops take 512 x 4 tiles so that two workgroups fit a CU (V-trace 512 x 2);
-    aligned and element-aligned rows, with truncations where the op has them, and bfloat16
-    bit-identical to the float32 result rounded.  On a 256-CU MI355X, 257 and 512 tiles
-    ([257,8192], [256,16384]) are the rule's edges and 513 and 256 ([171,24576],
-    [256,8192]) fall just outside it."""
+    ops whose tiles can double take 16384-step tiles, fewer than the CUs, in one round;
+    V-trace, whose largest tile is 8192 steps, takes 512 x 2 so that two workgroups fit a
+    CU.  Aligned and element-aligned rows, with truncations where the op has them, and
+    bfloat16 bit-identical to the float32 result rounded.  On a 256-CU MI355X, 257 and 512
+    tiles ([257,8192], [256,16384]) are the rules' edges and 513 and 256 ([171,24576],
+    [256,8192]) fall just outside them."""
     import torch
     from rl_triton import _native
     _check(op, *shape, seed=61, device=device)
