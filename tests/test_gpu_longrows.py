@@ -139,6 +139,35 @@ def test_row_counts_change_on_a_new_workspace(path, device, monkeypatch):
     assert not _native.workspace_error(device)
 
 
+@pytest.mark.parametrize("path", ["python", "fast"])
+def test_single_tile_rows_between_chained_calls(path, device, monkeypatch):
+    """Calls of one tile per row skip the look-back protocol and leave the workspace as
+    they found it.  On a new stream (a new, zeroed workspace), such calls queued between
+    chained ones, of changing row counts: every chained call must still find its slots'
+    epochs current and its counters at rest.  Every result matches the oracle and no wait
+    gives up."""
+    import torch
+    from rl_triton import _native
+    if path == "fast":
+        monkeypatch.delenv("RL_TRITON_CORRECTNESS_WARNINGS")
+    shapes = [("prefix_sum", 300, 3000), ("prefix_sum", 2, 300000), ("discounted_returns", 1000, 2101),
+              ("discounted_returns", 3, 200001), ("gae", 70, 4000), ("prefix_sum", 70, 9000),
+              ("eligibility_traces", 512, 2500), ("prefix_sum", 1, 600000), ("vtrace", 100, 4096),
+              ("vtrace", 2, 131073)]
+    stream = torch.cuda.Stream(device)
+    pending = []
+    with torch.cuda.stream(stream):
+        for i, (op, E, T) in enumerate(shapes * 2):
+            inp, params = _inputs(op, E, T, seed=700 + i)
+            pending.append((op, E, T, inp, params, run_api(op, inp, params, device)))
+    torch.cuda.synchronize()
+    for op, E, T, inp, params, got in pending:
+        exp = run_oracle(op, inp, params)
+        for name, g, e in zip(OUTPUTS[op], got, exp):
+            assert_close(g.cpu().numpy(), e, 1e-5, _atol(op, inp, e), f"{op}[{E},{T}] in sequence:{name}")
+    assert not _native.workspace_error(device)
+
+
 @pytest.mark.parametrize("op,shape", [("prefix_sum", (1, 1 << 23)), ("vtrace", (1, 1 << 21)),
                                       ("gae_masked", (1, 1 << 20)), ("backward_scan", (1, 3 << 20)),
                                       ("discounted_returns", (2, 1 << 21)),
@@ -189,6 +218,35 @@ def test_lookback_give_up_poisons_with_nan(device):
     assert np.array_equal(per_tile.any(axis=2), per_tile.all(axis=2)), "NaN covers part of a tile"
     assert not per_tile[:, 0].any(), "the row's first tile takes the row carry, never NaN"
     assert_close(g[~nan], exp[~nan], 1e-5, _atol(op, inp, exp), f"{op}[{E},{T}] outside the NaN tiles")
+
+
+@pytest.mark.parametrize("path", ["python", "fast"])
+def test_single_tile_rows_between_chained_calls(path, device, monkeypatch):
+    """Calls of one tile per row skip the look-back protocol and leave the workspace as
+    they found it.  On a new stream (a new, zeroed workspace), such calls queued between
+    chained ones, of changing row counts: every chained call must still find its slots'
+    epochs current and its counters at rest.  Every result matches the oracle and no wait
+    gives up."""
+    import torch
+    from rl_triton import _native
+    if path == "fast":
+        monkeypatch.delenv("RL_TRITON_CORRECTNESS_WARNINGS")
+    shapes = [("prefix_sum", 300, 3000), ("prefix_sum", 2, 300000), ("discounted_returns", 1000, 2101),
+              ("discounted_returns", 3, 200001), ("gae", 70, 4000), ("prefix_sum", 70, 9000),
+              ("eligibility_traces", 512, 2500), ("prefix_sum", 1, 600000), ("vtrace", 100, 4096),
+              ("vtrace", 2, 131073)]
+    stream = torch.cuda.Stream(device)
+    pending = []
+    with torch.cuda.stream(stream):
+        for i, (op, E, T) in enumerate(shapes * 2):
+            inp, params = _inputs(op, E, T, seed=700 + i)
+            pending.append((op, E, T, inp, params, run_api(op, inp, params, device)))
+    torch.cuda.synchronize()
+    for op, E, T, inp, params, got in pending:
+        exp = run_oracle(op, inp, params)
+        for name, g, e in zip(OUTPUTS[op], got, exp):
+            assert_close(g.cpu().numpy(), e, 1e-5, _atol(op, inp, e), f"{op}[{E},{T}] in sequence:{name}")
+    assert not _native.workspace_error(device)
 
 
 @pytest.mark.parametrize("op,shape", [("prefix_sum", (1, 1 << 23)), ("vtrace", (1, 1 << 21)),
