@@ -174,15 +174,20 @@ LongShape cu_shape(int64_t E, int64_t T) {
 
 inline int64_t tile_steps(LongShape s) { return (int64_t)s.threads * kSeg * s.segments; }
 
-// Rows much shorter than the tiles cu_shape picks.  Its rules size a tile for the CUs and
-// the look-back chain along a row, so a call of many rows of a few thousand steps ran one
-// tile per row that was mostly padding: a 2560-step row in a 32768-step tile, the prefix
-// sum [4096,2560] at 114 us against 22 us for a streaming kernel of its bytes.  Where more
-// than a quarter of a row's tile steps would be padding, the call takes the largest of the
-// op's tiles that pads a row by at most a quarter, or else the one that pads it least
-// (the larger on a tie).  Tiles of one size run at the op's own thread count, 4096-step
-// tiles at 512 threads; an 8192-step tile of a 1024-thread op between one and two tiles
-// per CU takes 512 threads, as in cu_shape.
+// The long-row tile shape of a call: cu_shape's, then two corrections.
+//   * Calls that leave CUs idle even at the op's own smallest tile take 4096-step tiles
+//     while those fit one round (below).
+//   * Rows much shorter than the tiles.  cu_shape sizes a tile for the CUs and the
+//     look-back chain along a row, so a call of many rows of a few thousand steps ran one
+//     tile per row that was mostly padding: a 2560-step row in a 32768-step tile, the
+//     prefix sum [4096,2560] at 114 us against 22 us for a streaming kernel of its bytes.
+//     Where more than a quarter of a row's tile steps would be padding, the call takes the
+//     largest of the op's tiles that pads a row by at most a quarter, or else the one that
+//     pads it least (the larger on a tie), unless its tiles fit the CUs in one round and
+//     the smaller ones would not.
+// Tiles of one size run at the op's own thread count, 4096-step tiles at 512 threads; an
+// 8192-step tile of a 1024-thread op between one and two tiles per CU takes 512 threads,
+// as in cu_shape.
 template <class Op>
 LongShape long_shape(int64_t E, int64_t T) {
   LongShape sh = cu_shape<Op>(E, T);
