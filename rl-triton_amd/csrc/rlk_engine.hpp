@@ -1344,9 +1344,12 @@ __global__ __launch_bounds__(NT) void chain_kernel(const Op op, int64_t E, int T
   uint64_t e_raw = 0, drawn = 0;
   // A call of one tile per row has no tile that waits on another: it skips the protocol
   // (the epoch, the count, the status words), and leaves the workspace as it found it, so
-  // every slot's epoch is still the next call's (1.5-4% faster on such calls, MI355X:
-  // TD(lambda) [4096,2560] 31.5 -> 30.2 us, discounted returns [150,10000] 6.65 -> 6.20).
-  const bool chained = tiles_per_row > 1;
+  // every slot's epoch is still the next call's (1.5-5% faster on such calls, MI355X:
+  // TD(lambda) [4096,2560] 31.5 -> 30.1 us, discounted returns [150,10000] 6.56 -> 6.23).
+  // Not in the 32768-step instances or the statistics ops, which sit at the VGPR limit:
+  // there the check spilled 12 B per lane (prefix sum [8,2^20-1], phased, 19.6 -> 20.1 us).
+  constexpr bool kSolo = NT * Q < 8192 && !Op::kBlockStats;
+  const bool chained = !kSolo || tiles_per_row > 1;
   if (tid == 0 && chained) e_raw = atomic_ld(sc + 24);
   auto count_drawn = [&]() {
     const uint64_t one = 1 + (e_raw >> 32);
