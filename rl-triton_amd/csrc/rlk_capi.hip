@@ -116,7 +116,9 @@ int rows_seg(int64_t T) { return T < 4 ? 1 : 4; }
 //     16.16 -> 14.41 us; prefix sum [64,40000] 11.18 -> 8.93 us.  V-trace's registers allow
 //     one 512 x 4 workgroup per CU, so it takes 512 x 2 (4096-step tiles, two workgroups
 //     per CU): [64,40000] 18.6 -> 16.4 us, [200,10000] 17.2 -> 15.4 us, bfloat16
-//     [96,30000] 15.7 -> 15.0 us, float32 [96,30000] 19.4 -> 19.7 us.
+//     [96,30000] 15.7 -> 15.0 us, float32 [96,30000] 19.4 -> 19.7 us.  (Ops whose tile can
+//     double take twice the tile first in these calls, one round of 16384-step tiles,
+//     faster still (cu_shape); only V-trace still takes this rule.)
 struct LongShape {
   int threads, segments;
 };
