@@ -538,10 +538,26 @@ __device__ __forceinline__ void replay(const M (&steps)[S], typename M::State x_
 }
 
 // ---------------------------------------------------------------------------------------
+// Cross-lane moves by DPP (gfx9 data-parallel primitives): a VALU modifier, no trip through
+// the LDS crossbar.  update_dpp(old, src): a lane whose source lane is invalid, or whose
+// row is masked off, keeps `old`.
+// ---------------------------------------------------------------------------------------
+constexpr int kDppRowShr = 0x110;     // + n: lane i <- lane i-n within its row of 16
+constexpr int kDppWaveShr1 = 0x138;   // lane i <- lane i-1 across the wave
+constexpr int kDppRowBcast15 = 0x142; // lane 15 of each row -> the next row
+constexpr int kDppRowBcast31 = 0x143; // lane 31 -> rows 2 and 3
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp(float src, float old) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(src), CTRL,
+                                                    ROW_MASK, 0xf, false));
+}
+
+// ---------------------------------------------------------------------------------------
 // Per-workgroup output statistics (ops with kBlockStats): float64 count, sum and sum of
-// squares of the outputs the op counts (op.stats()), reduced in a fixed order (lanes by a
-// fixed butterfly, waves in index order), so the partial a workgroup writes is the same bit
-// pattern on every run.  kStatWords doubles per workgroup.
+// squares of the outputs the op counts (op.stats()), reduced in a fixed order (lanes by
+// wave_total's DPP steps, waves in index order), so the partial a workgroup writes is the
+// same bit pattern on every run.  kStatWords doubles per workgroup.
 // ---------------------------------------------------------------------------------------
 constexpr int kStatWords = 3;
 
@@ -555,20 +571,41 @@ struct Stats {
   }
 };
 
+// A double moved by a DPP control (both halves alike); lanes without a source get 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_or_zero(double v) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, ROW_MASK, 0xf, false);
+  const uint32_t hi =
+      (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROW_MASK, 0xf, false);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// The wave's sum of v, in lane 63 (other lanes hold partial sums): prefixes within each row
+// of 16 lanes (row_shr 1, 2, 4, 8), then rows 0+1 and 2+3 (row_bcast 15), then all four
+// (row_bcast 31).  A fixed order, and all of it in VALU: a butterfly of ds_bpermute round
+// trips through the LDS crossbar costs one LDS latency per level.
+__device__ __forceinline__ double wave_total(double v) {
+  v += dpp_or_zero<kDppRowShr + 1, 0xf>(v);
+  v += dpp_or_zero<kDppRowShr + 2, 0xf>(v);
+  v += dpp_or_zero<kDppRowShr + 4, 0xf>(v);
+  v += dpp_or_zero<kDppRowShr + 8, 0xf>(v);
+  v += dpp_or_zero<kDppRowBcast15, 0xa>(v);
+  v += dpp_or_zero<kDppRowBcast31, 0xc>(v);
+  return v;
+}
+
 // Every thread of the workgroup calls this once; thread 0 writes
 // partials[kStatWords*blockIdx.x + {0,1,2}] = {n, sum, sum of squares}.
 template <int NT>
 __device__ __forceinline__ void block_stats(Stats st, double* __restrict__ partials) {
   constexpr int NW = NT / kWave;
   __shared__ double s_st[kStatWords][NW];
-#pragma unroll
-  for (int off = kWave / 2; off >= 1; off >>= 1) {
-    st.n += __shfl_xor(st.n, off, kWave);
-    st.sum += __shfl_xor(st.sum, off, kWave);
-    st.sq += __shfl_xor(st.sq, off, kWave);
-  }
+  st.n = wave_total(st.n);
+  st.sum = wave_total(st.sum);
+  st.sq = wave_total(st.sq);
   const int wave = threadIdx.x / kWave;
-  if (__lane_id() == 0) {
+  if (__lane_id() == kWave - 1) {
     s_st[0][wave] = st.n;
     s_st[1][wave] = st.sum;
     s_st[2][wave] = st.sq;
@@ -613,8 +650,8 @@ __global__ __launch_bounds__(NT) void reduce_partials_kernel(const double* __res
 }
 
 // Second launch of the normalisation: every workgroup combines the per-workgroup partials
-// of the first launch in one fixed order (thread i sums partials i, i+NT, ...; a fixed lane
-// butterfly; the waves in index order), so all agree on the statistics, then rewrites its
+// of the first launch in one fixed order (thread i sums partials i, i+NT, ...; the lanes by
+// wave_total; the waves in index order), so all agree on the statistics, then rewrites its
 // share of the n_all elements of x as (x - mean) / (std + eps): mean and std (unbiased,
 // count - 1, as torch computes x.std()) over the elements the first launch counted, which
 // are all of them, or the kept steps of a masked call.
@@ -657,11 +694,8 @@ __global__ __launch_bounds__(NT) void normalize_kernel(E* __restrict__ x,
     for (int k = 0; k < kStatWords; ++k) acc[k] += partials[kStatWords * i + k];
   }
 #pragma unroll
-  for (int off = kWave / 2; off >= 1; off >>= 1) {
-#pragma unroll
-    for (int k = 0; k < kStatWords; ++k) acc[k] += __shfl_xor(acc[k], off, kWave);
-  }
-  if (__lane_id() == 0) {
+  for (int k = 0; k < kStatWords; ++k) acc[k] = wave_total(acc[k]);
+  if (__lane_id() == kWave - 1) {
 #pragma unroll
     for (int k = 0; k < kStatWords; ++k) s_st[k][tid / kWave] = acc[k];
   }
@@ -691,22 +725,6 @@ __global__ __launch_bounds__(NT) void normalize_kernel(E* __restrict__ x,
     for (int64_t i = first; i < units; i += stride)
       store_one_nt(x + i, ((i == first ? v0.x : load_one_nt(x + i)) - m) / d);
   }
-}
-
-// ---------------------------------------------------------------------------------------
-// Cross-lane moves by DPP (gfx9 data-parallel primitives): a VALU modifier, no trip through
-// the LDS crossbar.  update_dpp(old, src): a lane whose source lane is invalid, or whose
-// row is masked off, keeps `old`.
-// ---------------------------------------------------------------------------------------
-constexpr int kDppRowShr = 0x110;     // + n: lane i <- lane i-n within its row of 16
-constexpr int kDppWaveShr1 = 0x138;   // lane i <- lane i-1 across the wave
-constexpr int kDppRowBcast15 = 0x142; // lane 15 of each row -> the next row
-constexpr int kDppRowBcast31 = 0x143; // lane 31 -> rows 2 and 3
-
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp(float src, float old) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(src), CTRL,
-                                                    ROW_MASK, 0xf, false));
 }
 
 // The previous lane's value (lane 0 keeps its own).
