@@ -671,3 +671,55 @@ def test_gae_normalized_single_element_is_nan_like_torch(device):
     ref = rl_triton.compute_gae(x, x, torch.zeros_like(x))
     assert torch.isnan(adv).all() and torch.isnan((ref - ref.mean()) / (ref.std() + 1e-8)).all()
     torch.testing.assert_close(ret, ref + x)
+
+
+def _normalized_cases(n=40, seed=91):
+    """Seeded compute_gae_normalized calls, masked and not: rows of 1 to 200000 steps (short,
+    multi-wave and look-back paths; up to 9000 rows, so from one scan workgroup to several
+    thousand partials), each bootstrap mode, with and without truncation."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        band = int(rng.integers(0, 3))
+        T = int([rng.integers(1, 129), rng.integers(129, 2049),
+                 math.exp(rng.uniform(math.log(2049), math.log(200000)))][band])
+        E = int(max(1, min(rng.integers(1, 9000), 1_500_000 // T)))
+        boot = str(rng.choice(["none", "row", "full"]))
+        trunc = 0.0 if boot == "row" else float(rng.choice([0.0, 0.03]))
+        cases.append((("gae_normalized", "gae_normalized_masked")[i % 2], E, T, boot, trunc, 9100 + i))
+    return cases
+
+
+@pytest.mark.parametrize("case", _normalized_cases(), ids=lambda c: f"{c[0]}-{c[1]}x{c[2]}-{c[3]}-{c[4]}")
+def test_gae_normalized_random_shapes(case, device):
+    """Seeded shapes against the float64 composition (statistics over the kept steps when
+    masked).  Every third case also runs in bfloat16: the returns are the float32 result
+    rounded, bit for bit; the advantages, normalised from the rounded raw advantages, agree
+    with the float32 path's to bfloat16 precision."""
+    op, E, T, boot, trunc, seed = case
+    inp, params = make_inputs(op, E, T, seed=seed, p_trunc=trunc, boot=boot)
+    params = dict(params, eps=1e-8)
+    what = f"{op}[{E},{T}] boot={boot} trunc={trunc}"
+    print(f"[normalized-random] {what}", flush=True)
+    adv, ret = run_api(op, inp, params, device)
+    adv_exp, ret_exp = run_oracle(op, inp, params)
+    raw_op = "gae_masked" if op == "gae_normalized_masked" else "gae"
+    raw = run_oracle(raw_op, inp, {k: v for k, v in params.items() if k != "eps"})[0]
+    kept = raw if op == "gae_normalized" else raw[np.asarray(inp["mask"]) != 0]
+    base = _long_atol("gae", inp, raw)
+    scale = max(1.0, float(np.max(np.abs(ret_exp))))
+    assert_close(ret.cpu().numpy(), ret_exp, 1e-5, base + 1e-6 * scale, f"{what}:returns")
+    if kept.size >= 2:
+        std = float(np.std(kept, ddof=1))
+        assert_close(adv.cpu().numpy(), adv_exp, 1e-5, base / min(std, 1.0) + 1e-6,
+                     f"{what}:advantages")
+    if seed % 3 == 0:
+        bf = torch.bfloat16
+        rounded = {k: (v if v is None else torch.as_tensor(v).to(bf).float().numpy())
+                   for k, v in inp.items()}
+        ab, rb = run_api(op, rounded, params, device, dtype=bf)
+        af, rf = run_api(op, rounded, params, device, dtype=torch.float32)
+        assert torch.equal(rb.view(torch.int16), rf.to(bf).view(torch.int16)), f"{what}: bf16 returns"
+        if kept.size >= 2:
+            torch.testing.assert_close(ab.float(), af, rtol=2.0 ** -7, atol=2.0 ** -7 * math.sqrt(2),
+                                       msg=f"{what}: bf16 advantages")
